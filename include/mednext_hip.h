@@ -1,0 +1,124 @@
+/*
+ * mednext_hip.h — C ABI of libmednext_hip.so, the gfx950 (MI355X) kernels behind
+ * the MedNeXt operator path.
+ *
+ * Conventions (shared by every entry point):
+ *   - Pointers are device pointers allocated by the caller (PyTorch's caching
+ *     allocator in the Python host). The library never allocates: entry points
+ *     that need scratch memory expose a *_workspace_bytes() query and take a
+ *     caller-owned workspace.
+ *   - Tensors are contiguous NCDHW (pointwise: [N, C, V] with V = D*H*W).
+ *   - `stream` is a hipStream_t (the caller's current stream); launches are
+ *     asynchronous and never synchronise.
+ *   - Return value is a mednext_status; on failure mednext_hip_last_error()
+ *     returns a message for the calling thread.
+ *   - Reductions (weight/bias/norm gradients) are deterministic: fixed-order
+ *     two-pass fp32/fp64 reductions, no floating-point atomics.
+ */
+#ifndef MEDNEXT_HIP_H
+#define MEDNEXT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum mednext_status {
+  MEDNEXT_STATUS_OK = 0,
+  MEDNEXT_STATUS_INVALID_ARGUMENT = 1,
+  MEDNEXT_STATUS_LAUNCH_ERROR = 2,
+  MEDNEXT_STATUS_UNSUPPORTED = 3
+};
+
+enum mednext_dtype {
+  MEDNEXT_DTYPE_F32 = 0,
+  MEDNEXT_DTYPE_F64 = 1,
+  MEDNEXT_DTYPE_F16 = 2,
+  MEDNEXT_DTYPE_BF16 = 3
+};
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* mednext_hip_last_error(void);
+
+/* ABI revision of this header; bumped on any signature change. */
+int32_t mednext_hip_abi_version(void);
+
+/* ------------------------------------------------------------------ depthwise
+ * Depthwise Conv3d, stride 1, odd cubic kernel k in {1,3,5}, zero "same"
+ * padding k/2, groups == C. weight is [C,1,k,k,k] and bias [C], both in the
+ * same dtype as x (the reference casts them to x.dtype before its op).
+ * tile_w (4, 8, 16, 32 or 64 output columns per workgroup) and depth_chunk
+ * (output planes per workgroup, >= 1) are the launch recipe chosen by the
+ * gfx950 tile policy.
+ */
+
+/* y = conv3d(x, weight, bias, padding=k//2, groups=C).
+ * Replaces the forward of mednext_accel::depthwise_conv3d_odd_regular
+ * (reference src/mednext_accel/ops/_triton/depthwise.py:549-563, which calls
+ * F.conv3d). bias may be NULL. */
+int32_t mednext_depthwise3d_fwd(const void* x, const void* weight, const void* bias, void* y,
+                                int64_t n, int64_t c, int64_t d, int64_t h, int64_t w,
+                                int32_t kernel_size, int32_t dtype, int32_t tile_w,
+                                int32_t depth_chunk, void* stream);
+
+/* grad_input = conv3d(grad_output, flip(weight), padding=k//2, groups=C).
+ * Replaces mednext_accel::depthwise_input_grad_odd_regular
+ * (reference ops/_triton/depthwise.py:159-203 kernel, :486-513 op). */
+int32_t mednext_depthwise3d_dgrad(const void* grad_output, const void* weight, void* grad_input,
+                                  int64_t n, int64_t c, int64_t d, int64_t h, int64_t w,
+                                  int32_t kernel_size, int32_t dtype, int32_t tile_w,
+                                  int32_t depth_chunk, void* stream);
+
+/* Bytes of fp32 (fp64 for MEDNEXT_DTYPE_F64) partials the wgrad launch needs. */
+size_t mednext_depthwise3d_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t d, int64_t h,
+                                                 int64_t w, int32_t kernel_size, int32_t dtype,
+                                                 int32_t tile_w, int32_t depth_chunk);
+
+/* grad_weight[c,t] = sum x[n,c,pos+t-p] * grad_output[n,c,pos] (dtype of x) and,
+ * when grad_bias != NULL, grad_bias[c] = sum grad_output[n,c,:] — fused in the
+ * same pass. Replaces mednext_accel::depthwise_weight_grad_odd_regular
+ * (reference ops/_triton/depthwise.py:13-83 kernels, :445-483 op) plus the
+ * native bias gradient the reference requests from aten.convolution_backward
+ * (:612-633). */
+int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_output, void* grad_weight,
+                                  void* grad_bias, void* workspace, size_t workspace_bytes,
+                                  int64_t n, int64_t c, int64_t d, int64_t h, int64_t w,
+                                  int32_t kernel_size, int32_t dtype, int32_t tile_w,
+                                  int32_t depth_chunk, void* stream);
+
+/* ---------------------------------------------------------------- group norm
+ * GroupNorm with groups == channels on [N, C, V] (V = spatial volume), biased
+ * variance, rstd = 1/sqrt(var + eps). Replaces the reference's
+ * nn.GroupNorm(in_channels, in_channels) inside MedNeXtBlock (reference
+ * src/mednext_accel/models/blocks.py:74, :84), which has no custom op in the
+ * reference. x and y dtypes are independent so a bf16 input can produce the
+ * fp32 output autocast gives the reference (pairs: f64/f64, f32/f32, bf16/f32,
+ * bf16/bf16, f16/f32, f16/f16). gamma/beta (nullable) are [C] in param_dtype.
+ * mean/rstd are [N*C] fp32 (fp64 when x is fp64). `splits` chunks each (n, c)
+ * row across workgroups (1..4096).
+ */
+size_t mednext_group_norm_workspace_bytes(int64_t n, int64_t c, int64_t spatial, int32_t splits);
+
+int32_t mednext_group_norm_fwd(const void* x, int32_t x_dtype, const void* gamma, const void* beta,
+                               int32_t param_dtype, void* y, int32_t y_dtype, void* mean,
+                               void* rstd, int64_t n, int64_t c, int64_t spatial, double eps,
+                               int32_t splits, void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/* grad_input (dtype of x, nullable), grad_gamma / grad_beta ([C], param_dtype,
+ * nullable) from grad_output (pairs dy/x: f64/f64, f32/f32, f32/bf16, bf16/bf16,
+ * f32/f16, f16/f16) and the saved mean/rstd. */
+int32_t mednext_group_norm_bwd(const void* grad_output, int32_t dy_dtype, const void* x,
+                               int32_t x_dtype, const void* mean, const void* rstd,
+                               const void* gamma, int32_t param_dtype, void* grad_input,
+                               void* grad_gamma, void* grad_beta, int64_t n, int64_t c,
+                               int64_t spatial, int32_t splits, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEDNEXT_HIP_H */

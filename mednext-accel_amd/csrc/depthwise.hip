@@ -1,0 +1,597 @@
+// Depthwise Conv3d (stride 1, odd cubic kernel, zero "same" padding) for gfx950:
+// forward, input gradient (same stencil with flipped taps) and weight gradient
+// with the bias gradient fused in the same pass.
+//
+// Work decomposition (all three kernels): one workgroup owns one (n, c) slab, a
+// run of `depth_chunk` output planes and one TH x TW tile of each plane. Input
+// planes stream along D through an LDS halo tile of (TH + 2p) x (TW + 8)
+// elements (converted to the accumulation type on the way in). Each thread
+// owns a kRH x 4 patch of outputs. Along D the forward/dgrad kernels scatter:
+// every input plane is read from LDS once and added into k rotating
+// per-output-plane register accumulators, so an output plane is complete (and
+// written) k-1 input planes after its first contribution. The weight-gradient
+// kernel keeps a k-plane ring of grad_output values in registers instead and
+// accumulates k^3 tap sums per thread, reduced per workgroup into a fp32/fp64
+// partial and then summed over workgroups in a fixed order (deterministic).
+#include "common.h"
+
+#include <type_traits>
+
+namespace mednext {
+namespace {
+
+constexpr int kMaxThreads = 256;
+constexpr int kRH = 2;  // output rows per thread
+
+struct DwGeom {
+  int C, D, H, W;
+  int TD;   // output planes per workgroup
+  int TWt;  // threads along w; tile width TW = 4 * TWt
+  int THt;  // threads along h holding outputs; tile height TH = kRH * THt
+  int nDc, nHt, nWt;
+};
+
+struct TileIdx {
+  int64_t nc;
+  int c, n, d0, th0, tw0, dc, ht, wt;
+};
+
+__device__ inline TileIdx tile_of_block(const DwGeom& g) {
+  TileIdx t;
+  int64_t bid = blockIdx.x;
+  t.wt = static_cast<int>(bid % g.nWt);
+  bid /= g.nWt;
+  t.ht = static_cast<int>(bid % g.nHt);
+  bid /= g.nHt;
+  t.dc = static_cast<int>(bid % g.nDc);
+  bid /= g.nDc;
+  t.nc = bid;
+  t.c = static_cast<int>(bid % g.C);
+  t.n = static_cast<int>(bid / g.C);
+  t.d0 = t.dc * g.TD;
+  t.th0 = t.ht * kRH * g.THt;
+  t.tw0 = t.wt * 4 * g.TWt;
+  return t;
+}
+
+// 16-byte LDS accesses (the row stride is a multiple of 4 elements and the
+// buffer is 16-byte aligned, so every group of 4 starts on a 16-byte boundary).
+__device__ inline void lds_store4(float* dst, const float v[4]) {
+  *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ inline void lds_store4(double* dst, const double v[4]) {
+  reinterpret_cast<double2*>(dst)[0] = make_double2(v[0], v[1]);
+  reinterpret_cast<double2*>(dst)[1] = make_double2(v[2], v[3]);
+}
+__device__ inline void lds_load4(const float* src, float v[4]) {
+  const float4 a = *reinterpret_cast<const float4*>(src);
+  v[0] = a.x;
+  v[1] = a.y;
+  v[2] = a.z;
+  v[3] = a.w;
+}
+__device__ inline void lds_load4(const double* src, double v[4]) {
+  const double2 a = reinterpret_cast<const double2*>(src)[0];
+  const double2 b = reinterpret_cast<const double2*>(src)[1];
+  v[0] = a.x;
+  v[1] = a.y;
+  v[2] = b.x;
+  v[3] = b.y;
+}
+
+// Fill the LDS halo tile with input plane `di` (zeros outside the volume).
+// LDS column j holds w = tw0 - 4 + j; LDS row r holds h = th0 - P + r.
+template <typename T, typename Acc, int P, bool VEC>
+__device__ inline void fill_plane(Acc* __restrict__ lds, const T* __restrict__ src, int di,
+                                  const DwGeom& g, int th0, int tw0, int lrows, int rs) {
+  const int nthreads = blockDim.x;
+  const bool plane_ok = di >= 0 && di < g.D;
+  const T* __restrict__ p = src + static_cast<int64_t>(plane_ok ? di : 0) * g.H * g.W;
+  if constexpr (VEC) {
+    const int groups = rs >> 2;
+    const int total = lrows * groups;
+    for (int e = threadIdx.x; e < total; e += nthreads) {
+      const int rr = e / groups;
+      const int gq = e - rr * groups;
+      const int h = th0 - P + rr;
+      const int w = tw0 - 4 + 4 * gq;
+      Acc v[4] = {Acc(0), Acc(0), Acc(0), Acc(0)};
+      // W % 4 == 0 and w % 4 == 0: a group is entirely inside or outside.
+      if (plane_ok && h >= 0 && h < g.H && w >= 0 && w < g.W) {
+        load4<T, Acc>(p + static_cast<int64_t>(h) * g.W + w, v);
+      }
+      lds_store4(lds + rr * rs + 4 * gq, v);
+    }
+  } else {
+    const int total = lrows * rs;
+    for (int e = threadIdx.x; e < total; e += nthreads) {
+      const int rr = e / rs;
+      const int cc = e - rr * rs;
+      const int h = th0 - P + rr;
+      const int w = tw0 - 4 + cc;
+      Acc v = Acc(0);
+      if (plane_ok && h >= 0 && h < g.H && w >= 0 && w < g.W) {
+        v = Cvt<T, Acc>::load(p[static_cast<int64_t>(h) * g.W + w]);
+      }
+      lds[rr * rs + cc] = v;
+    }
+  }
+}
+
+// Read this thread's (kRH + 2P) x 12 input window from the LDS tile: columns
+// 4*tx .. 4*tx+11 hold w = tw0 + 4*tx - 4 .. tw0 + 4*tx + 7.
+template <typename Acc, int P>
+__device__ inline void read_window(const Acc* __restrict__ lds, int ty, int tx, int rs,
+                                   Acc in[kRH + 2 * P][12]) {
+#pragma unroll
+  for (int j = 0; j < kRH + 2 * P; ++j) {
+    const Acc* row = lds + (ty * kRH + j) * rs + 4 * tx;
+    lds_load4(row, &in[j][0]);
+    lds_load4(row + 4, &in[j][4]);
+    lds_load4(row + 8, &in[j][8]);
+  }
+}
+
+// Per-channel taps, uniform across the workgroup. bf16 taps are fetched as
+// 32-bit words and split with integer shifts so they stay in scalar registers
+// (there is no 16-bit scalar load); the weight buffer must be 4-byte aligned.
+template <typename T, typename Acc, int K3, bool FLIP>
+__device__ inline void load_taps(const T* __restrict__ wt, int c, int channels, Acc wr[K3]) {
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    const uint32_t* __restrict__ words = reinterpret_cast<const uint32_t*>(wt);
+    const int64_t e0 = static_cast<int64_t>(c) * K3;
+    const int64_t total = static_cast<int64_t>(channels) * K3;
+#pragma unroll
+    for (int i = 0; i < K3; ++i) {
+      const int64_t e = e0 + (FLIP ? K3 - 1 - i : i);
+      if (e + 1 == total && (e & 1) == 0) {
+        // Last tap of an odd-length buffer: its 32-bit word would extend past
+        // the end, so read the 16-bit element itself.
+        wr[i] = bf16_to_f32(wt[e].bits);
+      } else {
+        const uint32_t word = words[e >> 1];
+        wr[i] = __uint_as_float((e & 1) ? (word & 0xffff0000u) : (word << 16));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < K3; ++i) {
+      wr[i] = Cvt<T, Acc>::load(wt[static_cast<int64_t>(c) * K3 + (FLIP ? K3 - 1 - i : i)]);
+    }
+  }
+}
+
+template <typename T, typename Acc, int K, bool FLIP, bool VEC, bool BIAS>
+__global__ __launch_bounds__(kMaxThreads) void dw_stencil_kernel(const T* __restrict__ x,
+                                                                 const T* __restrict__ wt,
+                                                                 const T* __restrict__ bias,
+                                                                 T* __restrict__ y, DwGeom g) {
+  constexpr int P = K / 2;
+  constexpr int K3 = K * K * K;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  Acc* lds = reinterpret_cast<Acc*>(smem_raw);
+
+  const TileIdx t = tile_of_block(g);
+  const int rs = 4 * g.TWt + 8;
+  const int lrows = kRH * g.THt + 2 * P;
+  const int tx = threadIdx.x % g.TWt;
+  const int ty = threadIdx.x / g.TWt;
+  const bool owner = ty < g.THt;
+
+  const int64_t plane = static_cast<int64_t>(g.H) * g.W;
+  const T* __restrict__ xnc = x + t.nc * g.D * plane;
+  T* __restrict__ ync = y + t.nc * g.D * plane;
+
+  Acc wr[K3];
+  load_taps<T, Acc, K3, FLIP>(wt, t.c, g.C, wr);
+  Acc b0 = Acc(0);
+  if constexpr (BIAS) b0 = Cvt<T, Acc>::load(bias[t.c]);
+
+  Acc acc[K][kRH][4];
+#pragma unroll
+  for (int s = 0; s < K; ++s)
+#pragma unroll
+    for (int r = 0; r < kRH; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[s][r][v] = Acc(0);
+
+  const int nplanes = g.TD + K - 1;
+  for (int q = 0; q < nplanes; q += K) {
+#pragma unroll
+    for (int s = 0; s < K; ++s) {
+      const int i = q + s;
+      if (i >= nplanes) break;
+      __syncthreads();
+      fill_plane<T, Acc, P, VEC>(lds, xnc, t.d0 - P + i, g, t.th0, t.tw0, lrows, rs);
+      __syncthreads();
+      if (owner) {
+        Acc in[kRH + 2 * P][12];
+        read_window<Acc, P>(lds, ty, tx, rs, in);
+        // Input plane i feeds output plane o = i - kd through tap kd.
+#pragma unroll
+        for (int kd = 0; kd < K; ++kd) {
+          const int slot = ((s - kd) % K + K) % K;
+#pragma unroll
+          for (int kh = 0; kh < K; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < K; ++kw) {
+              const Acc wv = wr[(kd * K + kh) * K + kw];
+#pragma unroll
+              for (int r = 0; r < kRH; ++r)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[slot][r][v] += in[r + kh][4 - P + v + kw] * wv;
+            }
+        }
+      }
+      // Output plane o = i - (K - 1) has now received all K input planes.
+      const int o = i - (K - 1);
+      const int cs = (s + 1) % K;
+      if (owner && o >= 0 && o < g.TD && t.d0 + o < g.D) {
+        T* __restrict__ dst = ync + static_cast<int64_t>(t.d0 + o) * plane;
+#pragma unroll
+        for (int r = 0; r < kRH; ++r) {
+          const int h = t.th0 + ty * kRH + r;
+          const int w = t.tw0 + 4 * tx;
+          if (h >= g.H) continue;
+          Acc out[4];
+#pragma unroll
+          for (int v = 0; v < 4; ++v) out[v] = acc[cs][r][v] + b0;
+          T* rowp = dst + static_cast<int64_t>(h) * g.W + w;
+          if constexpr (VEC) {
+            if (w < g.W) store4<T, Acc>(rowp, out);
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (w + v < g.W) rowp[v] = Cvt<T, Acc>::store(out[v]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kRH; ++r)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[cs][r][v] = Acc(0);
+    }
+  }
+}
+
+template <typename T, typename Acc, int K, bool VEC>
+__global__ __launch_bounds__(kMaxThreads) void dw_wgrad_kernel(const T* __restrict__ x,
+                                                               const T* __restrict__ dy,
+                                                               Acc* __restrict__ partial,
+                                                               DwGeom g, int splits) {
+  constexpr int P = K / 2;
+  constexpr int K3 = K * K * K;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  Acc* lds = reinterpret_cast<Acc*>(smem_raw);
+  __shared__ Acc red[kMaxThreads / 64][K3 + 1];
+
+  const TileIdx t = tile_of_block(g);
+  const int rs = 4 * g.TWt + 8;
+  const int lrows = kRH * g.THt + 2 * P;
+  const int tx = threadIdx.x % g.TWt;
+  const int ty = threadIdx.x / g.TWt;
+  const bool owner = ty < g.THt;
+
+  const int64_t plane = static_cast<int64_t>(g.H) * g.W;
+  const T* __restrict__ xnc = x + t.nc * g.D * plane;
+  const T* __restrict__ dync = dy + t.nc * g.D * plane;
+
+  Acc acc[K3 + 1];
+#pragma unroll
+  for (int i = 0; i < K3 + 1; ++i) acc[i] = Acc(0);
+  Acc dyr[K][kRH][4];
+#pragma unroll
+  for (int s = 0; s < K; ++s)
+#pragma unroll
+    for (int r = 0; r < kRH; ++r)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) dyr[s][r][v] = Acc(0);
+
+  const int h_base = t.th0 + ty * kRH;
+  const int w_base = t.tw0 + 4 * tx;
+  const int nplanes = g.TD + K - 1;
+  for (int q = 0; q < nplanes; q += K) {
+#pragma unroll
+    for (int s = 0; s < K; ++s) {
+      const int i = q + s;
+      if (i >= nplanes) break;
+      // grad_output plane o = i enters the ring at slot i % K == s.
+      {
+        const bool plane_ok = owner && i < g.TD && t.d0 + i < g.D;
+        const T* __restrict__ src = dync + static_cast<int64_t>(plane_ok ? t.d0 + i : 0) * plane;
+#pragma unroll
+        for (int r = 0; r < kRH; ++r) {
+          const int h = h_base + r;
+          Acc v4[4] = {Acc(0), Acc(0), Acc(0), Acc(0)};
+          if (plane_ok && h < g.H) {
+            const T* rowp = src + static_cast<int64_t>(h) * g.W + w_base;
+            if constexpr (VEC) {
+              if (w_base < g.W) load4<T, Acc>(rowp, v4);
+            } else {
+#pragma unroll
+              for (int v = 0; v < 4; ++v)
+                if (w_base + v < g.W) v4[v] = Cvt<T, Acc>::load(rowp[v]);
+            }
+          }
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            dyr[s][r][v] = v4[v];
+            acc[K3] += v4[v];
+          }
+        }
+      }
+      __syncthreads();
+      fill_plane<T, Acc, P, VEC>(lds, xnc, t.d0 - P + i, g, t.th0, t.tw0, lrows, rs);
+      __syncthreads();
+      if (owner) {
+        Acc in[kRH + 2 * P][12];
+        read_window<Acc, P>(lds, ty, tx, rs, in);
+        // Input plane i pairs with grad_output plane o = i - kd through tap kd.
+#pragma unroll
+        for (int kd = 0; kd < K; ++kd) {
+          const int slot = ((s - kd) % K + K) % K;
+#pragma unroll
+          for (int kh = 0; kh < K; ++kh)
+#pragma unroll
+            for (int kw = 0; kw < K; ++kw) {
+              Acc sum = acc[(kd * K + kh) * K + kw];
+#pragma unroll
+              for (int r = 0; r < kRH; ++r)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) sum += in[r + kh][4 - P + v + kw] * dyr[slot][r][v];
+              acc[(kd * K + kh) * K + kw] = sum;
+            }
+        }
+      }
+    }
+  }
+
+  // Workgroup reduction: fixed butterfly inside each wave, then waves in order.
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+#pragma unroll
+  for (int i = 0; i < K3 + 1; ++i) {
+    const Acc v = wave_sum(acc[i]);
+    if (lane == 0) red[wave][i] = v;
+  }
+  __syncthreads();
+  const int64_t split = ((static_cast<int64_t>(t.n) * g.nDc + t.dc) * g.nHt + t.ht) * g.nWt + t.wt;
+  for (int i = threadIdx.x; i < K3 + 1; i += blockDim.x) {
+    Acc v = red[0][i];
+    for (int wv = 1; wv < nwaves; ++wv) v += red[wv][i];
+    partial[(static_cast<int64_t>(t.c) * splits + split) * (K3 + 1) + i] = v;
+  }
+}
+
+template <typename T, typename Acc>
+__global__ void dw_wgrad_finish_kernel(const Acc* __restrict__ partial, T* __restrict__ dw,
+                                       T* __restrict__ db, int splits, int k3) {
+  const int c = blockIdx.x;
+  for (int i = threadIdx.x; i < k3 + 1; i += blockDim.x) {
+    double s = 0.0;
+    const Acc* p = partial + static_cast<int64_t>(c) * splits * (k3 + 1) + i;
+    for (int j = 0; j < splits; ++j) s += static_cast<double>(p[static_cast<int64_t>(j) * (k3 + 1)]);
+    if (i < k3) {
+      dw[static_cast<int64_t>(c) * k3 + i] = Cvt<T, Acc>::store(static_cast<Acc>(s));
+    } else if (db != nullptr) {
+      db[c] = Cvt<T, Acc>::store(static_cast<Acc>(s));
+    }
+  }
+}
+
+// ------------------------------------------------------------------ host side
+
+struct Plan {
+  DwGeom g;
+  int threads;
+  size_t lds_bytes;
+  int64_t blocks;
+  int splits;  // workgroups per channel (wgrad partial count)
+};
+
+int make_plan(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int acc_bytes,
+              int tile_w, int depth_chunk, Plan* out) {
+  MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && d >= 1 && h >= 1 && w >= 1, "shape must be positive");
+  MEDNEXT_CHECK_ARG(c < (int64_t(1) << 31) && d < (int64_t(1) << 31) && h < (int64_t(1) << 31) &&
+                        w < (int64_t(1) << 31),
+                    "each dimension must fit in int32");
+  MEDNEXT_CHECK_ARG(h * w < (int64_t(1) << 40), "plane too large");
+  MEDNEXT_CHECK_ARG(k == 1 || k == 3 || k == 5, "kernel_size must be 1, 3 or 5");
+  MEDNEXT_CHECK_ARG(tile_w == 4 || tile_w == 8 || tile_w == 16 || tile_w == 32 || tile_w == 64,
+                    "tile_w must be 4, 8, 16, 32 or 64");
+  MEDNEXT_CHECK_ARG(depth_chunk >= 1, "depth_chunk must be >= 1");
+  DwGeom g{};
+  g.C = static_cast<int>(c);
+  g.D = static_cast<int>(d);
+  g.H = static_cast<int>(h);
+  g.W = static_cast<int>(w);
+  g.TD = static_cast<int>(depth_chunk < d ? depth_chunk : d);
+  g.TWt = tile_w / 4;
+  int tht = kMaxThreads / g.TWt;
+  const int need = static_cast<int>(cdiv(h, kRH));
+  if (tht > need) tht = need;
+  g.THt = tht;
+  g.nDc = static_cast<int>(cdiv(d, g.TD));
+  g.nHt = static_cast<int>(cdiv(h, kRH * g.THt));
+  g.nWt = static_cast<int>(cdiv(w, 4 * g.TWt));
+  const int used = g.TWt * g.THt;
+  out->threads = static_cast<int>(cdiv(used, 64) * 64);
+  const int p = k / 2;
+  out->lds_bytes = static_cast<size_t>(kRH * g.THt + 2 * p) * (4 * g.TWt + 8) * acc_bytes;
+  MEDNEXT_CHECK_ARG(out->lds_bytes <= 64 * 1024, "tile needs more than 64 KiB of LDS");
+  out->splits = static_cast<int>(n) * g.nDc * g.nHt * g.nWt;
+  out->blocks = n * c * g.nDc * g.nHt * g.nWt;
+  MEDNEXT_CHECK_ARG(out->blocks < (int64_t(1) << 31), "grid too large");
+  out->g = g;
+  return MEDNEXT_STATUS_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <typename T, int K, bool FLIP>
+int launch_stencil_k(const void* x, const void* wt, const void* bias, void* y, const Plan& pl,
+                     bool vec, hipStream_t st) {
+  using Acc = typename AccOf<T>::type;
+  const dim3 grid(static_cast<unsigned>(pl.blocks));
+  const dim3 block(pl.threads);
+  auto px = static_cast<const T*>(x);
+  auto pw = static_cast<const T*>(wt);
+  auto pb = static_cast<const T*>(bias);
+  auto py = static_cast<T*>(y);
+  if (vec) {
+    if (bias)
+      hipLaunchKernelGGL((dw_stencil_kernel<T, Acc, K, FLIP, true, true>), grid, block,
+                         pl.lds_bytes, st, px, pw, pb, py, pl.g);
+    else
+      hipLaunchKernelGGL((dw_stencil_kernel<T, Acc, K, FLIP, true, false>), grid, block,
+                         pl.lds_bytes, st, px, pw, pb, py, pl.g);
+  } else {
+    if (bias)
+      hipLaunchKernelGGL((dw_stencil_kernel<T, Acc, K, FLIP, false, true>), grid, block,
+                         pl.lds_bytes, st, px, pw, pb, py, pl.g);
+    else
+      hipLaunchKernelGGL((dw_stencil_kernel<T, Acc, K, FLIP, false, false>), grid, block,
+                         pl.lds_bytes, st, px, pw, pb, py, pl.g);
+  }
+  MEDNEXT_CHECK_LAUNCH();
+  return MEDNEXT_STATUS_OK;
+}
+
+template <typename T, bool FLIP>
+int launch_stencil(const void* x, const void* wt, const void* bias, void* y, const Plan& pl,
+                   int k, bool vec, hipStream_t st) {
+  switch (k) {
+    case 1: return launch_stencil_k<T, 1, FLIP>(x, wt, bias, y, pl, vec, st);
+    case 3: return launch_stencil_k<T, 3, FLIP>(x, wt, bias, y, pl, vec, st);
+    default: return launch_stencil_k<T, 5, FLIP>(x, wt, bias, y, pl, vec, st);
+  }
+}
+
+int acc_bytes_of(int dtype) { return dtype == MEDNEXT_DTYPE_F64 ? 8 : 4; }
+
+bool dtype_ok(int dtype) {
+  return dtype == MEDNEXT_DTYPE_F32 || dtype == MEDNEXT_DTYPE_F64 || dtype == MEDNEXT_DTYPE_F16 ||
+         dtype == MEDNEXT_DTYPE_BF16;
+}
+
+template <bool FLIP>
+int stencil_entry(const void* x, const void* weight, const void* bias, void* y, int64_t n,
+                  int64_t c, int64_t d, int64_t h, int64_t w, int32_t k, int32_t dtype,
+                  int32_t tile_w, int32_t depth_chunk, void* stream) {
+  MEDNEXT_CHECK_ARG(x != nullptr && weight != nullptr && y != nullptr, "null tensor pointer");
+  MEDNEXT_CHECK_ARG(dtype_ok(dtype), "unsupported dtype");
+  MEDNEXT_CHECK_ARG((reinterpret_cast<uintptr_t>(weight) & 3u) == 0,
+                    "weight must be 4-byte aligned");
+  Plan pl;
+  int st = make_plan(n, c, d, h, w, k, acc_bytes_of(dtype), tile_w, depth_chunk, &pl);
+  if (st != MEDNEXT_STATUS_OK) return st;
+  const bool vec = (w % 4 == 0) && aligned16(x) && aligned16(y);
+  auto s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MEDNEXT_DTYPE_F32: return launch_stencil<float, FLIP>(x, weight, bias, y, pl, k, vec, s);
+    case MEDNEXT_DTYPE_F64: return launch_stencil<double, FLIP>(x, weight, bias, y, pl, k, vec, s);
+    case MEDNEXT_DTYPE_F16: return launch_stencil<f16_t, FLIP>(x, weight, bias, y, pl, k, vec, s);
+    default: return launch_stencil<bf16_t, FLIP>(x, weight, bias, y, pl, k, vec, s);
+  }
+}
+
+template <typename T, int K>
+int launch_wgrad_k(const void* x, const void* dy, void* dw, void* db, void* ws, const Plan& pl,
+                   bool vec, hipStream_t st) {
+  using Acc = typename AccOf<T>::type;
+  const dim3 grid(static_cast<unsigned>(pl.blocks));
+  const dim3 block(pl.threads);
+  auto px = static_cast<const T*>(x);
+  auto pdy = static_cast<const T*>(dy);
+  auto part = static_cast<Acc*>(ws);
+  if (vec)
+    hipLaunchKernelGGL((dw_wgrad_kernel<T, Acc, K, true>), grid, block, pl.lds_bytes, st, px, pdy,
+                       part, pl.g, pl.splits);
+  else
+    hipLaunchKernelGGL((dw_wgrad_kernel<T, Acc, K, false>), grid, block, pl.lds_bytes, st, px,
+                       pdy, part, pl.g, pl.splits);
+  MEDNEXT_CHECK_LAUNCH();
+  hipLaunchKernelGGL((dw_wgrad_finish_kernel<T, Acc>), dim3(pl.g.C), dim3(128), 0, st, part,
+                     static_cast<T*>(dw), static_cast<T*>(db), pl.splits, K * K * K);
+  MEDNEXT_CHECK_LAUNCH();
+  return MEDNEXT_STATUS_OK;
+}
+
+template <typename T>
+int launch_wgrad(const void* x, const void* dy, void* dw, void* db, void* ws, const Plan& pl, int k,
+                 bool vec, hipStream_t st) {
+  switch (k) {
+    case 1: return launch_wgrad_k<T, 1>(x, dy, dw, db, ws, pl, vec, st);
+    case 3: return launch_wgrad_k<T, 3>(x, dy, dw, db, ws, pl, vec, st);
+    default: return launch_wgrad_k<T, 5>(x, dy, dw, db, ws, pl, vec, st);
+  }
+}
+
+}  // namespace
+}  // namespace mednext
+
+using namespace mednext;
+
+extern "C" int32_t mednext_depthwise3d_fwd(const void* x, const void* weight, const void* bias,
+                                           void* y, int64_t n, int64_t c, int64_t d, int64_t h,
+                                           int64_t w, int32_t kernel_size, int32_t dtype,
+                                           int32_t tile_w, int32_t depth_chunk, void* stream) {
+  return stencil_entry<false>(x, weight, bias, y, n, c, d, h, w, kernel_size, dtype, tile_w,
+                              depth_chunk, stream);
+}
+
+extern "C" int32_t mednext_depthwise3d_dgrad(const void* grad_output, const void* weight,
+                                             void* grad_input, int64_t n, int64_t c, int64_t d,
+                                             int64_t h, int64_t w, int32_t kernel_size,
+                                             int32_t dtype, int32_t tile_w, int32_t depth_chunk,
+                                             void* stream) {
+  return stencil_entry<true>(grad_output, weight, nullptr, grad_input, n, c, d, h, w, kernel_size,
+                             dtype, tile_w, depth_chunk, stream);
+}
+
+extern "C" size_t mednext_depthwise3d_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t d,
+                                                            int64_t h, int64_t w,
+                                                            int32_t kernel_size, int32_t dtype,
+                                                            int32_t tile_w, int32_t depth_chunk) {
+  if (!dtype_ok(dtype)) return 0;
+  Plan pl;
+  if (make_plan(n, c, d, h, w, kernel_size, acc_bytes_of(dtype), tile_w, depth_chunk, &pl) !=
+      MEDNEXT_STATUS_OK)
+    return 0;
+  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
+  return static_cast<size_t>(c * pl.splits * (k3 + 1) * acc_bytes_of(dtype));
+}
+
+extern "C" int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_output,
+                                             void* grad_weight, void* grad_bias, void* workspace,
+                                             size_t workspace_bytes, int64_t n, int64_t c,
+                                             int64_t d, int64_t h, int64_t w, int32_t kernel_size,
+                                             int32_t dtype, int32_t tile_w, int32_t depth_chunk,
+                                             void* stream) {
+  MEDNEXT_CHECK_ARG(x != nullptr && grad_output != nullptr && grad_weight != nullptr,
+                    "null tensor pointer");
+  MEDNEXT_CHECK_ARG(dtype_ok(dtype), "unsupported dtype");
+  Plan pl;
+  int st = make_plan(n, c, d, h, w, kernel_size, acc_bytes_of(dtype), tile_w, depth_chunk, &pl);
+  if (st != MEDNEXT_STATUS_OK) return st;
+  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
+  const size_t need = static_cast<size_t>(c * pl.splits * (k3 + 1) * acc_bytes_of(dtype));
+  MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+  const bool vec = (w % 4 == 0) && aligned16(x) && aligned16(grad_output);
+  auto s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MEDNEXT_DTYPE_F32:
+      return launch_wgrad<float>(x, grad_output, grad_weight, grad_bias, workspace, pl,
+                                 kernel_size, vec, s);
+    case MEDNEXT_DTYPE_F64:
+      return launch_wgrad<double>(x, grad_output, grad_weight, grad_bias, workspace, pl,
+                                  kernel_size, vec, s);
+    case MEDNEXT_DTYPE_F16:
+      return launch_wgrad<f16_t>(x, grad_output, grad_weight, grad_bias, workspace, pl,
+                                 kernel_size, vec, s);
+    default:
+      return launch_wgrad<bf16_t>(x, grad_output, grad_weight, grad_bias, workspace, pl,
+                                  kernel_size, vec, s);
+  }
+}

@@ -1,0 +1,414 @@
+"""PyTorch operators backed by libmednext_hip.so.
+
+Two layers, mirroring the reference's ``ops/_triton/depthwise.py``:
+
+* low-level launchers (``depthwise_forward``, ``depthwise_input_grad``,
+  ``depthwise_weight_grad``, ``group_norm_forward``, ``group_norm_backward``) that
+  validate tensors and raise ``ValueError`` exactly where the reference's
+  launchers do (reference ``ops/_triton/depthwise.py:271-302, 351-390``);
+* ``torch.library`` custom ops under the ``mednext_accel_amd`` namespace with
+  fake-tensor and autograd registrations, so they trace under
+  ``torch.compile(fullgraph=True)`` and pass ``torch.library.opcheck``.
+
+Every kernel runs on PyTorch's current stream; every output and workspace is
+allocated by PyTorch. There is no fallback: if the library is missing the
+launch raises.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _hip
+from .tiles import depthwise_recipe, group_norm_splits
+
+SUPPORTED_KERNELS = (1, 3, 5)
+
+
+# --------------------------------------------------------------------------- checks
+
+
+def _check_device(*tensors: Tensor) -> None:
+    if not all(t.is_cuda for t in tensors):
+        raise ValueError("CUDA (ROCm) tensors are required")
+
+
+def _check_recipe(recipe) -> tuple[int, int]:
+    if recipe is None or len(recipe) != 2:
+        raise ValueError("recipe must be [tile_w, depth_chunk]")
+    tile_w, depth_chunk = int(recipe[0]), int(recipe[1])
+    if tile_w not in (4, 8, 16, 32, 64) or depth_chunk < 1:
+        raise ValueError("tile_w must be 4..64 (power of two) and depth_chunk >= 1")
+    return tile_w, depth_chunk
+
+
+def _check_depthwise(x: Tensor, weight: Tensor) -> int:
+    if x.ndim != 5 or weight.ndim != 5:
+        raise ValueError("input and weight must be NCDHW and C1KKK tensors")
+    if not (x.is_contiguous() and weight.is_contiguous()):
+        raise ValueError("contiguous tensors are required")
+    channels = x.shape[1]
+    if weight.shape[0] != channels or weight.shape[1] != 1 or len(set(weight.shape[2:])) != 1:
+        raise ValueError("weight must have shape [C, 1, K, K, K]")
+    kernel_size = int(weight.shape[2])
+    if kernel_size < 1 or kernel_size % 2 == 0:
+        raise ValueError("kernel_size must be a positive odd integer")
+    if kernel_size not in SUPPORTED_KERNELS:
+        raise ValueError(f"kernel_size must be one of {SUPPORTED_KERNELS}")
+    if weight.dtype != x.dtype:
+        raise ValueError("weight must have the input's dtype")
+    return kernel_size
+
+
+def _recipe_for(x: Tensor, kernel_size: int, recipe) -> tuple[int, int]:
+    if recipe is None:
+        n, c, d, h, w = (int(s) for s in x.shape)
+        recipe = depthwise_recipe(n, c, (d, h, w), kernel_size)
+    return _check_recipe(recipe)
+
+
+# ------------------------------------------------------------------ low-level launchers
+
+
+def depthwise_forward(
+    x: Tensor, weight: Tensor, bias: Tensor | None = None, recipe=None
+) -> Tensor:
+    """y = conv3d(x, weight, bias, padding=k//2, groups=C) on the HIP stencil kernel."""
+    _check_device(x, weight, *(() if bias is None else (bias,)))
+    kernel_size = _check_depthwise(x, weight)
+    if bias is not None and (bias.shape != (x.shape[1],) or bias.dtype != x.dtype):
+        raise ValueError("bias must be [C] in the input's dtype")
+    tile_w, depth_chunk = _recipe_for(x, kernel_size, recipe)
+    y = torch.empty_like(x)
+    if x.numel() == 0:
+        return y
+    n, c, d, h, w = x.shape
+    lib = _hip.load()
+    _hip.check(
+        lib.mednext_depthwise3d_fwd(
+            x.data_ptr(), weight.data_ptr(), _hip.ptr(bias.contiguous() if bias is not None else None),
+            y.data_ptr(), n, c, d, h, w, kernel_size, _hip.dtype_code(x.dtype), tile_w,
+            depth_chunk, _hip.stream_of(x),
+        ),
+        "mednext_depthwise3d_fwd",
+    )
+    return y
+
+
+def depthwise_input_grad(grad_output: Tensor, weight: Tensor, recipe=None) -> Tensor:
+    """Stride-one same-padding depthwise dX (reference depthwise.py:271-302)."""
+    _check_device(grad_output, weight)
+    kernel_size = _check_depthwise(grad_output, weight)
+    tile_w, depth_chunk = _recipe_for(grad_output, kernel_size, recipe)
+    out = torch.empty_like(grad_output)
+    if grad_output.numel() == 0:
+        return out
+    n, c, d, h, w = grad_output.shape
+    lib = _hip.load()
+    _hip.check(
+        lib.mednext_depthwise3d_dgrad(
+            grad_output.data_ptr(), weight.data_ptr(), out.data_ptr(), n, c, d, h, w,
+            kernel_size, _hip.dtype_code(grad_output.dtype), tile_w, depth_chunk,
+            _hip.stream_of(grad_output),
+        ),
+        "mednext_depthwise3d_dgrad",
+    )
+    return out
+
+
+def depthwise_weight_grad(
+    x: Tensor, grad_output: Tensor, kernel_size: int = 3, recipe=None
+) -> tuple[Tensor, Tensor]:
+    """Depthwise dW [C,1,k,k,k] and fused dB [C], both in x.dtype
+    (reference depthwise.py:351-390 computes dW only; dB came from ATen)."""
+    _check_device(x, grad_output)
+    if x.shape != grad_output.shape or x.ndim != 5:
+        raise ValueError("x and grad_output must have the same NCDHW shape")
+    if not (x.is_contiguous() and grad_output.is_contiguous()):
+        raise ValueError("contiguous NCDHW tensors are required")
+    if x.dtype != grad_output.dtype:
+        raise ValueError("x and grad_output must share a dtype")
+    if kernel_size < 1 or kernel_size % 2 == 0:
+        raise ValueError("kernel_size must be a positive odd integer")
+    if kernel_size not in SUPPORTED_KERNELS:
+        raise ValueError(f"kernel_size must be one of {SUPPORTED_KERNELS}")
+    n, c, d, h, w = (int(s) for s in x.shape)
+    tile_w, depth_chunk = _recipe_for(x, kernel_size, recipe)
+    grad_weight = torch.empty((c, 1, kernel_size, kernel_size, kernel_size), device=x.device, dtype=x.dtype)
+    grad_bias = torch.empty((c,), device=x.device, dtype=x.dtype)
+    if x.numel() == 0:
+        return grad_weight.zero_(), grad_bias.zero_()
+    code = _hip.dtype_code(x.dtype)
+    lib = _hip.load()
+    nbytes = lib.mednext_depthwise3d_wgrad_workspace_bytes(
+        n, c, d, h, w, kernel_size, code, tile_w, depth_chunk
+    )
+    if nbytes == 0:
+        raise _hip.HipLibraryError(f"wgrad workspace query failed: {_hip.last_error()}")
+    workspace = torch.empty((nbytes,), device=x.device, dtype=torch.uint8)
+    _hip.check(
+        lib.mednext_depthwise3d_wgrad(
+            x.data_ptr(), grad_output.data_ptr(), grad_weight.data_ptr(), grad_bias.data_ptr(),
+            workspace.data_ptr(), nbytes, n, c, d, h, w, kernel_size, code, tile_w, depth_chunk,
+            _hip.stream_of(x),
+        ),
+        "mednext_depthwise3d_wgrad",
+    )
+    return grad_weight, grad_bias
+
+
+def _stats_dtype(x: Tensor) -> torch.dtype:
+    return torch.float64 if x.dtype == torch.float64 else torch.float32
+
+
+def group_norm_forward(
+    x: Tensor,
+    weight: Tensor | None,
+    bias: Tensor | None,
+    eps: float = 1e-5,
+    out_dtype: torch.dtype | None = None,
+    splits: int | None = None,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """GroupNorm(C, C) forward: returns (y, mean [N*C], rstd [N*C])."""
+    _check_device(x)
+    if x.ndim < 2 or not x.is_contiguous():
+        raise ValueError("a contiguous [N, C, ...] input is required")
+    n, c = int(x.shape[0]), int(x.shape[1])
+    v = x.numel() // max(1, n * c)
+    params = [p for p in (weight, bias) if p is not None]
+    pdtype = params[0].dtype if params else torch.float32
+    for p in params:
+        if p.shape != (c,) or p.dtype != pdtype or not p.is_cuda:
+            raise ValueError("affine parameters must be [C] CUDA tensors of one dtype")
+    out_dtype = x.dtype if out_dtype is None else out_dtype
+    y = torch.empty(x.shape, device=x.device, dtype=out_dtype)
+    mean = torch.empty((n * c,), device=x.device, dtype=_stats_dtype(x))
+    rstd = torch.empty_like(mean)
+    if x.numel() == 0:
+        return y, mean, rstd
+    splits = group_norm_splits(n, c, v) if splits is None else int(splits)
+    lib = _hip.load()
+    nbytes = lib.mednext_group_norm_workspace_bytes(n, c, v, splits)
+    workspace = torch.empty((max(1, nbytes),), device=x.device, dtype=torch.uint8)
+    _hip.check(
+        lib.mednext_group_norm_fwd(
+            x.data_ptr(), _hip.dtype_code(x.dtype), _hip.ptr(weight), _hip.ptr(bias),
+            _hip.dtype_code(pdtype), y.data_ptr(), _hip.dtype_code(out_dtype), mean.data_ptr(),
+            rstd.data_ptr(), n, c, v, float(eps), splits, workspace.data_ptr(), nbytes,
+            _hip.stream_of(x),
+        ),
+        "mednext_group_norm_fwd",
+    )
+    return y, mean, rstd
+
+
+def group_norm_backward(
+    grad_output: Tensor,
+    x: Tensor,
+    mean: Tensor,
+    rstd: Tensor,
+    weight: Tensor | None,
+    need_input: bool = True,
+    need_weight: bool = True,
+    need_bias: bool = True,
+    param_dtype: torch.dtype = torch.float32,
+    splits: int | None = None,
+) -> tuple[Tensor | None, Tensor | None, Tensor | None]:
+    """GroupNorm(C, C) backward: (dx in x.dtype, dgamma, dbeta in param_dtype)."""
+    _check_device(grad_output, x, mean, rstd)
+    if grad_output.shape != x.shape or not (grad_output.is_contiguous() and x.is_contiguous()):
+        raise ValueError("grad_output and x must be contiguous with the same shape")
+    n, c = int(x.shape[0]), int(x.shape[1])
+    v = x.numel() // max(1, n * c)
+    if weight is not None:
+        param_dtype = weight.dtype
+    dx = torch.empty_like(x) if need_input else None
+    dgamma = torch.empty((c,), device=x.device, dtype=param_dtype) if need_weight else None
+    dbeta = torch.empty((c,), device=x.device, dtype=param_dtype) if need_bias else None
+    if x.numel() == 0:
+        return dx, (None if dgamma is None else dgamma.zero_()), (None if dbeta is None else dbeta.zero_())
+    splits = group_norm_splits(n, c, v) if splits is None else int(splits)
+    lib = _hip.load()
+    nbytes = lib.mednext_group_norm_workspace_bytes(n, c, v, splits)
+    workspace = torch.empty((max(1, nbytes),), device=x.device, dtype=torch.uint8)
+    _hip.check(
+        lib.mednext_group_norm_bwd(
+            grad_output.data_ptr(), _hip.dtype_code(grad_output.dtype), x.data_ptr(),
+            _hip.dtype_code(x.dtype), mean.data_ptr(), rstd.data_ptr(), _hip.ptr(weight),
+            _hip.dtype_code(param_dtype), _hip.ptr(dx), _hip.ptr(dgamma), _hip.ptr(dbeta), n, c,
+            v, splits, workspace.data_ptr(), nbytes, _hip.stream_of(x),
+        ),
+        "mednext_group_norm_bwd",
+    )
+    return dx, dgamma, dbeta
+
+
+# ------------------------------------------------------------------------ custom ops
+
+
+@torch.library.custom_op("mednext_accel_amd::depthwise_input_grad_odd_regular", mutates_args=())
+def depthwise_input_grad_regular(
+    grad_output: Tensor, weight: Tensor, kernel_size: int, recipe: list[int]
+) -> Tensor:
+    """dX for one regular depthwise shape (reference depthwise.py:486-513)."""
+    return depthwise_input_grad(grad_output.contiguous(), weight.contiguous(), recipe)
+
+
+@depthwise_input_grad_regular.register_fake
+def _(grad_output, weight, kernel_size, recipe):
+    return torch.empty_like(grad_output, memory_format=torch.contiguous_format)
+
+
+@torch.library.custom_op("mednext_accel_amd::depthwise_weight_grad_odd_regular", mutates_args=())
+def depthwise_weight_grad_regular(
+    x: Tensor, grad_output: Tensor, kernel_size: int, recipe: list[int]
+) -> tuple[Tensor, Tensor]:
+    """(dW, dB) for one regular depthwise shape (reference depthwise.py:445-483)."""
+    return depthwise_weight_grad(x.contiguous(), grad_output.contiguous(), kernel_size, recipe)
+
+
+@depthwise_weight_grad_regular.register_fake
+def _(x, grad_output, kernel_size, recipe):
+    c = x.shape[1]
+    return (
+        x.new_empty((c, 1, kernel_size, kernel_size, kernel_size)),
+        x.new_empty((c,)),
+    )
+
+
+@torch.library.custom_op("mednext_accel_amd::depthwise_conv3d_odd_regular", mutates_args=())
+def depthwise_conv3d_regular(
+    x: Tensor,
+    weight: Tensor,
+    bias: Tensor | None,
+    kernel_size: int,
+    fwd_recipe: list[int],
+    dx_recipe: list[int],
+    dw_recipe: list[int],
+    custom_fwd: bool = True,
+    custom_dx: bool = True,
+    custom_dw: bool = True,
+) -> Tensor:
+    """Depthwise Conv3d with per-phase HIP/native selection
+    (reference depthwise.py:549-563, which always runs F.conv3d forward)."""
+    if custom_fwd:
+        return depthwise_forward(x, weight, bias, fwd_recipe)
+    return torch.nn.functional.conv3d(x, weight, bias, padding=kernel_size // 2, groups=x.shape[1])
+
+
+@depthwise_conv3d_regular.register_fake
+def _(x, weight, bias, kernel_size, fwd_recipe, dx_recipe, dw_recipe, custom_fwd=True, custom_dx=True, custom_dw=True):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+def _setup_depthwise(ctx, inputs, output):
+    x, weight, bias, kernel_size, _fwd, dx_recipe, dw_recipe, _cf, custom_dx, custom_dw = inputs
+    ctx.save_for_backward(x, weight)
+    ctx.has_bias = bias is not None
+    ctx.kernel_size = kernel_size
+    ctx.dx_recipe = list(dx_recipe)
+    ctx.dw_recipe = list(dw_recipe)
+    ctx.custom_dx = custom_dx
+    ctx.custom_dw = custom_dw
+
+
+def _depthwise_backward(ctx, grad_output):
+    """Mirror of the reference's per-phase mask (depthwise.py:609-648), except
+    that dB is fused into the custom dW pass instead of always going native."""
+    x, weight = ctx.saved_tensors
+    grad_output = grad_output.contiguous()
+    need_dx, need_dw, need_db = ctx.needs_input_grad[:3]
+    need_db = need_db and ctx.has_bias
+    custom_db = need_db and need_dw and ctx.custom_dw
+    native_mask = [need_dx and not ctx.custom_dx, need_dw and not ctx.custom_dw, need_db and not custom_db]
+    grad_input = grad_weight = grad_bias = None
+    if any(native_mask):
+        pad = ctx.kernel_size // 2
+        channels = x.shape[1]
+        grad_input, grad_weight, grad_bias = torch.ops.aten.convolution_backward(
+            grad_output, x, weight, [channels] if ctx.has_bias else None, [1, 1, 1],
+            [pad, pad, pad], [1, 1, 1], False, [0, 0, 0], channels, native_mask,
+        )
+    if need_dx and ctx.custom_dx:
+        grad_input = depthwise_input_grad_regular(grad_output, weight, ctx.kernel_size, ctx.dx_recipe)
+    if need_dw and ctx.custom_dw:
+        grad_weight, fused_bias = depthwise_weight_grad_regular(x, grad_output, ctx.kernel_size, ctx.dw_recipe)
+        if custom_db:
+            grad_bias = fused_bias
+    return grad_input, grad_weight, grad_bias, None, None, None, None, None, None, None
+
+
+depthwise_conv3d_regular.register_autograd(_depthwise_backward, setup_context=_setup_depthwise)
+
+
+@torch.library.custom_op("mednext_accel_amd::group_norm_channels", mutates_args=())
+def group_norm_channels(
+    x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: float, out_dtype: torch.dtype | None
+) -> tuple[Tensor, Tensor, Tensor]:
+    """GroupNorm(C, C): (y, mean, rstd). ``out_dtype`` lets a bf16 input produce
+    the fp32 output the reference gets from autocast's fp32 group_norm."""
+    return group_norm_forward(x.contiguous(), weight, bias, eps, out_dtype)
+
+
+@group_norm_channels.register_fake
+def _(x, weight, bias, eps, out_dtype):
+    n, c = x.shape[0], x.shape[1]
+    stats = torch.float64 if x.dtype == torch.float64 else torch.float32
+    return (
+        torch.empty(x.shape, dtype=x.dtype if out_dtype is None else out_dtype, device=x.device),
+        x.new_empty((n * c,), dtype=stats),
+        x.new_empty((n * c,), dtype=stats),
+    )
+
+
+@torch.library.custom_op("mednext_accel_amd::group_norm_channels_backward", mutates_args=())
+def group_norm_channels_backward(
+    grad_output: Tensor,
+    x: Tensor,
+    mean: Tensor,
+    rstd: Tensor,
+    weight: Tensor | None,
+    param_dtype: torch.dtype,
+) -> tuple[Tensor, Tensor, Tensor]:
+    dx, dgamma, dbeta = group_norm_backward(
+        grad_output.contiguous(), x.contiguous(), mean, rstd, weight, True, True, True, param_dtype
+    )
+    return dx, dgamma, dbeta
+
+
+@group_norm_channels_backward.register_fake
+def _(grad_output, x, mean, rstd, weight, param_dtype):
+    c = x.shape[1]
+    return (
+        torch.empty_like(x, memory_format=torch.contiguous_format),
+        x.new_empty((c,), dtype=param_dtype),
+        x.new_empty((c,), dtype=param_dtype),
+    )
+
+
+def _setup_group_norm(ctx, inputs, output):
+    x, weight, bias, _eps, _out_dtype = inputs
+    _y, mean, rstd = output
+    ctx.mark_non_differentiable(mean, rstd)
+    ctx.save_for_backward(x, mean, rstd, weight)
+    ctx.param_dtype = (weight if weight is not None else bias).dtype if (weight is not None or bias is not None) else torch.float32
+    ctx.has_weight = weight is not None
+    ctx.has_bias = bias is not None
+
+
+def _group_norm_backward(ctx, grad_y, _grad_mean, _grad_rstd):
+    x, mean, rstd, weight = ctx.saved_tensors
+    dx, dgamma, dbeta = group_norm_channels_backward(
+        grad_y, x, mean, rstd, weight if ctx.has_weight else None, ctx.param_dtype
+    )
+    return (
+        dx,
+        dgamma if ctx.has_weight else None,
+        dbeta if ctx.has_bias else None,
+        None,
+        None,
+    )
+
+
+group_norm_channels.register_autograd(_group_norm_backward, setup_context=_setup_group_norm)

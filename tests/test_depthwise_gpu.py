@@ -1,0 +1,169 @@
+"""HIP depthwise Conv3d (fwd, dgrad, wgrad + fused dB) parity on the GPU.
+
+Small shapes are checked against the CPU oracle and the golden fixtures; the
+BASELINE sizes (cfg0 fp32 1x32x64^3, cfg1 bf16 stage shapes) against the oracle
+(cfg0) or the reference's own torch path in fp32 on the same device (cfg1).
+Tolerances (normwise max relative error, tests/helpers.py): fp64 1e-12;
+fp32 1e-5 outputs / dX, 1e-4 dW and dB; bf16 / fp16 2e-2.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from helpers import BF16, FP32_OUT, FP32_WGRAD, max_rel
+from mednext_accel_amd import hip_ops
+from mednext_accel_amd.tiles import depthwise_recipe
+from oracle import depthwise as odw
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = np.load(Path(__file__).with_name("golden") / "golden_ops.npz")
+DEV = "cuda"
+TOL = {
+    torch.float64: (1e-12, 1e-12),
+    torch.float32: (FP32_OUT, FP32_WGRAD),
+    torch.bfloat16: (BF16, BF16),
+    torch.float16: (BF16, BF16),
+}
+
+
+def run_all(x, w, b, dy, recipe=None):
+    k = w.shape[-1]
+    y = hip_ops.depthwise_forward(x, w, b, recipe)
+    dx = hip_ops.depthwise_input_grad(dy, w, recipe)
+    dw, db = hip_ops.depthwise_weight_grad(x, dy, k, recipe)
+    torch.cuda.synchronize()
+    return y, dx, dw, db
+
+
+@pytest.mark.parametrize("k", [1, 3, 5])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16, torch.float16])
+def test_golden_shape_all_dtypes(k, dtype):
+    print(f"[depthwise golden] k={k} dtype={dtype}", flush=True)
+    g = {n: GOLDEN[f"dw_k{k}_{n}"] for n in ("x", "w", "b", "dy", "y", "dx", "dw", "db")}
+    cast = lambda a: torch.from_numpy(a).to(dtype)  # noqa: E731
+    x, w, b, dy = (cast(g[n]) for n in ("x", "w", "b", "dy"))
+    y, dx, dw, db = run_all(*(t.to(DEV) for t in (x, w, b, dy)))
+    out_tol, w_tol = TOL[dtype]
+    if dtype == torch.float64:
+        expect = g
+    else:  # oracle on the dtype-rounded inputs
+        xn, wn, bn, dyn = (t.double().numpy() for t in (x, w, b, dy))
+        expect = {
+            "y": odw.forward(xn, wn, bn),
+            "dx": odw.input_grad(dyn, wn),
+            "dw": odw.weight_grad(xn, dyn, k),
+            "db": odw.bias_grad(dyn),
+        }
+    assert max_rel(y, expect["y"]) <= out_tol
+    assert max_rel(dx, expect["dx"]) <= out_tol
+    assert max_rel(dw, expect["dw"]) <= w_tol
+    assert max_rel(db, expect["db"]) <= w_tol
+    assert y.dtype == dx.dtype == dw.dtype == db.dtype == dtype
+
+
+@pytest.mark.parametrize(
+    "shape,recipe",
+    [
+        ((1, 2, 9, 11, 13), [4, 2]),  # W not a multiple of 4 -> scalar path
+        ((2, 3, 3, 5, 8), [8, 1]),  # depth_chunk 1, tiny D
+        ((1, 1, 17, 33, 70), [64, 5]),  # ragged tiles in every direction
+        ((3, 2, 6, 2, 4), [4, 100]),  # depth_chunk > D
+        ((1, 4, 8, 8, 64), [16, 3]),
+    ],
+)
+@pytest.mark.parametrize("k", [3, 5])
+def test_ragged_shapes_and_recipes_fp32(shape, recipe, k):
+    print(f"[depthwise ragged] shape={shape} recipe={recipe} k={k}", flush=True)
+    gen = torch.Generator().manual_seed(k + shape[-1])
+    x = torch.randn(shape, generator=gen)
+    w = torch.randn(shape[1], 1, k, k, k, generator=gen)
+    b = torch.randn(shape[1], generator=gen)
+    dy = torch.randn(shape, generator=gen)
+    y, dx, dw, db = run_all(*(t.to(DEV) for t in (x, w, b, dy)), recipe=recipe)
+    xn, wn, bn, dyn = (t.double().numpy() for t in (x, w, b, dy))
+    assert max_rel(y, odw.forward(xn, wn, bn)) <= FP32_OUT
+    assert max_rel(dx, odw.input_grad(dyn, wn)) <= FP32_OUT
+    assert max_rel(dw, odw.weight_grad(xn, dyn, k)) <= FP32_WGRAD
+    assert max_rel(db, odw.bias_grad(dyn)) <= FP32_WGRAD
+
+
+def test_cfg0_fp32_1x32x64_against_oracle():
+    """fp32 1x32x64^3, k3, w ~ U(+-1/sqrt(27)), b = 0."""
+    print("[depthwise cfg0] fp32 1x32x64^3", flush=True)
+    gen = torch.Generator().manual_seed(1)
+    x = torch.randn(1, 32, 64, 64, 64, generator=gen)
+    bound = 1.0 / 27**0.5
+    w = (torch.rand(32, 1, 3, 3, 3, generator=gen) * 2 - 1) * bound
+    b = torch.zeros(32)
+    dy = torch.randn(1, 32, 64, 64, 64, generator=torch.Generator().manual_seed(2))
+    y, dx, dw, db = run_all(*(t.to(DEV) for t in (x, w, b, dy)))
+    xn, wn, bn, dyn = (t.double().numpy() for t in (x, w, b, dy))
+    assert max_rel(y, odw.forward(xn, wn, bn)) <= FP32_OUT
+    assert max_rel(dx, odw.input_grad(dyn, wn)) <= FP32_OUT
+    assert max_rel(dw, odw.weight_grad(xn, dyn, 3)) <= FP32_WGRAD
+    assert max_rel(db, odw.bias_grad(dyn)) <= FP32_WGRAD
+
+
+STAGES = [(32, 128), (64, 64), (128, 32), (256, 16), (512, 8)]
+
+
+@pytest.mark.parametrize("k", [3, 5])
+@pytest.mark.parametrize("channels,size", STAGES)
+def test_cfg1_bf16_stage_shapes_against_torch(channels, size, k):
+    """bf16 in / fp32 accumulate at the MedNeXt stage shapes;
+    reference = the reference's torch path (F.conv3d + autograd) in fp32 on the
+    same bf16-rounded inputs."""
+    print(f"[depthwise cfg1] C={channels} S={size} k={k}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(channels * 7 + k)
+    shape = (1, channels, size, size, size)
+    x = torch.randn(shape, generator=gen, device=DEV).bfloat16()
+    dy = torch.randn(shape, generator=gen, device=DEV).bfloat16()
+    bound = 1.0 / (k**3) ** 0.5
+    w = ((torch.rand(channels, 1, k, k, k, generator=gen, device=DEV) * 2 - 1) * bound).bfloat16()
+    b = (torch.rand(channels, generator=gen, device=DEV) - 0.5).bfloat16()
+    y, dx, dw, db = run_all(x, w, b, dy)
+    xf, wf, bf = (t.float().requires_grad_() for t in (x, w, b))
+    yf = F.conv3d(xf, wf, bf, padding=k // 2, groups=channels)
+    rdx, rdw, rdb = torch.autograd.grad(yf, (xf, wf, bf), dy.float())
+    assert max_rel(y, yf) <= BF16
+    assert max_rel(dx, rdx) <= BF16
+    assert max_rel(dw, rdw) <= BF16
+    assert max_rel(db, rdb) <= BF16
+
+
+def test_recipe_default_is_valid_for_stage_shapes():
+    for channels, size in STAGES:
+        for k in (3, 5):
+            tile_w, depth_chunk = depthwise_recipe(1, channels, (size,) * 3, k)
+            assert tile_w <= size or tile_w == 4
+            assert 1 <= depth_chunk <= size
+
+
+def test_deterministic_weight_grad():
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    x = torch.randn(1, 16, 32, 32, 32, generator=gen, device=DEV)
+    dy = torch.randn(1, 16, 32, 32, 32, generator=gen, device=DEV)
+    a = hip_ops.depthwise_weight_grad(x, dy, 3)
+    b = hip_ops.depthwise_weight_grad(x, dy, 3)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_launcher_argument_errors():
+    x = torch.randn(1, 2, 4, 4, 4, device=DEV)
+    with pytest.raises(ValueError):
+        hip_ops.depthwise_input_grad(x, torch.randn(2, 1, 2, 2, 2, device=DEV))  # even k
+    with pytest.raises(ValueError):
+        hip_ops.depthwise_input_grad(x.transpose(2, 3), torch.randn(2, 1, 3, 3, 3, device=DEV))
+    with pytest.raises(ValueError):
+        hip_ops.depthwise_weight_grad(x, torch.randn(1, 2, 4, 4, 5, device=DEV), 3)
+    with pytest.raises(ValueError):
+        hip_ops.depthwise_forward(x.cpu(), torch.randn(2, 1, 3, 3, 3))
+    with pytest.raises(ValueError):
+        hip_ops.depthwise_forward(x, torch.randn(2, 1, 7, 7, 7, device=DEV))  # k=7 unsupported
