@@ -1,0 +1,260 @@
+#!/usr/bin/env python
+"""Benchmark of the MedNeXt operator path on one MI355X.
+
+Headline (BASELINE.json metric "depthwise Conv3d fwd+bwd GB/s (% of HBM
+peak)"): one step = depthwise Conv3d forward + input-grad + weight-grad (with
+the fused bias grad) at the configs[1] headline shape, N=1 C=32 D=H=W=128, k=3,
+bf16 in / fp32 accumulate. ``value`` = algorithmic bytes of the three phases
+(12 * E bytes: two bf16 streams per phase) / their summed HIP-event time, with
+inputs resident in HBM and rotated over three input sets (>256 MiB Infinity
+Cache) so repeated timing cannot hit in MALL.
+
+Also reported: per-phase microseconds, the roofline of the dominant kernel
+(with HBM traffic from the committed rocprofv3 --pmc summary when present),
+the reference's CPU path timed on this host (``cpu_baseline``) and, when the
+model path is available, the MedNeXt-Base 128^3 training-step time.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _path in (ROOT / "mednext-accel_amd", ROOT):
+    if str(_path) not in sys.path:
+        sys.path.insert(0, str(_path))
+
+METRIC = "depthwise Conv3d fwd+bwd GB/s (% of HBM peak); MedNeXt-B 128³ train step ms"
+HBM_PEAK_GBS = 8000.0
+TRAFFIC_SUMMARY = ROOT / "profiles" / "depthwise_k3_c32_128_bf16_traffic.json"
+
+
+def parse_args() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--channels", type=int, default=32)
+    ap.add_argument("--size", type=int, default=128)
+    ap.add_argument("--kernel-size", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    ap.add_argument(
+        "--copy-calibration",
+        action="store_true",
+        help="before timing, run 3 untimed torch.neg launches over 2^27 bf16 elements (256 MiB read, "
+        "256 MiB written): the known-size kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE",
+    )
+    return ap.parse_args()
+
+
+def time_depthwise(args, torch, hip_ops):
+    dev = torch.device("cuda:0")
+    c, s, k = args.channels, args.size, args.kernel_size
+    shape = (1, c, s, s, s)
+    elements = c * s**3
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    bound = 1.0 / (k**3) ** 0.5
+    w = ((torch.rand(c, 1, k, k, k, generator=gen, device=dev) * 2 - 1) * bound).bfloat16()
+    b = ((torch.rand(c, generator=gen, device=dev) * 2 - 1) * bound).bfloat16()
+    # Three resident input sets (x, dy): 3 * 2 * 134 MB > 256 MB Infinity Cache.
+    sets = [
+        (
+            torch.randn(shape, generator=gen, device=dev).bfloat16(),
+            torch.randn(shape, generator=gen, device=dev).bfloat16(),
+        )
+        for _ in range(3)
+    ]
+    if args.copy_calibration:
+        src = torch.randn(2**27, generator=gen, device=dev).bfloat16()
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        del src, dst
+    torch.cuda.synchronize()
+
+    def step(i: int, events=None):
+        x, dy = sets[i % len(sets)]
+        if events:
+            events[0].record()
+        y = hip_ops.depthwise_forward(x, w, b)
+        if events:
+            events[1].record()
+        dx = hip_ops.depthwise_input_grad(dy, w)
+        if events:
+            events[2].record()
+        dw, db = hip_ops.depthwise_weight_grad(x, dy, k)
+        if events:
+            events[3].record()
+        return y, dx, dw, db
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    all_events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for i, ev in enumerate(all_events):
+        step(i, ev)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    phase_ms = {
+        "forward": [ev[0].elapsed_time(ev[1]) for ev in all_events],
+        "input_grad": [ev[1].elapsed_time(ev[2]) for ev in all_events],
+        "weight_grad": [ev[2].elapsed_time(ev[3]) for ev in all_events],
+    }
+    mean_ms = {name: statistics.fmean(v) for name, v in phase_ms.items()}
+    median_us = {name: 1000.0 * statistics.median(v) for name, v in phase_ms.items()}
+    step_ms = sum(mean_ms.values())
+    bytes_per_phase = 2 * elements * 2  # two bf16 streams of E elements
+    return {
+        "elements": elements,
+        "bytes_per_phase": bytes_per_phase,
+        "mean_ms": mean_ms,
+        "median_us": median_us,
+        "step_ms": step_ms,
+        "wall_ms_per_step": 1000.0 * wall / max(1, args.steps),
+        "gbs": 3 * bytes_per_phase / (step_ms * 1e-3) / 1e9,
+    }
+
+
+# Kernel-name prefixes (rocprofv3 short names) launched by each phase at k=3 bf16.
+PHASE_KERNELS = {
+    "forward": ("dw_mfma_stencil_kernel<3, false",),
+    "input_grad": ("dw_mfma_stencil_kernel<3, true",),
+    "weight_grad": ("dw_mfma_wgrad_kernel<3,", "dw_wgrad_finish_kernel<"),
+}
+
+
+def load_traffic(phase: str, kernel_size: int):
+    """HBM bytes per launch of ``phase`` from the committed, calibrated
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (k=3 headline workload only)."""
+    if kernel_size != 3 or not TRAFFIC_SUMMARY.exists():
+        return None
+    try:
+        kernels = json.loads(TRAFFIC_SUMMARY.read_text())["kernels"]
+    except (OSError, ValueError, KeyError):
+        return None
+    total, found = 0, set()
+    for name, entry in kernels.items():
+        for prefix in PHASE_KERNELS[phase]:
+            if name.startswith(prefix):
+                total += entry["hbm_bytes_per_launch"]
+                found.add(prefix)
+    return total if len(found) == len(PHASE_KERNELS[phase]) else None
+
+
+def cpu_baseline(args, torch):
+    """The reference's CPU path (F.conv3d + aten.convolution_backward) on a
+    bounded sample: cfg0's fp32 1x32x64^3 (fp32: bf16 CPU depthwise-3D is not a
+    reliable baseline), repeated until ~cpu_seconds are spent."""
+    from oracle.reference_cpu import depthwise_phases
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(1)
+    c, s, k = 32, 64, 3
+    x = torch.randn(1, c, s, s, s, generator=gen)
+    w = (torch.rand(c, 1, k, k, k, generator=gen) * 2 - 1) / (k**3) ** 0.5
+    b = torch.zeros(c)
+    dy = torch.randn(1, c, s, s, s, generator=torch.Generator().manual_seed(2))
+    depthwise_phases(x, w, b, dy)  # warmup
+    times = []
+    budget_end = time.perf_counter() + args.cpu_seconds
+    while len(times) < 3 or (time.perf_counter() < budget_end and len(times) < 50):
+        t0 = time.perf_counter()
+        depthwise_phases(x, w, b, dy)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    elements = c * s**3
+    bytes_fwd_bwd = 3 * 2 * elements * 4  # three phases, two fp32 streams each
+    return {
+        "value": round(bytes_fwd_bwd / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": (
+            f"reference CPU path (F.conv3d fwd + aten.convolution_backward dX, dW+dB) on cfg0 "
+            f"fp32 1x{c}x{s}^3 k{k}, {len(times)} reps, median {med * 1000:.1f} ms per fwd+bwd; "
+            f"same 24*E algorithmic-byte count as the GPU metric's fp32 form; os.cpu_count()={threads}"
+        ),
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only (got --gpus {args.gpus}): this operator path has no "
+            "multi-GPU mode; see DESIGN.md for how it would shard.",
+            file=sys.stderr,
+        )
+        return 2
+    import torch
+
+    from mednext_accel_amd import hip_ops
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dw = time_depthwise(args, torch, hip_ops)
+    phase_us = {name: round(1000.0 * ms, 2) for name, ms in dw["mean_ms"].items()}
+    dominant = max(dw["mean_ms"], key=dw["mean_ms"].get)
+    achieved = dw["bytes_per_phase"] / (dw["mean_ms"][dominant] * 1e-3) / 1e9
+    roofline = {
+        "bound": "hbm",
+        "kernel": {
+            "forward": "dw_mfma_stencil_kernel<K,FLIP=false>",
+            "input_grad": "dw_mfma_stencil_kernel<K,FLIP=true>",
+            "weight_grad": "dw_mfma_wgrad_kernel + dw_wgrad_finish_kernel",
+        }[dominant],
+        "phase": dominant,
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": load_traffic(dominant, args.kernel_size) if (args.channels, args.size) == (32, 128) else None,
+        "algorithmic_bytes_per_launch": dw["bytes_per_phase"],
+    }
+    result = {
+        "metric": METRIC,
+        "value": round(dw["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dw["step_ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (
+                f"depthwise_conv3d k{args.kernel_size} forward + input_grad + weight_grad(+fused bias_grad), "
+                f"N=1 C={args.channels} D=H=W={args.size}, bf16 in / fp32 accumulate, inputs ~N(0,1) "
+                "rotated over 3 resident sets (BASELINE configs[1] headline shape)"
+            ),
+            "hbm_frac_of_peak": round(dw["gbs"] / HBM_PEAK_GBS, 4),
+            "phase_us": phase_us,
+            "phase_median_us": {k: round(v, 2) for k, v in dw["median_us"].items()},
+            "wall_ms_per_step": round(dw["wall_ms_per_step"], 4),
+        },
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(args, torch)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -32,6 +32,12 @@ enum mednext_status {
   MEDNEXT_STATUS_UNSUPPORTED = 3
 };
 
+/* Depthwise compute engine. VALU: fp32/fp64 FMA stencil, every dtype.
+ * MFMA: bf16 banded-Toeplitz matrix-core kernels (k in {3,5}, W % 8 == 0,
+ * W >= 32, H >= 32, one (n, c) slab < 2 GiB; weight-grad also W % 32 == 0);
+ * tile_w is then the columns per workgroup (32, 64 or 128). */
+enum mednext_engine { MEDNEXT_ENGINE_VALU = 0, MEDNEXT_ENGINE_MFMA = 1 };
+
 enum mednext_dtype {
   MEDNEXT_DTYPE_F32 = 0,
   MEDNEXT_DTYPE_F64 = 1,
@@ -49,9 +55,9 @@ int32_t mednext_hip_abi_version(void);
  * Depthwise Conv3d, stride 1, odd cubic kernel k in {1,3,5}, zero "same"
  * padding k/2, groups == C. weight is [C,1,k,k,k] and bias [C], both in the
  * same dtype as x (the reference casts them to x.dtype before its op).
- * tile_w (4, 8, 16, 32 or 64 output columns per workgroup) and depth_chunk
- * (output planes per workgroup, >= 1) are the launch recipe chosen by the
- * gfx950 tile policy.
+ * engine (mednext_engine), tile_w (VALU: 4, 8, 16, 32 or 64 output columns per
+ * workgroup; MFMA: 32, 64 or 128) and depth_chunk (output planes per
+ * workgroup, >= 1) are the launch recipe chosen by the gfx950 tile policy.
  */
 
 /* y = conv3d(x, weight, bias, padding=k//2, groups=C).
@@ -60,21 +66,24 @@ int32_t mednext_hip_abi_version(void);
  * F.conv3d). bias may be NULL. */
 int32_t mednext_depthwise3d_fwd(const void* x, const void* weight, const void* bias, void* y,
                                 int64_t n, int64_t c, int64_t d, int64_t h, int64_t w,
-                                int32_t kernel_size, int32_t dtype, int32_t tile_w,
-                                int32_t depth_chunk, void* stream);
+                                int32_t kernel_size, int32_t dtype, int32_t engine,
+                                int32_t tile_w, int32_t depth_chunk, void* stream);
 
 /* grad_input = conv3d(grad_output, flip(weight), padding=k//2, groups=C).
  * Replaces mednext_accel::depthwise_input_grad_odd_regular
  * (reference ops/_triton/depthwise.py:159-203 kernel, :486-513 op). */
 int32_t mednext_depthwise3d_dgrad(const void* grad_output, const void* weight, void* grad_input,
                                   int64_t n, int64_t c, int64_t d, int64_t h, int64_t w,
-                                  int32_t kernel_size, int32_t dtype, int32_t tile_w,
-                                  int32_t depth_chunk, void* stream);
+                                  int32_t kernel_size, int32_t dtype, int32_t engine,
+                                  int32_t tile_w, int32_t depth_chunk, void* stream);
 
-/* Bytes of fp32 (fp64 for MEDNEXT_DTYPE_F64) partials the wgrad launch needs. */
+/* Bytes of fp32 (fp64 for MEDNEXT_DTYPE_F64) partials the wgrad launch needs
+ * (0 if the shape / recipe is unsupported). The MFMA engine additionally needs
+ * W % 32 == 0. */
 size_t mednext_depthwise3d_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t d, int64_t h,
                                                  int64_t w, int32_t kernel_size, int32_t dtype,
-                                                 int32_t tile_w, int32_t depth_chunk);
+                                                 int32_t engine, int32_t tile_w,
+                                                 int32_t depth_chunk);
 
 /* grad_weight[c,t] = sum x[n,c,pos+t-p] * grad_output[n,c,pos] (dtype of x) and,
  * when grad_bias != NULL, grad_bias[c] = sum grad_output[n,c,:] — fused in the
@@ -85,8 +94,8 @@ size_t mednext_depthwise3d_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t d
 int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_output, void* grad_weight,
                                   void* grad_bias, void* workspace, size_t workspace_bytes,
                                   int64_t n, int64_t c, int64_t d, int64_t h, int64_t w,
-                                  int32_t kernel_size, int32_t dtype, int32_t tile_w,
-                                  int32_t depth_chunk, void* stream);
+                                  int32_t kernel_size, int32_t dtype, int32_t engine,
+                                  int32_t tile_w, int32_t depth_chunk, void* stream);
 
 /* ---------------------------------------------------------------- group norm
  * GroupNorm with groups == channels on [N, C, V] (V = spatial volume), biased

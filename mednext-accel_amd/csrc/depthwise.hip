@@ -14,6 +14,7 @@
 // accumulates k^3 tap sums per thread, reduced per workgroup into a fp32/fp64
 // partial and then summed over workgroups in a fixed order (deterministic).
 #include "common.h"
+#include "depthwise_mfma.h"
 
 #include <type_traits>
 
@@ -360,24 +361,45 @@ __global__ __launch_bounds__(kMaxThreads) void dw_wgrad_kernel(const T* __restri
   for (int i = threadIdx.x; i < K3 + 1; i += blockDim.x) {
     Acc v = red[0][i];
     for (int wv = 1; wv < nwaves; ++wv) v += red[wv][i];
-    partial[(static_cast<int64_t>(t.c) * splits + split) * (K3 + 1) + i] = v;
+    partial[(static_cast<int64_t>(t.c) * (K3 + 1) + i) * splits + split] = v;
   }
 }
 
+// Sum the per-workgroup partials of one (channel, tap) in a fixed order: one
+// wave per tap, lane j takes partials j, j + 64, ... in fp64, then a fixed
+// butterfly. Partials are laid out [C][k^3 + 1][splits]; tap k^3 is the bias.
 template <typename T, typename Acc>
-__global__ void dw_wgrad_finish_kernel(const Acc* __restrict__ partial, T* __restrict__ dw,
-                                       T* __restrict__ db, int splits, int k3) {
-  const int c = blockIdx.x;
-  for (int i = threadIdx.x; i < k3 + 1; i += blockDim.x) {
-    double s = 0.0;
-    const Acc* p = partial + static_cast<int64_t>(c) * splits * (k3 + 1) + i;
-    for (int j = 0; j < splits; ++j) s += static_cast<double>(p[static_cast<int64_t>(j) * (k3 + 1)]);
-    if (i < k3) {
-      dw[static_cast<int64_t>(c) * k3 + i] = Cvt<T, Acc>::store(static_cast<Acc>(s));
+__global__ __launch_bounds__(256) void dw_wgrad_finish_kernel(const Acc* __restrict__ partial,
+                                                              T* __restrict__ dw,
+                                                              T* __restrict__ db, int channels,
+                                                              int splits, int k3) {
+  const int lane = threadIdx.x & 63;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (item >= static_cast<int64_t>(channels) * (k3 + 1)) return;
+  const Acc* p = partial + item * splits;
+  double s = 0.0;
+  for (int j = lane; j < splits; j += 64) s += static_cast<double>(p[j]);
+  s = wave_sum(s);
+  if (lane == 0) {
+    const int64_t c = item / (k3 + 1);
+    const int t = static_cast<int>(item - c * (k3 + 1));
+    if (t < k3) {
+      dw[c * k3 + t] = Cvt<T, Acc>::store(static_cast<Acc>(s));
     } else if (db != nullptr) {
       db[c] = Cvt<T, Acc>::store(static_cast<Acc>(s));
     }
   }
+}
+
+template <typename T, typename Acc>
+int launch_finish(const Acc* part, void* dw, void* db, int64_t c, int splits, int k3,
+                  hipStream_t st) {
+  const int64_t items = c * (k3 + 1);
+  hipLaunchKernelGGL((dw_wgrad_finish_kernel<T, Acc>), dim3(static_cast<unsigned>(cdiv(items, 4))),
+                     dim3(256), 0, st, part, static_cast<T*>(dw), static_cast<T*>(db),
+                     static_cast<int>(c), splits, k3);
+  MEDNEXT_CHECK_LAUNCH();
+  return MEDNEXT_STATUS_OK;
 }
 
 // ------------------------------------------------------------------ host side
@@ -478,16 +500,26 @@ bool dtype_ok(int dtype) {
 template <bool FLIP>
 int stencil_entry(const void* x, const void* weight, const void* bias, void* y, int64_t n,
                   int64_t c, int64_t d, int64_t h, int64_t w, int32_t k, int32_t dtype,
-                  int32_t tile_w, int32_t depth_chunk, void* stream) {
+                  int32_t engine, int32_t tile_w, int32_t depth_chunk, void* stream) {
   MEDNEXT_CHECK_ARG(x != nullptr && weight != nullptr && y != nullptr, "null tensor pointer");
   MEDNEXT_CHECK_ARG(dtype_ok(dtype), "unsupported dtype");
   MEDNEXT_CHECK_ARG((reinterpret_cast<uintptr_t>(weight) & 3u) == 0,
                     "weight must be 4-byte aligned");
+  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_VALU || engine == MEDNEXT_ENGINE_MFMA,
+                    "engine must be MEDNEXT_ENGINE_VALU or MEDNEXT_ENGINE_MFMA");
+  auto s = static_cast<hipStream_t>(stream);
+  if (engine == MEDNEXT_ENGINE_MFMA) {
+    MEDNEXT_CHECK_ARG(dtype == MEDNEXT_DTYPE_BF16, "the MFMA engine is bf16 only");
+    MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && d >= 1 && h < (int64_t(1) << 31) &&
+                          c < (int64_t(1) << 31) && d < (int64_t(1) << 31),
+                      "shape out of range");
+    MEDNEXT_CHECK_ARG(aligned16(x) && aligned16(y), "MFMA engine needs 16-byte aligned tensors");
+    return dw_mfma_stencil(x, weight, bias, y, n, c, d, h, w, k, FLIP, tile_w, depth_chunk, s);
+  }
   Plan pl;
   int st = make_plan(n, c, d, h, w, k, acc_bytes_of(dtype), tile_w, depth_chunk, &pl);
   if (st != MEDNEXT_STATUS_OK) return st;
   const bool vec = (w % 4 == 0) && aligned16(x) && aligned16(y);
-  auto s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case MEDNEXT_DTYPE_F32: return launch_stencil<float, FLIP>(x, weight, bias, y, pl, k, vec, s);
     case MEDNEXT_DTYPE_F64: return launch_stencil<double, FLIP>(x, weight, bias, y, pl, k, vec, s);
@@ -512,10 +544,7 @@ int launch_wgrad_k(const void* x, const void* dy, void* dw, void* db, void* ws, 
     hipLaunchKernelGGL((dw_wgrad_kernel<T, Acc, K, false>), grid, block, pl.lds_bytes, st, px,
                        pdy, part, pl.g, pl.splits);
   MEDNEXT_CHECK_LAUNCH();
-  hipLaunchKernelGGL((dw_wgrad_finish_kernel<T, Acc>), dim3(pl.g.C), dim3(128), 0, st, part,
-                     static_cast<T*>(dw), static_cast<T*>(db), pl.splits, K * K * K);
-  MEDNEXT_CHECK_LAUNCH();
-  return MEDNEXT_STATUS_OK;
+  return launch_finish<T, Acc>(part, dw, db, pl.g.C, pl.splits, K * K * K, st);
 }
 
 template <typename T>
@@ -536,30 +565,39 @@ using namespace mednext;
 extern "C" int32_t mednext_depthwise3d_fwd(const void* x, const void* weight, const void* bias,
                                            void* y, int64_t n, int64_t c, int64_t d, int64_t h,
                                            int64_t w, int32_t kernel_size, int32_t dtype,
-                                           int32_t tile_w, int32_t depth_chunk, void* stream) {
-  return stencil_entry<false>(x, weight, bias, y, n, c, d, h, w, kernel_size, dtype, tile_w,
-                              depth_chunk, stream);
+                                           int32_t engine, int32_t tile_w, int32_t depth_chunk,
+                                           void* stream) {
+  return stencil_entry<false>(x, weight, bias, y, n, c, d, h, w, kernel_size, dtype, engine,
+                              tile_w, depth_chunk, stream);
 }
 
 extern "C" int32_t mednext_depthwise3d_dgrad(const void* grad_output, const void* weight,
                                              void* grad_input, int64_t n, int64_t c, int64_t d,
                                              int64_t h, int64_t w, int32_t kernel_size,
-                                             int32_t dtype, int32_t tile_w, int32_t depth_chunk,
-                                             void* stream) {
+                                             int32_t dtype, int32_t engine, int32_t tile_w,
+                                             int32_t depth_chunk, void* stream) {
   return stencil_entry<true>(grad_output, weight, nullptr, grad_input, n, c, d, h, w, kernel_size,
-                             dtype, tile_w, depth_chunk, stream);
+                             dtype, engine, tile_w, depth_chunk, stream);
 }
 
 extern "C" size_t mednext_depthwise3d_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t d,
                                                             int64_t h, int64_t w,
                                                             int32_t kernel_size, int32_t dtype,
-                                                            int32_t tile_w, int32_t depth_chunk) {
+                                                            int32_t engine, int32_t tile_w,
+                                                            int32_t depth_chunk) {
   if (!dtype_ok(dtype)) return 0;
+  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
+  if (engine == MEDNEXT_ENGINE_MFMA) {
+    if (dtype != MEDNEXT_DTYPE_BF16) return 0;
+    const int splits = dw_mfma_wgrad_splits(n, c, d, h, w, kernel_size, tile_w, depth_chunk);
+    if (splits <= 0) return 0;
+    return static_cast<size_t>(c * splits * (k3 + 1) * 4);
+  }
+  if (engine != MEDNEXT_ENGINE_VALU) return 0;
   Plan pl;
   if (make_plan(n, c, d, h, w, kernel_size, acc_bytes_of(dtype), tile_w, depth_chunk, &pl) !=
       MEDNEXT_STATUS_OK)
     return 0;
-  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
   return static_cast<size_t>(c * pl.splits * (k3 + 1) * acc_bytes_of(dtype));
 }
 
@@ -567,19 +605,39 @@ extern "C" int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_out
                                              void* grad_weight, void* grad_bias, void* workspace,
                                              size_t workspace_bytes, int64_t n, int64_t c,
                                              int64_t d, int64_t h, int64_t w, int32_t kernel_size,
-                                             int32_t dtype, int32_t tile_w, int32_t depth_chunk,
-                                             void* stream) {
+                                             int32_t dtype, int32_t engine, int32_t tile_w,
+                                             int32_t depth_chunk, void* stream) {
   MEDNEXT_CHECK_ARG(x != nullptr && grad_output != nullptr && grad_weight != nullptr,
                     "null tensor pointer");
   MEDNEXT_CHECK_ARG(dtype_ok(dtype), "unsupported dtype");
+  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_VALU || engine == MEDNEXT_ENGINE_MFMA,
+                    "engine must be MEDNEXT_ENGINE_VALU or MEDNEXT_ENGINE_MFMA");
+  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
+  auto s = static_cast<hipStream_t>(stream);
+  if (engine == MEDNEXT_ENGINE_MFMA) {
+    MEDNEXT_CHECK_ARG(dtype == MEDNEXT_DTYPE_BF16, "the MFMA engine is bf16 only");
+    MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && d >= 1 && c < (int64_t(1) << 31) &&
+                          d < (int64_t(1) << 31) && h < (int64_t(1) << 31),
+                      "shape out of range");
+    MEDNEXT_CHECK_ARG(aligned16(x) && aligned16(grad_output),
+                      "MFMA engine needs 16-byte aligned tensors");
+    const int splits = dw_mfma_wgrad_splits(n, c, d, h, w, kernel_size, tile_w, depth_chunk);
+    MEDNEXT_CHECK_ARG(splits > 0,
+                      "MFMA wgrad needs k in {3,5}, W % 32 == 0, H >= 32, tile_w in {32,64,128}");
+    const size_t need = static_cast<size_t>(c * splits * (k3 + 1) * 4);
+    MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+    auto part = static_cast<float*>(workspace);
+    int st = dw_mfma_wgrad(x, grad_output, part, n, c, d, h, w, kernel_size, tile_w, depth_chunk, s);
+    if (st != MEDNEXT_STATUS_OK) return st;
+    return launch_finish<bf16_t, float>(part, grad_weight, grad_bias, c, splits,
+                                        static_cast<int>(k3), s);
+  }
   Plan pl;
   int st = make_plan(n, c, d, h, w, kernel_size, acc_bytes_of(dtype), tile_w, depth_chunk, &pl);
   if (st != MEDNEXT_STATUS_OK) return st;
-  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
   const size_t need = static_cast<size_t>(c * pl.splits * (k3 + 1) * acc_bytes_of(dtype));
   MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
   const bool vec = (w % 4 == 0) && aligned16(x) && aligned16(grad_output);
-  auto s = static_cast<hipStream_t>(stream);
   switch (dtype) {
     case MEDNEXT_DTYPE_F32:
       return launch_wgrad<float>(x, grad_output, grad_weight, grad_bias, workspace, pl,

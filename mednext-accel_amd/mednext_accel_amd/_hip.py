@@ -32,19 +32,19 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     "mednext_hip_abi_version": (_i32, ()),
     "mednext_depthwise3d_fwd": (
         _i32,
-        (_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p),
+        (_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
     ),
     "mednext_depthwise3d_dgrad": (
         _i32,
-        (_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p),
+        (_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
     ),
     "mednext_depthwise3d_wgrad_workspace_bytes": (
         c_size_t,
-        (_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32),
+        (_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32),
     ),
     "mednext_depthwise3d_wgrad": (
         _i32,
-        (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _p),
+        (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
     ),
     "mednext_group_norm_workspace_bytes": (c_size_t, (_i64, _i64, _i64, _i32)),
     "mednext_group_norm_fwd": (
@@ -57,7 +57,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

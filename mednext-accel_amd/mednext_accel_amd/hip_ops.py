@@ -21,7 +21,7 @@ import torch
 from torch import Tensor
 
 from . import _hip
-from .tiles import depthwise_recipe, group_norm_splits
+from .tiles import ENGINE_MFMA, ENGINE_VALU, depthwise_recipe, group_norm_splits
 
 SUPPORTED_KERNELS = (1, 3, 5)
 
@@ -34,13 +34,21 @@ def _check_device(*tensors: Tensor) -> None:
         raise ValueError("CUDA (ROCm) tensors are required")
 
 
-def _check_recipe(recipe) -> tuple[int, int]:
-    if recipe is None or len(recipe) != 2:
-        raise ValueError("recipe must be [tile_w, depth_chunk]")
-    tile_w, depth_chunk = int(recipe[0]), int(recipe[1])
-    if tile_w not in (4, 8, 16, 32, 64) or depth_chunk < 1:
-        raise ValueError("tile_w must be 4..64 (power of two) and depth_chunk >= 1")
-    return tile_w, depth_chunk
+def _check_recipe(recipe) -> tuple[int, int, int]:
+    if recipe is None or len(recipe) != 3:
+        raise ValueError("recipe must be [engine, tile_w, depth_chunk]")
+    engine, tile_w, depth_chunk = (int(v) for v in recipe)
+    if engine == ENGINE_VALU:
+        if tile_w not in (4, 8, 16, 32, 64):
+            raise ValueError("VALU tile_w must be 4, 8, 16, 32 or 64")
+    elif engine == ENGINE_MFMA:
+        if tile_w not in (32, 64, 128):
+            raise ValueError("MFMA tile_w must be 32, 64 or 128")
+    else:
+        raise ValueError("engine must be 0 (VALU) or 1 (MFMA)")
+    if depth_chunk < 1:
+        raise ValueError("depth_chunk must be >= 1")
+    return engine, tile_w, depth_chunk
 
 
 def _check_depthwise(x: Tensor, weight: Tensor) -> int:
@@ -61,10 +69,11 @@ def _check_depthwise(x: Tensor, weight: Tensor) -> int:
     return kernel_size
 
 
-def _recipe_for(x: Tensor, kernel_size: int, recipe) -> tuple[int, int]:
+def _recipe_for(x: Tensor, kernel_size: int, recipe, phase: str) -> tuple[int, int, int]:
     if recipe is None:
-        n, c, d, h, w = (int(s) for s in x.shape)
-        recipe = depthwise_recipe(n, c, (d, h, w), kernel_size)
+        n, c, d, h, w = (int(v) for v in x.shape)
+        dtype = str(x.dtype).removeprefix("torch.")
+        recipe = depthwise_recipe(n, c, (d, h, w), kernel_size, dtype, phase)
     return _check_recipe(recipe)
 
 
@@ -79,7 +88,7 @@ def depthwise_forward(
     kernel_size = _check_depthwise(x, weight)
     if bias is not None and (bias.shape != (x.shape[1],) or bias.dtype != x.dtype):
         raise ValueError("bias must be [C] in the input's dtype")
-    tile_w, depth_chunk = _recipe_for(x, kernel_size, recipe)
+    engine, tile_w, depth_chunk = _recipe_for(x, kernel_size, recipe, "forward")
     y = torch.empty_like(x)
     if x.numel() == 0:
         return y
@@ -88,7 +97,7 @@ def depthwise_forward(
     _hip.check(
         lib.mednext_depthwise3d_fwd(
             x.data_ptr(), weight.data_ptr(), _hip.ptr(bias.contiguous() if bias is not None else None),
-            y.data_ptr(), n, c, d, h, w, kernel_size, _hip.dtype_code(x.dtype), tile_w,
+            y.data_ptr(), n, c, d, h, w, kernel_size, _hip.dtype_code(x.dtype), engine, tile_w,
             depth_chunk, _hip.stream_of(x),
         ),
         "mednext_depthwise3d_fwd",
@@ -100,7 +109,7 @@ def depthwise_input_grad(grad_output: Tensor, weight: Tensor, recipe=None) -> Te
     """Stride-one same-padding depthwise dX (reference depthwise.py:271-302)."""
     _check_device(grad_output, weight)
     kernel_size = _check_depthwise(grad_output, weight)
-    tile_w, depth_chunk = _recipe_for(grad_output, kernel_size, recipe)
+    engine, tile_w, depth_chunk = _recipe_for(grad_output, kernel_size, recipe, "input_grad")
     out = torch.empty_like(grad_output)
     if grad_output.numel() == 0:
         return out
@@ -109,7 +118,7 @@ def depthwise_input_grad(grad_output: Tensor, weight: Tensor, recipe=None) -> Te
     _hip.check(
         lib.mednext_depthwise3d_dgrad(
             grad_output.data_ptr(), weight.data_ptr(), out.data_ptr(), n, c, d, h, w,
-            kernel_size, _hip.dtype_code(grad_output.dtype), tile_w, depth_chunk,
+            kernel_size, _hip.dtype_code(grad_output.dtype), engine, tile_w, depth_chunk,
             _hip.stream_of(grad_output),
         ),
         "mednext_depthwise3d_dgrad",
@@ -134,7 +143,7 @@ def depthwise_weight_grad(
     if kernel_size not in SUPPORTED_KERNELS:
         raise ValueError(f"kernel_size must be one of {SUPPORTED_KERNELS}")
     n, c, d, h, w = (int(s) for s in x.shape)
-    tile_w, depth_chunk = _recipe_for(x, kernel_size, recipe)
+    engine, tile_w, depth_chunk = _recipe_for(x, kernel_size, recipe, "weight_grad")
     grad_weight = torch.empty((c, 1, kernel_size, kernel_size, kernel_size), device=x.device, dtype=x.dtype)
     grad_bias = torch.empty((c,), device=x.device, dtype=x.dtype)
     if x.numel() == 0:
@@ -142,7 +151,7 @@ def depthwise_weight_grad(
     code = _hip.dtype_code(x.dtype)
     lib = _hip.load()
     nbytes = lib.mednext_depthwise3d_wgrad_workspace_bytes(
-        n, c, d, h, w, kernel_size, code, tile_w, depth_chunk
+        n, c, d, h, w, kernel_size, code, engine, tile_w, depth_chunk
     )
     if nbytes == 0:
         raise _hip.HipLibraryError(f"wgrad workspace query failed: {_hip.last_error()}")
@@ -150,8 +159,8 @@ def depthwise_weight_grad(
     _hip.check(
         lib.mednext_depthwise3d_wgrad(
             x.data_ptr(), grad_output.data_ptr(), grad_weight.data_ptr(), grad_bias.data_ptr(),
-            workspace.data_ptr(), nbytes, n, c, d, h, w, kernel_size, code, tile_w, depth_chunk,
-            _hip.stream_of(x),
+            workspace.data_ptr(), nbytes, n, c, d, h, w, kernel_size, code, engine, tile_w,
+            depth_chunk, _hip.stream_of(x),
         ),
         "mednext_depthwise3d_wgrad",
     )

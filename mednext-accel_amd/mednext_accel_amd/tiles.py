@@ -40,7 +40,7 @@ class DepthwiseTile:
     lds_bytes: int
 
     def as_list(self) -> list[int]:
-        return [self.tile_w, self.depth_chunk]
+        return [ENGINE_VALU, self.tile_w, self.depth_chunk]
 
 
 def depthwise_plan(
@@ -83,27 +83,83 @@ def depthwise_plan(
     )
 
 
-def depthwise_recipe(
-    batch: int, channels: int, spatial: tuple[int, int, int], kernel_size: int
-) -> list[int]:
-    """Default ``[tile_w, depth_chunk]`` for fwd / dgrad / wgrad on gfx950.
+ENGINE_VALU = 0
+ENGINE_MFMA = 1
+MFMA_TILE_ROWS = 32  # two 16-row MFMA tiles per workgroup
+PHASES = ("forward", "input_grad", "weight_grad")
 
-    The tile is as wide as the plane allows (up to 64 columns, i.e. 128 bytes of
-    bf16 per row segment) and as tall as 256 threads reach. The D-run per
-    workgroup is the longest that still yields TARGET_WORKGROUPS workgroups, but
-    at least 4 planes per halo of k-1 so re-read halo planes stay below ~50%.
-    """
+
+def mfma_supported(spatial: tuple[int, int, int], kernel_size: int, phase: str) -> bool:
+    """Shapes the bf16 matrix-core kernels take (mirrors depthwise_mfma.hip)."""
     d, h, w = spatial
+    ok = kernel_size in (3, 5) and w % 8 == 0 and w >= 32 and h >= 32 and d * h * w * 2 < 2**31
+    if phase == "weight_grad":
+        ok = ok and w % 32 == 0
+    return ok
+
+
+def _depth_chunk(d: int, slabs: int, kernel_size: int, target: int = TARGET_WORKGROUPS) -> int:
+    wanted_chunks = _cdiv(target, max(1, slabs))
+    depth_chunk = max(1, _cdiv(d, wanted_chunks))
+    floor = min(d, max(4, 2 * (kernel_size - 1)))
+    return max(depth_chunk, floor)
+
+
+# Workgroups a matrix-core depthwise launch aims for, per (phase kind, k). The
+# forward / input-grad kernel holds two 16x(tile_w) accumulator rows per wave and
+# runs at 2 workgroups per CU (k=3) or 1 (k=5, larger LDS halo), so it wants
+# long D-runs and ~1-2 workgroups per CU; the weight-grad kernel is lighter and
+# prefers ~4 per CU. Measured on MI355X at the MedNeXt stage shapes
+# (C32 128^3, C64 64^3, C128 32^3; k=3 and 5): these targets reproduce the best
+# depth_chunk of a sweep over {4..64} within run-to-run noise.
+MFMA_TARGET_WORKGROUPS = {
+    ("stencil", 3): 2 * CU_COUNT,
+    ("stencil", 5): CU_COUNT,
+    ("weight_grad", 3): 4 * CU_COUNT,
+    ("weight_grad", 5): 2 * CU_COUNT,
+}
+MFMA_WGRAD_ROWS = 16
+
+
+def depthwise_recipe(
+    batch: int,
+    channels: int,
+    spatial: tuple[int, int, int],
+    kernel_size: int,
+    dtype: str = "float32",
+    phase: str = "forward",
+) -> list[int]:
+    """Default ``[engine, tile_w, depth_chunk]`` for one depthwise phase on gfx950.
+
+    bf16 shapes the matrix-core kernels take use them. Forward / input-grad:
+    ``tile_w = min(128, W)`` columns x 32 rows per workgroup. Weight-grad: full
+    rows of 64 columns (k=3) or up to 128 (k=5) x 16 rows. The D-run per
+    workgroup is the longest that still yields ``MFMA_TARGET_WORKGROUPS``.
+    Everything else runs the VALU stencil with the widest tile the plane allows
+    (up to 64 columns) and a D-run that yields TARGET_WORKGROUPS workgroups. In
+    both cases at least 4 planes (2(k-1) for k=5) per workgroup, so re-read
+    halo planes stay small.
+    """
+    if phase not in PHASES:
+        raise ValueError(f"phase must be one of {PHASES}")
+    d, h, w = spatial
+    if dtype == "bfloat16" and mfma_supported(spatial, kernel_size, phase):
+        if phase == "weight_grad":
+            cap = 64 if kernel_size == 3 else 128
+            rows, kind = MFMA_WGRAD_ROWS, "weight_grad"
+        else:
+            cap, rows, kind = 128, MFMA_TILE_ROWS, "stencil"
+        tile_w = 32
+        while tile_w < cap and tile_w * 2 <= w:
+            tile_w *= 2
+        slabs = batch * channels * _cdiv(h, rows) * _cdiv(w, tile_w)
+        target = MFMA_TARGET_WORKGROUPS[(kind, kernel_size)]
+        return [ENGINE_MFMA, tile_w, _depth_chunk(d, slabs, kernel_size, target)]
     tile_w = 4
     while tile_w < 64 and tile_w < w:
         tile_w *= 2
     plan = depthwise_plan(batch, channels, spatial, kernel_size, tile_w, d)
-    slabs = plan.workgroups  # workgroups with depth_chunk == D
-    wanted_chunks = _cdiv(TARGET_WORKGROUPS, max(1, slabs))
-    depth_chunk = max(1, _cdiv(d, wanted_chunks))
-    floor = min(d, max(4, 2 * (kernel_size - 1)))
-    depth_chunk = max(depth_chunk, floor)
-    return [tile_w, depth_chunk]
+    return [ENGINE_VALU, tile_w, _depth_chunk(d, plan.workgroups, kernel_size)]
 
 
 def group_norm_splits(batch: int, channels: int, spatial_volume: int) -> int:

@@ -50,10 +50,14 @@ def test_abi_version_and_error_slot():
     lib = _hip.load()
     assert lib.mednext_hip_abi_version() == _hip.ABI_VERSION
     # Invalid arguments are rejected before any device work.
-    status = lib.mednext_depthwise3d_fwd(None, None, None, None, 1, 1, 1, 1, 1, 3, 0, 64, 1, None)
+    status = lib.mednext_depthwise3d_fwd(None, None, None, None, 1, 1, 1, 1, 1, 3, 0, 0, 64, 1, None)
     assert status == 1
     assert "null tensor pointer" in _hip.last_error()
-    status = lib.mednext_depthwise3d_fwd(8, 8, None, 8, 1, 1, 1, 1, 1, 7, 0, 64, 1, None)
+    status = lib.mednext_depthwise3d_fwd(8, 8, None, 8, 1, 1, 1, 1, 1, 7, 0, 0, 64, 1, None)
     assert status == 1 and "kernel_size" in _hip.last_error()
-    assert lib.mednext_depthwise3d_wgrad_workspace_bytes(1, 32, 128, 128, 128, 3, 3, 64, 32) > 0
+    assert lib.mednext_depthwise3d_wgrad_workspace_bytes(1, 32, 128, 128, 128, 3, 3, 0, 64, 32) > 0
+    assert lib.mednext_depthwise3d_wgrad_workspace_bytes(1, 32, 128, 128, 128, 3, 3, 1, 64, 16) > 0
+    # MFMA engine rejects fp32 and W not a multiple of 32.
+    assert lib.mednext_depthwise3d_wgrad_workspace_bytes(1, 32, 128, 128, 128, 3, 0, 1, 64, 16) == 0
+    assert lib.mednext_depthwise3d_wgrad_workspace_bytes(1, 32, 128, 128, 40, 3, 3, 1, 64, 16) == 0
     assert lib.mednext_group_norm_workspace_bytes(1, 32, 128**3, 32) == 1 * 32 * 33 * 2 * 8

@@ -71,11 +71,11 @@ def test_golden_shape_all_dtypes(k, dtype):
 @pytest.mark.parametrize(
     "shape,recipe",
     [
-        ((1, 2, 9, 11, 13), [4, 2]),  # W not a multiple of 4 -> scalar path
-        ((2, 3, 3, 5, 8), [8, 1]),  # depth_chunk 1, tiny D
-        ((1, 1, 17, 33, 70), [64, 5]),  # ragged tiles in every direction
-        ((3, 2, 6, 2, 4), [4, 100]),  # depth_chunk > D
-        ((1, 4, 8, 8, 64), [16, 3]),
+        ((1, 2, 9, 11, 13), [0, 4, 2]),  # W not a multiple of 4 -> scalar path
+        ((2, 3, 3, 5, 8), [0, 8, 1]),  # depth_chunk 1, tiny D
+        ((1, 1, 17, 33, 70), [0, 64, 5]),  # ragged tiles in every direction
+        ((3, 2, 6, 2, 4), [0, 4, 100]),  # depth_chunk > D
+        ((1, 4, 8, 8, 64), [0, 16, 3]),
     ],
 )
 @pytest.mark.parametrize("k", [3, 5])
@@ -138,12 +138,48 @@ def test_cfg1_bf16_stage_shapes_against_torch(channels, size, k):
     assert max_rel(db, rdb) <= BF16
 
 
+@pytest.mark.parametrize(
+    "shape,fwd_recipe,dw_recipe",
+    [
+        ((1, 2, 9, 33, 40), [1, 64, 4], None),  # ragged H and W, forward/dgrad only
+        ((2, 3, 5, 32, 32), [1, 32, 2], [1, 32, 2]),
+        ((1, 2, 7, 35, 64), [1, 128, 3], [1, 64, 3]),  # tile wider than W, ragged H
+        ((1, 1, 19, 48, 96), [1, 32, 19], [1, 32, 100]),  # depth_chunk >= D
+        ((1, 2, 3, 64, 128), [1, 128, 1], [1, 64, 1]),  # depth_chunk 1
+    ],
+)
+@pytest.mark.parametrize("k", [3, 5])
+def test_mfma_engine_bf16_against_oracle(shape, fwd_recipe, dw_recipe, k):
+    print(f"[depthwise mfma] shape={shape} fwd={fwd_recipe} dw={dw_recipe} k={k}", flush=True)
+    gen = torch.Generator().manual_seed(k * 31 + shape[2])
+    x = torch.randn(shape, generator=gen).bfloat16()
+    w = (torch.randn(shape[1], 1, k, k, k, generator=gen) / k).bfloat16()
+    b = torch.randn(shape[1], generator=gen).bfloat16()
+    dy = torch.randn(shape, generator=gen).bfloat16()
+    xg, wg, bg, dyg = (t.to(DEV) for t in (x, w, b, dy))
+    y = hip_ops.depthwise_forward(xg, wg, bg, fwd_recipe)
+    dx = hip_ops.depthwise_input_grad(dyg, wg, fwd_recipe)
+    xn, wn, bn, dyn = (t.double().numpy() for t in (x, w, b, dy))
+    assert max_rel(y, odw.forward(xn, wn, bn)) <= BF16
+    assert max_rel(dx, odw.input_grad(dyn, wn)) <= BF16
+    # The MFMA path must agree with the fp32-accumulating VALU path to bf16 rounding.
+    y_valu = hip_ops.depthwise_forward(xg, wg, bg, [0, 32, 4])
+    assert max_rel(y, y_valu) <= 1e-2
+    if dw_recipe is not None:
+        dw, db = hip_ops.depthwise_weight_grad(xg, dyg, k, dw_recipe)
+        assert max_rel(dw, odw.weight_grad(xn, dyn, k)) <= BF16
+        assert max_rel(db, odw.bias_grad(dyn)) <= BF16
+
+
 def test_recipe_default_is_valid_for_stage_shapes():
     for channels, size in STAGES:
         for k in (3, 5):
-            tile_w, depth_chunk = depthwise_recipe(1, channels, (size,) * 3, k)
-            assert tile_w <= size or tile_w == 4
-            assert 1 <= depth_chunk <= size
+            for dtype in ("bfloat16", "float32"):
+                for phase in ("forward", "input_grad", "weight_grad"):
+                    engine, tile_w, depth_chunk = depthwise_recipe(1, channels, (size,) * 3, k, dtype, phase)
+                    assert engine in (0, 1)
+                    assert engine == 0 or dtype == "bfloat16"
+                    assert 1 <= depth_chunk <= size
 
 
 def test_deterministic_weight_grad():

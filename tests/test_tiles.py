@@ -1,0 +1,63 @@
+"""CDNA4 tile-recipe invariants (CPU only): valid launch parameters, LDS within
+budget, and enough workgroups to fill 256 CUs wherever the problem allows."""
+
+from __future__ import annotations
+
+import pytest
+
+from mednext_accel_amd import tiles
+
+STAGES = [(32, 128), (64, 64), (128, 32), (256, 16), (512, 8)]
+
+
+@pytest.mark.parametrize("channels,size", STAGES)
+@pytest.mark.parametrize("k", [3, 5])
+@pytest.mark.parametrize("dtype", ["bfloat16", "float32", "float16"])
+@pytest.mark.parametrize("phase", tiles.PHASES)
+def test_depthwise_recipe_invariants(channels, size, k, dtype, phase):
+    engine, tile_w, depth_chunk = tiles.depthwise_recipe(1, channels, (size,) * 3, k, dtype, phase)
+    assert 1 <= depth_chunk <= size
+    if engine == tiles.ENGINE_MFMA:
+        assert dtype == "bfloat16" and tiles.mfma_supported((size,) * 3, k, phase)
+        assert tile_w in (32, 64, 128) and tile_w <= max(32, size)
+        rows = tiles.MFMA_WGRAD_ROWS if phase == "weight_grad" else tiles.MFMA_TILE_ROWS
+        wgs = channels * -(-size // rows) * -(-size // tile_w) * -(-size // depth_chunk)
+        kind = "weight_grad" if phase == "weight_grad" else "stencil"
+        target = tiles.MFMA_TARGET_WORKGROUPS[(kind, k)]
+    else:
+        plan = tiles.depthwise_plan(1, channels, (size,) * 3, k, tile_w, depth_chunk)
+        assert plan.lds_bytes <= 64 * 1024
+        assert plan.threads <= tiles.MAX_THREADS
+        wgs = plan.workgroups
+        target = tiles.TARGET_WORKGROUPS
+    # Fill the chip unless the minimum D-run (halo bound) forbids it.
+    floor = min(size, max(4, 2 * (k - 1)))
+    assert wgs >= target or depth_chunk == floor
+
+
+def test_bf16_stage0_uses_matrix_cores():
+    for phase in tiles.PHASES:
+        assert tiles.depthwise_recipe(1, 32, (128,) * 3, 3, "bfloat16", phase)[0] == tiles.ENGINE_MFMA
+
+
+def test_mfma_requires_aligned_planes():
+    assert not tiles.mfma_supported((8, 8, 8), 3, "forward")
+    assert not tiles.mfma_supported((64, 64, 40), 3, "weight_grad")
+    assert tiles.mfma_supported((64, 64, 40), 3, "forward")
+    assert not tiles.mfma_supported((64, 64, 64), 1, "forward")
+
+
+@pytest.mark.parametrize("rows,volume", [(32, 128**3), (512, 8**3), (1, 10), (4096, 16**3)])
+def test_group_norm_splits(rows, volume):
+    splits = tiles.group_norm_splits(1, rows, volume)
+    assert 1 <= splits <= tiles.MAX_GN_SPLITS
+    assert splits == 1 or volume // splits >= 4096
+
+
+def test_mfma_stage0_recipes_match_measured_best():
+    """C32 128^3 bf16 (the headline shape): the sweep-best launch shapes."""
+    r = tiles.depthwise_recipe
+    assert r(1, 32, (128,) * 3, 3, "bfloat16", "forward") == [tiles.ENGINE_MFMA, 128, 32]
+    assert r(1, 32, (128,) * 3, 3, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 64, 64]
+    assert r(1, 32, (128,) * 3, 5, "bfloat16", "forward") == [tiles.ENGINE_MFMA, 128, 64]
+    assert r(1, 64, (64,) * 3, 3, "bfloat16", "input_grad") == [tiles.ENGINE_MFMA, 64, 16]
