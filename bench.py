@@ -46,6 +46,10 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--size", type=int, default=128)
     ap.add_argument("--kernel-size", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-train-step", action="store_true", help="skip the MedNeXt-Base training-step timing")
+    ap.add_argument("--train-steps", type=int, default=50)
+    ap.add_argument("--train-warmup", type=int, default=20)
+    ap.add_argument("--train-size", type=int, default=128)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     ap.add_argument(
         "--copy-calibration",
@@ -132,6 +136,43 @@ PHASE_KERNELS = {
     "input_grad": ("dw_mfma_stencil_kernel<3, true",),
     "weight_grad": ("dw_mfma_wgrad_kernel<3,", "dw_wgrad_finish_kernel<"),
 }
+
+
+def time_train_step(args, torch, optimization: str) -> dict:
+    """MedNeXt-Base (1 in, 3 classes, k3, deep supervision) training step at
+    1x1xS^3 in bf16 autocast with AdamW, the reference's step protocol
+    (benchmarks/implementations.py:133-190): event median over the timed steps."""
+    from mednext_accel_amd import mednext_base
+    from mednext_accel_amd.step import make_training_step
+
+    torch.manual_seed(1234)
+    model = mednext_base(in_channels=1, out_channels=3, kernel_size=3, deep_supervision=True, optimization=optimization)
+    model = model.cuda().train()
+    step = make_training_step(model, size=args.train_size, device="cuda")
+    for _ in range(args.train_warmup):
+        step()
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    events = []
+    wall0 = time.perf_counter()
+    for _ in range(args.train_steps):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        step()
+        end.record()
+        events.append((start, end))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    times = [a.elapsed_time(b) for a, b in events]
+    result = {
+        "median_step_ms": round(statistics.median(times), 3),
+        "mean_wall_step_ms": round(1000.0 * wall / max(1, args.train_steps), 3),
+        "peak_allocated_mib": round(torch.cuda.max_memory_allocated() / 2**20, 1),
+        "final_loss": round(float(step.last_loss.detach()), 5),
+    }
+    del step, model
+    torch.cuda.empty_cache()
+    return result
 
 
 def load_traffic(phase: str, kernel_size: int):
@@ -250,6 +291,20 @@ def main() -> int:
         },
         "roofline": roofline,
     }
+    if not args.no_train_step:
+        ours = time_train_step(args, torch, "auto")
+        eager = time_train_step(args, torch, "reference")
+        result["train_step"] = {
+            "model": (
+                f"MedNeXt-Base k3, 1x1x{args.train_size}^3, 5-head deep supervision, bf16 autocast, AdamW lr 1e-3, "
+                "random init, synthetic N(0,1) input and uniform labels (BASELINE configs[3])"
+            ),
+            "steps": args.train_steps,
+            "warmup": args.train_warmup,
+            "hip": ours,
+            "reference_eager": eager,
+            "speedup_vs_reference_eager": round(eager["median_step_ms"] / ours["median_step_ms"], 3),
+        }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, torch)
     print(json.dumps(result))

@@ -1,0 +1,430 @@
+"""Policy-driven module wrappers that keep the native modules' Parameters and keys.
+
+Mirrors the reference's selection hook (ops/adaptive.py:15-376):
+``install_adaptive_operators`` swaps eligible children in place for wrappers
+that hold the *same* ``Parameter`` objects, so ``parameters()`` and
+``state_dict()`` keys are unchanged; each wrapper resolves, per forward, which
+implementation runs from the execution context (phase, device, autocast dtype,
+shape) through a ``PolicyResolver``.
+
+Routes:
+  * ``AdaptiveDepthwise3d``: forward / dX / dW each resolve independently; any
+    HIP selection runs the ``mednext_accel_amd::depthwise_conv3d_odd_regular``
+    op with the per-phase launch recipes, with native PyTorch for phases that
+    resolve to ``reference``. Stride-2 and transposed depthwise convolutions run
+    natively.
+  * ``AdaptivePointwise3d``: ``pointwise_gemm_per_sample`` (the reference's
+    per-sample ``addmm`` route) or native ``F.conv3d``.
+  * ``AdaptiveGroupNorm3d`` (new; the reference has no GroupNorm hook): the HIP
+    GroupNorm(C, C) op or native ``F.group_norm``. Under autocast it returns
+    float32 like autocast's float32 ``group_norm``.
+
+Unsupported inputs (CPU tensors, evaluation, non-contiguous, ...) take the
+native PyTorch route, as in the reference. A HIP selection on a GPU never falls
+back: if the HIP library is missing the call raises.
+"""
+
+from __future__ import annotations
+
+import functools
+from dataclasses import dataclass
+
+import torch
+from torch import Tensor, nn
+from torch.nn import functional as F
+
+from .optimization.descriptors import ExecutionContext, OperatorDescriptor
+from .optimization.policy_resolver import PolicyDecision, PolicyResolver
+
+
+@dataclass(frozen=True, slots=True)
+class ModelOptimizationContext:
+    family: str
+    variant: str
+    checkpointing: str
+    allow_approximate: bool = False
+
+
+def _dtype_name(dtype: torch.dtype | str) -> str:
+    return str(dtype).removeprefix("torch.")
+
+
+def _query_device(index: int) -> tuple[tuple[int, int], int, str | None]:
+    props = torch.cuda.get_device_properties(index)
+    arch = getattr(props, "gcnArchName", None) if torch.version.hip else None
+    if arch:
+        arch = arch.split(":")[0]
+    return torch.cuda.get_device_capability(index), int(props.total_memory), arch or None
+
+
+_cached_device = functools.lru_cache(maxsize=None)(_query_device)
+
+
+def device_facts(index: int) -> tuple[tuple[int, int], int, str | None]:
+    """(capability, total memory, ISA name or None) of one GPU. Cached in eager
+    mode (queried once per device); queried directly while torch.compile traces."""
+    if torch.compiler.is_compiling():
+        return _query_device(index)
+    return _cached_device(index)
+
+
+def execution_context_for_shape(
+    model_context: ModelOptimizationContext,
+    *,
+    batch_size: int,
+    spatial_shape: tuple[int, ...],
+    dtype: torch.dtype | str,
+    device_type: str,
+    sm: tuple[int, int] | None,
+    total_vram_bytes: int,
+    training: bool = True,
+    export: bool = False,
+    arch: str | None = None,
+) -> ExecutionContext:
+    return ExecutionContext(
+        phase="export" if export else ("training" if training else "inference"),
+        device_type=device_type,
+        sm=sm,
+        total_vram_bytes=total_vram_bytes,
+        dtype=_dtype_name(dtype),
+        batch_size=batch_size,
+        spatial_shape=spatial_shape,
+        model_family=model_context.family,
+        variant=model_context.variant,
+        checkpointing=model_context.checkpointing,
+        export=export,
+        allow_approximate=model_context.allow_approximate,
+        arch=arch,
+    )
+
+
+def _effective_dtype(x: Tensor) -> torch.dtype:
+    device = x.device.type
+    if torch.is_autocast_enabled(device) and x.dtype != torch.float64:
+        return torch.get_autocast_dtype(device)
+    return x.dtype
+
+
+def _context_from_tensor(x: Tensor, model_context: ModelOptimizationContext, *, training: bool) -> ExecutionContext:
+    export = torch.jit.is_tracing() or torch.onnx.is_in_onnx_export()
+    sm, vram, arch = None, 0, None
+    if x.device.type == "cuda" and not export:
+        sm, vram, arch = device_facts(x.device.index if x.device.index is not None else torch.cuda.current_device())
+    return execution_context_for_shape(
+        model_context,
+        batch_size=1 if x.ndim == 4 else int(x.shape[0]),
+        spatial_shape=tuple(int(s) for s in x.shape[-3:]),
+        dtype=_effective_dtype(x),
+        device_type=x.device.type,
+        sm=sm,
+        total_vram_bytes=vram,
+        training=training,
+        export=export,
+        arch=arch,
+    )
+
+
+def _conv_descriptor(conv: nn.Module, *, role: str | None) -> OperatorDescriptor:
+    """Family naming as in the reference (ops/adaptive.py:80-109)."""
+    transpose = isinstance(conv, (nn.ConvTranspose2d, nn.ConvTranspose3d))
+    dims = len(conv.kernel_size)
+    depthwise = conv.groups == conv.in_channels == conv.out_channels
+    if depthwise:
+        family = "depthwise_conv_transpose" if transpose else "depthwise_conv"
+    elif transpose:
+        family = "conv_transpose"
+    elif conv.kernel_size == (1,) * dims and conv.groups == 1:
+        family = "pointwise_conv"
+    else:
+        family = "conv"
+    direction = "transpose" if transpose else ("downsample" if conv.stride[0] == 2 else "regular")
+    return OperatorDescriptor.convolution(
+        family=f"{family}{dims}d",
+        direction=direction,
+        in_channels=conv.in_channels,
+        out_channels=conv.out_channels,
+        kernel_size=conv.kernel_size,
+        stride=conv.stride,
+        padding=conv.padding,
+        dilation=conv.dilation,
+        groups=conv.groups,
+        role=role,
+    )
+
+
+def _norm_descriptor(norm: nn.GroupNorm, *, role: str | None = None) -> OperatorDescriptor:
+    return OperatorDescriptor.normalization(family="group_norm3d", channels=norm.num_channels, role=role)
+
+
+def _hip_ops():
+    from . import hip_ops  # loads libmednext_hip.so; raises if it is missing
+
+    return hip_ops
+
+
+class _AdaptiveModule(nn.Module):
+    resolver: PolicyResolver
+    model_context: ModelOptimizationContext
+    descriptor: OperatorDescriptor
+
+    def _warn_for_device(self) -> None:
+        reference = self.weight if getattr(self, "weight", None) is not None else getattr(self, "bias", None)
+        if reference is not None and reference.device.type == "cuda":
+            sm, _, arch = device_facts(reference.device.index or 0)
+            if arch is not None:
+                self.resolver.warn_for_target("amd", arch)
+            else:
+                self.resolver.warn_for_sm(sm)
+
+    def _apply(self, fn, recurse=True):
+        result = super()._apply(fn, recurse=recurse)
+        self._warn_for_device()
+        return result
+
+    def decision_for_shape(
+        self,
+        *,
+        batch_size: int,
+        spatial_shape: tuple[int, int, int],
+        dtype: torch.dtype | str,
+        device_type: str,
+        sm: tuple[int, int] | None,
+        total_vram_bytes: int,
+        arch: str | None = None,
+        phase: str | None = None,
+    ) -> PolicyDecision:
+        context = execution_context_for_shape(
+            self.model_context,
+            batch_size=batch_size,
+            spatial_shape=spatial_shape,
+            dtype=dtype,
+            device_type=device_type,
+            sm=sm,
+            total_vram_bytes=total_vram_bytes,
+            training=self.training,
+            arch=arch,
+        )
+        return self.resolver.resolve(self.descriptor, context, phase or context.phase)
+
+
+class AdaptivePointwise3d(_AdaptiveModule):
+    _mednext_accel_backend_kind = "pointwise_gemm"
+
+    def __init__(
+        self,
+        conv: nn.Conv3d,
+        resolver: PolicyResolver,
+        model_context: ModelOptimizationContext,
+        *,
+        role: str | None = None,
+    ) -> None:
+        super().__init__()
+        self.weight = conv.weight
+        self.bias = conv.bias
+        for name in ("in_channels", "out_channels", "kernel_size", "stride", "padding", "dilation", "groups"):
+            setattr(self, name, getattr(conv, name))
+        self.descriptor = _conv_descriptor(conv, role=role)
+        self.resolver = resolver
+        self.model_context = model_context
+        self.train(conv.training)
+        self._warn_for_device()
+
+    def _gemm(self, x: Tensor) -> Tensor:
+        """Per-sample ``W @ X[n] + b`` (reference ops/adaptive.py:174-188)."""
+        squeeze = x.ndim == 4
+        if squeeze:
+            x = x.unsqueeze(0)
+        spatial = x.shape[2:]
+        weight = self.weight.reshape(self.out_channels, self.in_channels)
+        rows = []
+        for sample in x.reshape(x.shape[0], self.in_channels, -1).unbind(0):
+            rows.append(torch.mm(weight, sample) if self.bias is None else torch.addmm(self.bias[:, None], weight, sample))
+        out = torch.stack(rows).reshape(x.shape[0], self.out_channels, *spatial)
+        return out.squeeze(0) if squeeze else out
+
+    def forward(self, x: Tensor) -> Tensor:
+        context = _context_from_tensor(x, self.model_context, training=self.training)
+        decision = self.resolver.resolve(self.descriptor, context, context.phase)
+        if (
+            decision.implementation == "pointwise_gemm_per_sample"
+            and torch.is_grad_enabled()
+            and x.ndim == 5
+            and x.is_contiguous()
+        ):
+            return self._gemm(x)
+        return F.conv3d(x, self.weight, self.bias)
+
+
+class AdaptiveDepthwise3d(_AdaptiveModule):
+    _mednext_accel_backend_kind = "depthwise"
+
+    def __init__(
+        self,
+        conv: nn.Conv3d | nn.ConvTranspose3d,
+        resolver: PolicyResolver,
+        model_context: ModelOptimizationContext,
+        *,
+        role: str | None = None,
+    ) -> None:
+        super().__init__()
+        self.weight = conv.weight
+        self.bias = conv.bias
+        for name in ("in_channels", "out_channels", "kernel_size", "stride", "padding", "dilation", "groups"):
+            setattr(self, name, getattr(conv, name))
+        self.output_padding = getattr(conv, "output_padding", (0, 0, 0))
+        self.transpose = isinstance(conv, nn.ConvTranspose3d)
+        self.descriptor = _conv_descriptor(conv, role=role)
+        self.resolver = resolver
+        self.model_context = model_context
+        self.train(conv.training)
+        self._warn_for_device()
+
+    def _reference(self, x: Tensor) -> Tensor:
+        if self.transpose:
+            return F.conv_transpose3d(
+                x, self.weight, self.bias, self.stride, self.padding, self.output_padding, self.groups, self.dilation
+            )
+        return F.conv3d(x, self.weight, self.bias, self.stride, self.padding, self.dilation, self.groups)
+
+    def phase_decisions(self, context: ExecutionContext) -> tuple[PolicyDecision, PolicyDecision, PolicyDecision]:
+        return tuple(self.resolver.resolve(self.descriptor, context, p) for p in ("forward", "backward_input", "backward_weight"))
+
+    def forward(self, x: Tensor) -> Tensor:
+        context = _context_from_tensor(x, self.model_context, training=self.training)
+        if (
+            context.phase != "training"
+            or context.device_type != "cuda"
+            or not torch.is_grad_enabled()
+            or x.ndim != 5
+            or self.transpose
+            or self.stride != (1, 1, 1)
+            or self.output_padding != (0, 0, 0)
+            or not x.is_contiguous()
+        ):
+            return self._reference(x)
+        fwd, dx, dw = self.phase_decisions(context)
+        custom = [d.implementation != "reference" for d in (fwd, dx, dw)]
+        if not any(custom):
+            return self._reference(x)
+        hip_ops = _hip_ops()
+        dtype = getattr(torch, context.dtype)
+        x = x.to(dtype)
+        weight = self.weight.to(dtype)
+        bias = self.bias.to(dtype) if self.bias is not None else None
+
+        def recipe(decision: PolicyDecision) -> list[int]:
+            p = decision.parameters
+            return [int(p.get("engine", 0)), int(p.get("tile_w", 0)), int(p.get("depth_chunk", 0))] if p else []
+
+        return hip_ops.depthwise_conv3d_regular(
+            x, weight, bias, self.kernel_size[0], recipe(fwd), recipe(dx), recipe(dw), *custom
+        )
+
+
+class AdaptiveGroupNorm3d(_AdaptiveModule):
+    """GroupNorm with groups == channels over 5-D inputs (MedNeXt's ``norm``)."""
+
+    _mednext_accel_backend_kind = "group_norm"
+
+    def __init__(
+        self,
+        norm: nn.GroupNorm,
+        resolver: PolicyResolver,
+        model_context: ModelOptimizationContext,
+        *,
+        role: str | None = None,
+    ) -> None:
+        super().__init__()
+        self.weight = norm.weight
+        self.bias = norm.bias
+        self.num_groups = norm.num_groups
+        self.num_channels = norm.num_channels
+        self.eps = norm.eps
+        self.affine = norm.affine
+        self.descriptor = _norm_descriptor(norm, role=role)
+        self.resolver = resolver
+        self.model_context = model_context
+        self.train(norm.training)
+        self._warn_for_device()
+
+    def _reference(self, x: Tensor) -> Tensor:
+        return F.group_norm(x, self.num_groups, self.weight, self.bias, self.eps)
+
+    def forward(self, x: Tensor) -> Tensor:
+        if x.ndim != 5 or not x.is_contiguous() or not torch.is_grad_enabled():
+            return self._reference(x)
+        context = _context_from_tensor(x, self.model_context, training=self.training)
+        decision = self.resolver.resolve(self.descriptor, context, context.phase)
+        if decision.implementation != "hip_group_norm":
+            return self._reference(x)
+        hip_ops = _hip_ops()
+        autocast = torch.is_autocast_enabled(x.device.type) and x.dtype != torch.float64
+        # Autocast runs group_norm in float32 (input cast up, float32 result);
+        # the kernel reads the low-precision input directly, which is exact.
+        out_dtype = torch.float32 if autocast else None
+        weight, bias = self.weight, self.bias
+        if autocast:
+            weight = weight.float() if weight is not None else None
+            bias = bias.float() if bias is not None else None
+        y, _mean, _rstd = hip_ops.group_norm_channels(x, weight, bias, self.eps, out_dtype)
+        return y
+
+    def extra_repr(self) -> str:
+        return f"{self.num_groups}, {self.num_channels}, eps={self.eps}, affine={self.affine}"
+
+
+def _pointwise_eligible(module: nn.Module) -> bool:
+    return (
+        type(module) is nn.Conv3d
+        and module.kernel_size == (1, 1, 1)
+        and module.stride == (1, 1, 1)
+        and module.padding == (0, 0, 0)
+        and module.dilation == (1, 1, 1)
+        and module.groups == 1
+        and module.padding_mode == "zeros"
+    )
+
+
+def _depthwise_eligible(module: nn.Module) -> bool:
+    if type(module) not in (nn.Conv3d, nn.ConvTranspose3d):
+        return False
+    k = module.kernel_size[0]
+    return (
+        len(set(module.kernel_size)) == 1
+        and k % 2 == 1
+        and module.in_channels == module.out_channels == module.groups
+        and module.stride in ((1, 1, 1), (2, 2, 2))
+        and module.padding == (k // 2,) * 3
+        and module.dilation == (1, 1, 1)
+        and getattr(module, "padding_mode", "zeros") == "zeros"
+        and getattr(module, "output_padding", (0, 0, 0)) == (0, 0, 0)
+    )
+
+
+def _group_norm_eligible(module: nn.Module) -> bool:
+    return type(module) is nn.GroupNorm and module.num_groups == module.num_channels
+
+
+def install_adaptive_operators(
+    model: nn.Module,
+    *,
+    resolver: PolicyResolver,
+    model_context: ModelOptimizationContext,
+    _prefix: str = "",
+) -> int:
+    """Swap eligible children for wrappers in place; returns how many were swapped."""
+    count = 0
+    for name, child in list(model.named_children()):
+        role = f"{_prefix}.{name}" if _prefix else name
+        if _pointwise_eligible(child):
+            wrapper: nn.Module = AdaptivePointwise3d(child, resolver, model_context, role=role)
+        elif _depthwise_eligible(child):
+            wrapper = AdaptiveDepthwise3d(child, resolver, model_context, role=role)
+        elif _group_norm_eligible(child):
+            wrapper = AdaptiveGroupNorm3d(child, resolver, model_context, role=role)
+        else:
+            count += install_adaptive_operators(child, resolver=resolver, model_context=model_context, _prefix=role)
+            continue
+        setattr(model, name, wrapper)
+        count += 1
+    return count
