@@ -50,6 +50,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--train-steps", type=int, default=50)
     ap.add_argument("--train-warmup", type=int, default=20)
     ap.add_argument("--train-size", type=int, default=128)
+    ap.add_argument("--no-eager-step", action="store_true", help="time only the HIP-backed training step")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     ap.add_argument(
         "--copy-calibration",
@@ -136,6 +137,30 @@ PHASE_KERNELS = {
     "input_grad": ("dw_mfma_stencil_kernel<3, true",),
     "weight_grad": ("dw_mfma_wgrad_kernel<3,", "dw_wgrad_finish_kernel<"),
 }
+
+
+def time_copy_ceiling(torch) -> dict:
+    """Attainable streaming rate on this GPU: torch.neg over 2^27 bf16 elements
+    (256 MiB read + 256 MiB written), median of 20 event-timed launches over
+    two rotating buffer pairs (1 GiB in total, above the 256 MiB Infinity Cache)."""
+    n = 2**27
+    pairs = [(torch.randn(n, device="cuda").bfloat16(), torch.empty(n, device="cuda", dtype=torch.bfloat16)) for _ in range(2)]
+    for i in range(4):
+        torch.neg(pairs[i % 2][0], out=pairs[i % 2][1])
+    torch.cuda.synchronize()
+    events = []
+    for i in range(20):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        torch.neg(pairs[i % 2][0], out=pairs[i % 2][1])
+        b.record()
+        events.append((a, b))
+    torch.cuda.synchronize()
+    ms = statistics.median(a.elapsed_time(b) for a, b in events)
+    del pairs
+    torch.cuda.empty_cache()
+    return {"kernel": "torch.neg, 2^27 bf16 (512 MiB moved)", "us": round(ms * 1000, 2),
+            "gbs": round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)}
 
 
 def time_train_step(args, torch, optimization: str) -> dict:
@@ -247,6 +272,7 @@ def main() -> int:
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
     dw = time_depthwise(args, torch, hip_ops)
+    ceiling = time_copy_ceiling(torch)
     phase_us = {name: round(1000.0 * ms, 2) for name, ms in dw["mean_ms"].items()}
     dominant = max(dw["mean_ms"], key=dw["mean_ms"].get)
     achieved = dw["bytes_per_phase"] / (dw["mean_ms"][dominant] * 1e-3) / 1e9
@@ -263,6 +289,8 @@ def main() -> int:
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
         "traffic": load_traffic(dominant, args.kernel_size) if (args.channels, args.size) == (32, 128) else None,
+        "copy_ceiling_gbs": ceiling["gbs"],
+        "frac_of_copy_ceiling": round(achieved / ceiling["gbs"], 4),
         "algorithmic_bytes_per_launch": dw["bytes_per_phase"],
     }
     result = {
@@ -288,12 +316,13 @@ def main() -> int:
             "phase_us": phase_us,
             "phase_median_us": {k: round(v, 2) for k, v in dw["median_us"].items()},
             "wall_ms_per_step": round(dw["wall_ms_per_step"], 4),
+            "copy_ceiling": ceiling,
         },
         "roofline": roofline,
     }
     if not args.no_train_step:
         ours = time_train_step(args, torch, "auto")
-        eager = time_train_step(args, torch, "reference")
+        eager = None if args.no_eager_step else time_train_step(args, torch, "reference")
         result["train_step"] = {
             "model": (
                 f"MedNeXt-Base k3, 1x1x{args.train_size}^3, 5-head deep supervision, bf16 autocast, AdamW lr 1e-3, "
@@ -303,7 +332,7 @@ def main() -> int:
             "warmup": args.train_warmup,
             "hip": ours,
             "reference_eager": eager,
-            "speedup_vs_reference_eager": round(eager["median_step_ms"] / ours["median_step_ms"], 3),
+            "speedup_vs_reference_eager": round(eager["median_step_ms"] / ours["median_step_ms"], 3) if eager else None,
         }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, torch)
