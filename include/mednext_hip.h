@@ -126,6 +126,55 @@ int32_t mednext_group_norm_bwd(const void* grad_output, int32_t dy_dtype, const 
                                int64_t spatial, int32_t splits, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------ pointwise
+ * 1x1x1 convolution as a per-sample GEMM on bf16 matrix cores (fp32
+ * accumulate): x [N][K][V], y [N][M][V] (V = D*H*W voxels), weight [M][K]
+ * (weight_layout 0) or [K][M] (weight_layout 1, i.e. the transposed product
+ * for the input gradient: grad_x = W^T . grad_y with W the conv's [M][K]).
+ * Requirements: bf16, K % 32 == 0, K <= 512, M % 16 == 0, V % 8 == 0, one
+ * sample's x and y each < 2 GiB, 16-byte aligned pointers.
+ * Prologue, applied to every x element as loaded:
+ *   MEDNEXT_PW_PROLOGUE_GELU: x -> GELU(x) (exact erf form).
+ * Epilogue, applied to each accumulator y[n][m][v] (bias may be NULL):
+ *   BIAS:          y = acc + bias[m]
+ *   BIAS_GELU:     y = GELU(acc + bias[m])
+ *   BIAS_RESIDUAL: y = acc + bias[m] + aux[n][m][v]
+ *   GELU_GRAD:     y = acc * GELU'(aux[n][m][v])   (bias unused)
+ */
+enum mednext_pw_prologue { MEDNEXT_PW_PROLOGUE_NONE = 0, MEDNEXT_PW_PROLOGUE_GELU = 1 };
+enum mednext_pw_epilogue {
+  MEDNEXT_PW_EPILOGUE_BIAS = 0,
+  MEDNEXT_PW_EPILOGUE_BIAS_GELU = 1,
+  MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL = 2,
+  MEDNEXT_PW_EPILOGUE_GELU_GRAD = 3
+};
+
+/* y = epilogue(op(W) . prologue(x)); blocks_per_sample = workgroups along V
+ * per (sample, 64-row output block), from the gfx950 tile policy.
+ * Replaces the forward of AdaptivePointwise3d (reference
+ * src/mednext_accel/ops/adaptive.py:174-200: per-sample addmm / F.conv3d) and,
+ * with the epilogues, the GELU (models/blocks.py:39-41) and residual add
+ * (blocks.py:89-90) around it; with weight_layout 1 it is the conv's input
+ * gradient (the backward of the same addmm). */
+int32_t mednext_pointwise_fwd(const void* x, const void* weight, const void* bias, const void* aux,
+                              void* y, int64_t n, int64_t k, int64_t m, int64_t v,
+                              int32_t weight_layout, int32_t prologue, int32_t epilogue,
+                              int32_t dtype, int32_t blocks_per_sample, void* stream);
+
+/* fp32 bytes of per-split partials the weight-gradient launch needs. */
+size_t mednext_pointwise_wgrad_workspace_bytes(int64_t n, int64_t k, int64_t m, int64_t v,
+                                               int32_t splits);
+
+/* grad_weight[M][K] = sum_{n,v} grad_output[n][m][v] * prologue(x[n][k][v]);
+ * grad_bias[m] = sum_{n,v} grad_output[n][m][v] (skipped when NULL). Both bf16;
+ * fixed-order reduction (bit-reproducible). splits = workgroups per sample
+ * along V. Replaces the weight/bias gradient of the reference's pointwise
+ * conv (adaptive.py:174-200, autograd of addmm / conv3d). */
+int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* grad_weight,
+                                void* grad_bias, void* workspace, size_t workspace_bytes,
+                                int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
+                                int32_t dtype, int32_t splits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,18 +20,13 @@
 // The compiler waits only for the set being stored. PD divides k so every
 // register-set index is static under the k-fold unroll.
 //
-// Lane layout of v_mfma_f32_16x16x32_bf16 (verified on gfx950): lane l holds
-// A[l%16][8*(l/16) + j], B[8*(l/16) + j][l%16] (j = 0..7) and
-// C[4*(l/16) + r][l%16] (r = 0..3).
+// Buffer helpers and the MFMA lane layout: cdna4.h.
+#include "cdna4.h"
 #include "common.h"
 #include "depthwise_mfma.h"
 
 namespace mednext {
 namespace {
-
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kRT = 2;  // 16-row tiles per workgroup plane (32 rows)
@@ -63,35 +58,6 @@ __device__ inline BlockPos block_pos(const MGeom& g) {
 }
 
 __device__ inline uint4 lds_read16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-
-// Raw buffer access to one (n, c) slab. An offset at or past the slab size
-// (kOob) reads zeros / drops the store in hardware, so halo padding and
-// masking need no branches (and the waitcnt pass sees straight-line code).
-typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
-constexpr uint32_t kOob = 0x80000000u;
-
-__device__ inline __amdgpu_buffer_rsrc_t slab_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
-                                           0x00020000);
-}
-__device__ inline uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-// Streaming load: cache policy 2 sets the non-temporal bit (data read once is
-// not kept in the caches). Non-temporal stores measured ~40% slower here.
-__device__ inline uint4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2);
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-__device__ inline uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-__device__ inline void buf_store8(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t lo, uint32_t hi) {
-  const u32x2_t v = {lo, hi};
-  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0);
-}
 
 // ------------------------------------------------------------------ stencil
 

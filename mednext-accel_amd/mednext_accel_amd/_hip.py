@@ -55,9 +55,18 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _i32, _p, _i32, _p, _p, _p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _p, c_size_t, _p),
     ),
+    "mednext_pointwise_fwd": (
+        _i32,
+        (_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
+    ),
+    "mednext_pointwise_wgrad_workspace_bytes": (c_size_t, (_i64, _i64, _i64, _i64, _i32)),
+    "mednext_pointwise_wgrad": (
+        _i32,
+        (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p),
+    ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

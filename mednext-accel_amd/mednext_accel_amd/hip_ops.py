@@ -21,7 +21,14 @@ import torch
 from torch import Tensor
 
 from . import _hip
-from .tiles import ENGINE_MFMA, ENGINE_VALU, depthwise_recipe, group_norm_splits
+from .tiles import (
+    ENGINE_MFMA,
+    ENGINE_VALU,
+    depthwise_recipe,
+    group_norm_splits,
+    pointwise_blocks,
+    pointwise_wgrad_splits,
+)
 
 SUPPORTED_KERNELS = (1, 3, 5)
 
@@ -253,6 +260,109 @@ def group_norm_backward(
     return dx, dgamma, dbeta
 
 
+# --------------------------------------------------------------------- pointwise
+
+PW_PROLOGUE_NONE, PW_PROLOGUE_GELU = 0, 1
+PW_EPILOGUE_BIAS, PW_EPILOGUE_BIAS_GELU, PW_EPILOGUE_BIAS_RESIDUAL, PW_EPILOGUE_GELU_GRAD = 0, 1, 2, 3
+
+
+def _weight2d(weight: Tensor) -> Tensor:
+    if weight.ndim not in (2, 5) or (weight.ndim == 5 and tuple(weight.shape[2:]) != (1, 1, 1)):
+        raise ValueError("pointwise weight must be [Cout, Cin] or [Cout, Cin, 1, 1, 1]")
+    return weight.reshape(weight.shape[0], weight.shape[1])
+
+
+def _check_pointwise_tensor(t: Tensor, name: str) -> None:
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{name} must be bfloat16")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if t.ndim < 3:
+        raise ValueError(f"{name} must be [N, C, *spatial]")
+
+
+def pointwise_conv(
+    x: Tensor,
+    weight: Tensor,
+    bias: Tensor | None = None,
+    *,
+    aux: Tensor | None = None,
+    prologue: int = PW_PROLOGUE_NONE,
+    epilogue: int = PW_EPILOGUE_BIAS,
+    transpose: bool = False,
+    blocks: int | None = None,
+) -> Tensor:
+    """``y = epilogue(W . prologue(x) [+ b])`` per sample on the matrix cores.
+
+    ``weight`` is the conv's [Cout, Cin(, 1, 1, 1)]; with ``transpose=True`` the
+    product is ``W^T . x`` (the conv's input gradient). ``aux`` is the residual
+    (BIAS_RESIDUAL) or the GELU pre-activation (GELU_GRAD), shaped like ``y``.
+    """
+    _check_device(x, weight)
+    _check_pointwise_tensor(x, "x")
+    w2 = _weight2d(weight)
+    if w2.dtype != torch.bfloat16:
+        raise ValueError("weight must be bfloat16")
+    w2 = w2.contiguous()
+    k, m = (w2.shape[0], w2.shape[1]) if transpose else (w2.shape[1], w2.shape[0])
+    if x.shape[1] != k:
+        raise ValueError(f"x has {x.shape[1]} channels, the weight expects {k}")
+    n, v = x.shape[0], x[0, 0].numel()
+    y = x.new_empty((n, m, *x.shape[2:]))
+    if bias is not None:
+        if bias.shape != (m,) or bias.dtype != torch.bfloat16:
+            raise ValueError("bias must be a bfloat16 [Cout] tensor")
+        bias = bias.contiguous()
+    if aux is not None:
+        _check_pointwise_tensor(aux, "aux")
+        if aux.shape != y.shape:
+            raise ValueError("aux must have the output's shape")
+    if blocks is None:
+        blocks = pointwise_blocks(n, k, m, v)
+    lib = _hip.load()
+    _hip.check(
+        lib.mednext_pointwise_fwd(
+            x.data_ptr(), w2.data_ptr(), _hip.ptr(bias), _hip.ptr(aux), y.data_ptr(),
+            n, k, m, v, 1 if transpose else 0, prologue, epilogue, _hip.DTYPE_CODES[torch.bfloat16],
+            int(blocks), _hip.stream_of(x),
+        ),
+        "mednext_pointwise_fwd",
+    )
+    return y
+
+
+def pointwise_weight_grad(
+    grad_output: Tensor,
+    x: Tensor,
+    *,
+    prologue: int = PW_PROLOGUE_NONE,
+    with_bias: bool = True,
+    splits: int | None = None,
+) -> tuple[Tensor, Tensor | None]:
+    """(dW [Cout, Cin, 1, 1, 1], dB [Cout] or None) of ``y = W . prologue(x) + b``."""
+    _check_device(grad_output, x)
+    _check_pointwise_tensor(grad_output, "grad_output")
+    _check_pointwise_tensor(x, "x")
+    if grad_output.shape[0] != x.shape[0] or grad_output.shape[2:] != x.shape[2:]:
+        raise ValueError("grad_output and x must share batch and spatial shape")
+    n, k, m, v = x.shape[0], x.shape[1], grad_output.shape[1], x[0, 0].numel()
+    if splits is None:
+        splits = pointwise_wgrad_splits(n, k, m, v)
+    lib = _hip.load()
+    nbytes = lib.mednext_pointwise_wgrad_workspace_bytes(n, k, m, v, int(splits))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+    dw = x.new_empty((m, k, 1, 1, 1))
+    db = x.new_empty((m,)) if with_bias else None
+    _hip.check(
+        lib.mednext_pointwise_wgrad(
+            grad_output.data_ptr(), x.data_ptr(), dw.data_ptr(), _hip.ptr(db), ws.data_ptr(), nbytes,
+            n, k, m, v, prologue, _hip.DTYPE_CODES[torch.bfloat16], int(splits), _hip.stream_of(x),
+        ),
+        "mednext_pointwise_wgrad",
+    )
+    return dw, db
+
+
 # ------------------------------------------------------------------------ custom ops
 
 
@@ -421,3 +531,139 @@ def _group_norm_backward(ctx, grad_y, _grad_mean, _grad_rstd):
 
 
 group_norm_channels.register_autograd(_group_norm_backward, setup_context=_setup_group_norm)
+
+
+# ---------------------------------------------------------- pointwise custom ops
+
+
+@torch.library.custom_op("mednext_accel_amd::pointwise_input_grad", mutates_args=())
+def pointwise_input_grad_op(grad_output: Tensor, weight: Tensor) -> Tensor:
+    """dX = W^T . dY of a 1x1x1 conv (bf16)."""
+    return pointwise_conv(grad_output.contiguous(), weight, transpose=True)
+
+
+@pointwise_input_grad_op.register_fake
+def _(grad_output, weight):
+    return grad_output.new_empty((grad_output.shape[0], weight.shape[1], *grad_output.shape[2:]))
+
+
+@torch.library.custom_op("mednext_accel_amd::pointwise_weight_grad", mutates_args=())
+def pointwise_weight_grad_op(grad_output: Tensor, x: Tensor, gelu_input: bool) -> tuple[Tensor, Tensor]:
+    """(dW, dB) of ``y = W . act(x) + b`` with act = GELU when ``gelu_input``."""
+    prologue = PW_PROLOGUE_GELU if gelu_input else PW_PROLOGUE_NONE
+    dw, db = pointwise_weight_grad(grad_output.contiguous(), x.contiguous(), prologue=prologue, with_bias=True)
+    return dw, db
+
+
+@pointwise_weight_grad_op.register_fake
+def _(grad_output, x, gelu_input):
+    m, k = grad_output.shape[1], x.shape[1]
+    return x.new_empty((m, k, 1, 1, 1)), x.new_empty((m,))
+
+
+@torch.library.custom_op("mednext_accel_amd::pointwise_conv3d", mutates_args=())
+def pointwise_conv3d(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+    """1x1x1 Conv3d (bf16) on the matrix cores: the GEMM route of the reference's
+    AdaptivePointwise3d (ops/adaptive.py:174-200)."""
+    return pointwise_conv(x.contiguous(), weight, bias)
+
+
+@pointwise_conv3d.register_fake
+def _(x, weight, bias):
+    return x.new_empty((x.shape[0], weight.shape[0], *x.shape[2:]))
+
+
+def _setup_pointwise(ctx, inputs, output):
+    x, weight, bias = inputs
+    ctx.save_for_backward(x, weight)
+    ctx.has_bias = bias is not None
+
+
+def _pointwise_backward(ctx, grad_output):
+    x, weight = ctx.saved_tensors
+    need_x, need_w, need_b = ctx.needs_input_grad
+    grad_output = grad_output.contiguous()
+    dx = pointwise_input_grad_op(grad_output, weight) if need_x else None
+    dw = db = None
+    if need_w or (need_b and ctx.has_bias):
+        dw, db = pointwise_weight_grad_op(grad_output, x, False)
+    return dx, dw if need_w else None, db if (need_b and ctx.has_bias) else None
+
+
+pointwise_conv3d.register_autograd(_pointwise_backward, setup_context=_setup_pointwise)
+
+
+@torch.library.custom_op("mednext_accel_amd::mlp_expansion", mutates_args=())
+def mlp_expansion(
+    x: Tensor, w1: Tensor, b1: Tensor | None, w2: Tensor, b2: Tensor | None, residual: Tensor | None
+) -> tuple[Tensor, Tensor]:
+    """MedNeXt block expansion, fused: ``out = W2 . GELU(W1 . x + b1) + b2 (+ residual)``
+    (reference models/blocks.py:79-80 and the residual add :89-90).
+
+    Returns ``(out, h)`` with ``h = W1 . x + b1`` the pre-activation the
+    backward needs; GELU(h) is recomputed inside the project GEMM instead of
+    being stored."""
+    x = x.contiguous()
+    h = pointwise_conv(x, w1, b1, epilogue=PW_EPILOGUE_BIAS)
+    if residual is None:
+        out = pointwise_conv(h, w2, b2, prologue=PW_PROLOGUE_GELU, epilogue=PW_EPILOGUE_BIAS)
+    else:
+        out = pointwise_conv(
+            h, w2, b2, aux=residual.contiguous(), prologue=PW_PROLOGUE_GELU, epilogue=PW_EPILOGUE_BIAS_RESIDUAL
+        )
+    return out, h
+
+
+@mlp_expansion.register_fake
+def _(x, w1, b1, w2, b2, residual):
+    h = x.new_empty((x.shape[0], w1.shape[0], *x.shape[2:]))
+    return x.new_empty((x.shape[0], w2.shape[0], *x.shape[2:])), h
+
+
+@torch.library.custom_op("mednext_accel_amd::mlp_expansion_backward", mutates_args=())
+def mlp_expansion_backward(
+    grad_out: Tensor, x: Tensor, h: Tensor, w1: Tensor, w2: Tensor
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dx, dW1, db1, dW2, db2) of ``mlp_expansion``:
+    dh = (W2^T . dout) * GELU'(h); dW2 = dout . GELU(h)^T; dW1 = dh . x^T; dx = W1^T . dh."""
+    grad_out = grad_out.contiguous()
+    dh = pointwise_conv(grad_out, w2, aux=h, epilogue=PW_EPILOGUE_GELU_GRAD, transpose=True)
+    dw2, db2 = pointwise_weight_grad(grad_out, h, prologue=PW_PROLOGUE_GELU)
+    dw1, db1 = pointwise_weight_grad(dh, x.contiguous())
+    dx = pointwise_conv(dh, w1, transpose=True)
+    return dx, dw1, db1, dw2, db2
+
+
+@mlp_expansion_backward.register_fake
+def _(grad_out, x, h, w1, w2):
+    return (
+        torch.empty_like(x),
+        w1.new_empty(w1.shape),
+        w1.new_empty((w1.shape[0],)),
+        w2.new_empty(w2.shape),
+        w2.new_empty((w2.shape[0],)),
+    )
+
+
+def _setup_mlp(ctx, inputs, output):
+    x, w1, b1, w2, b2, residual = inputs
+    _out, h = output
+    ctx.mark_non_differentiable(h)
+    ctx.save_for_backward(x, h, w1, w2)
+    ctx.has_b1, ctx.has_b2, ctx.has_residual = b1 is not None, b2 is not None, residual is not None
+
+
+def _mlp_backward(ctx, grad_out, _grad_h):
+    x, h, w1, w2 = ctx.saved_tensors
+    dx, dw1, db1, dw2, db2 = mlp_expansion_backward(grad_out, x, h, w1, w2)
+    return (
+        dx,
+        dw1,
+        db1 if ctx.has_b1 else None,
+        dw2,
+        db2 if ctx.has_b2 else None,
+        grad_out if ctx.has_residual else None,
+    )
+
+
+mlp_expansion.register_autograd(_mlp_backward, setup_context=_setup_mlp)

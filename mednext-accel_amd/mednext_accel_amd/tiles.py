@@ -168,3 +168,44 @@ def group_norm_splits(batch: int, channels: int, spatial_volume: int) -> int:
     by_occupancy = _cdiv(TARGET_WORKGROUPS, rows)
     by_size = max(1, spatial_volume // 4096)
     return max(1, min(by_occupancy, by_size, MAX_GN_SPLITS))
+
+
+# ------------------------------------------------------------------ pointwise
+
+PW_CHUNK = 128  # voxels per wave step of pw_fwd_kernel
+PW_ROWS = 64  # output rows per pw_fwd workgroup
+PW_MAX_K = 512
+PW_WG_STEP = 32  # voxels per pw_wgrad MFMA step
+PW_WG_TILE = 64
+
+
+def pointwise_supported(in_channels: int, out_channels: int, voxels: int) -> bool:
+    """Shapes the bf16 matrix-core pointwise kernels take (mirrors pointwise.hip).
+
+    Forward GEMM: K = in_channels, M = out_channels; its input gradient swaps
+    them, so both directions need K % 32 == 0, K <= 512 and M % 16 == 0.
+    """
+    fwd = in_channels % 32 == 0 and in_channels <= PW_MAX_K and out_channels % 16 == 0
+    dgrad = out_channels % 32 == 0 and out_channels <= PW_MAX_K and in_channels % 16 == 0
+    small = in_channels * voxels * 2 < 2**31 and out_channels * voxels * 2 < 2**31
+    return fwd and dgrad and voxels % 8 == 0 and small
+
+
+def pointwise_blocks(batch: int, k: int, m: int, voxels: int) -> int:
+    """Workgroups per (sample, 64-row block) for pw_fwd_kernel: one resident
+    workgroup per CU across the grid (the kernel runs one wave per SIMD), each
+    wave looping over at least two 128-voxel chunks."""
+    del k
+    chunks = _cdiv(voxels, PW_CHUNK)
+    slabs = max(1, batch * _cdiv(m, PW_ROWS))
+    wanted = _cdiv(CU_COUNT, slabs)
+    return max(1, min(wanted, _cdiv(chunks, 4 * 2)))
+
+
+def pointwise_wgrad_splits(batch: int, k: int, m: int, voxels: int) -> int:
+    """V-splits per sample for pw_wgrad_kernel: ~4 workgroups per CU over the
+    grid, each wave doing at least four 32-voxel steps."""
+    steps = _cdiv(voxels, PW_WG_STEP)
+    tiles = max(1, batch * _cdiv(m, PW_WG_TILE) * _cdiv(k, PW_WG_TILE))
+    wanted = _cdiv(TARGET_WORKGROUPS, tiles)
+    return max(1, min(wanted, _cdiv(steps, 4 * 4), 65535))

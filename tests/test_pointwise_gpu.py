@@ -1,0 +1,217 @@
+"""HIP pointwise (1x1x1) GEMMs with fused GELU / residual epilogues on the GPU.
+
+Small and ragged shapes are checked against the float64 oracle on the same
+bf16-rounded inputs; the MedNeXt stage shapes against PyTorch in fp32. The
+kernels take bf16 operands and accumulate in fp32, so the bar is the bf16
+autocast tolerance (normwise max relative error <= 2e-2).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from helpers import BF16, max_rel
+from mednext_accel_amd import hip_ops
+from mednext_accel_amd.hip_ops import (
+    PW_EPILOGUE_BIAS,
+    PW_EPILOGUE_BIAS_GELU,
+    PW_EPILOGUE_BIAS_RESIDUAL,
+    PW_EPILOGUE_GELU_GRAD,
+    PW_PROLOGUE_GELU,
+    PW_PROLOGUE_NONE,
+)
+from oracle import pointwise as opw
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def bf(shape, gen, scale=1.0):
+    return (torch.randn(shape, generator=gen) * scale).bfloat16()
+
+
+def f64(t):
+    return t.double().cpu().numpy()
+
+
+SHAPES = [
+    # (n, cin, cout, spatial)
+    (1, 32, 64, (4, 8, 8)),  # V = 256: two full chunks
+    (2, 64, 32, (3, 5, 8)),  # V = 120: ragged last chunk, batch 2
+    (1, 96, 48, (2, 4, 16)),  # K = 3 x 32, M = 48 (partial 64-row block)
+    (1, 32, 192, (1, 8, 17 * 8)),  # M = 192: three row blocks
+    (1, 512, 128, (2, 2, 8)),  # K = 512 (largest LDS weight block)
+]
+
+
+@pytest.mark.parametrize("n,cin,cout,spatial", SHAPES)
+@pytest.mark.parametrize("epilogue", ["bias", "bias_gelu", "bias_residual", "none"])
+def test_forward_epilogues_against_oracle(n, cin, cout, spatial, epilogue):
+    print(f"[pw fwd] n={n} cin={cin} cout={cout} spatial={spatial} epi={epilogue}", flush=True)
+    gen = torch.Generator().manual_seed(cin * 7 + cout)
+    x = bf((n, cin, *spatial), gen)
+    w = bf((cout, cin, 1, 1, 1), gen, cin**-0.5)
+    b = bf((cout,), gen)
+    res = bf((n, cout, *spatial), gen)
+    code = {"bias": PW_EPILOGUE_BIAS, "none": PW_EPILOGUE_BIAS, "bias_gelu": PW_EPILOGUE_BIAS_GELU,
+            "bias_residual": PW_EPILOGUE_BIAS_RESIDUAL}[epilogue]
+    bias = None if epilogue == "none" else b
+    y = hip_ops.pointwise_conv(
+        x.to(DEV), w.to(DEV), None if bias is None else bias.to(DEV),
+        aux=res.to(DEV) if epilogue == "bias_residual" else None, epilogue=code,
+    )
+    expect = opw.conv1x1(f64(x), f64(w), None if bias is None else f64(bias))
+    if epilogue == "bias_gelu":
+        expect = opw.gelu(expect)
+    if epilogue == "bias_residual":
+        expect = expect + f64(res)
+    assert y.dtype == torch.bfloat16 and y.shape == (n, cout, *spatial)
+    assert max_rel(y, expect) <= BF16
+
+
+# Shapes valid in both directions (the transposed product has K = cout).
+BOTH_WAYS = [(1, 32, 64, (4, 8, 8)), (2, 64, 32, (3, 5, 8)), (1, 32, 192, (1, 8, 17 * 8)), (1, 96, 64, (2, 4, 16))]
+
+
+@pytest.mark.parametrize("n,cin,cout,spatial", BOTH_WAYS)
+def test_gelu_prologue_and_transposed_product(n, cin, cout, spatial):
+    gen = torch.Generator().manual_seed(3 * cin + cout)
+    x = bf((n, cin, *spatial), gen, 2.0)
+    w = bf((cout, cin, 1, 1, 1), gen, cin**-0.5)
+    b = bf((cout,), gen)
+    y = hip_ops.pointwise_conv(x.to(DEV), w.to(DEV), b.to(DEV), prologue=PW_PROLOGUE_GELU)
+    assert max_rel(y, opw.conv1x1(opw.gelu(f64(x)), f64(w), f64(b))) <= BF16
+    # Input gradient: dX = W^T dY, weight given in the conv's own [Cout, Cin] layout.
+    dy = bf((n, cout, *spatial), gen)
+    dx = hip_ops.pointwise_conv(dy.to(DEV), w.to(DEV), transpose=True)
+    want_dx, _, _ = opw.conv1x1_backward(f64(dy), f64(x), f64(w))
+    assert dx.shape == x.shape and max_rel(dx, want_dx) <= BF16
+    # GELU backward fused into the input gradient: dH = (W^T dY) * GELU'(h).
+    h = bf((n, cin, *spatial), gen, 2.0)
+    dh = hip_ops.pointwise_conv(dy.to(DEV), w.to(DEV), aux=h.to(DEV), epilogue=PW_EPILOGUE_GELU_GRAD, transpose=True)
+    assert max_rel(dh, want_dx * opw.gelu_grad(f64(h))) <= BF16
+
+
+@pytest.mark.parametrize("n,cin,cout,spatial", SHAPES)
+@pytest.mark.parametrize("gelu_input", [False, True])
+def test_weight_and_bias_grad_against_oracle(n, cin, cout, spatial, gelu_input):
+    print(f"[pw wgrad] n={n} cin={cin} cout={cout} spatial={spatial} gelu={gelu_input}", flush=True)
+    gen = torch.Generator().manual_seed(11 * cin + cout)
+    x = bf((n, cin, *spatial), gen)
+    dy = bf((n, cout, *spatial), gen)
+    w0 = np.zeros((cout, cin, 1, 1, 1))
+    prologue = PW_PROLOGUE_GELU if gelu_input else PW_PROLOGUE_NONE
+    dw, db = hip_ops.pointwise_weight_grad(dy.to(DEV), x.to(DEV), prologue=prologue)
+    xin = opw.gelu(f64(x)) if gelu_input else f64(x)
+    _, want_dw, want_db = opw.conv1x1_backward(f64(dy), xin, w0)
+    assert dw.shape == (cout, cin, 1, 1, 1) and db.shape == (cout,)
+    assert max_rel(dw, want_dw) <= BF16
+    assert max_rel(db, want_db) <= BF16
+
+
+@pytest.mark.parametrize("splits", [1, 3, 64])
+def test_weight_grad_splits_and_determinism(splits):
+    gen = torch.Generator().manual_seed(5)
+    x = bf((2, 64, 8, 8, 24), gen).to(DEV)
+    dy = bf((2, 96, 8, 8, 24), gen).to(DEV)
+    a = hip_ops.pointwise_weight_grad(dy, x, splits=splits)
+    b = hip_ops.pointwise_weight_grad(dy, x, splits=splits)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    _, want_dw, want_db = opw.conv1x1_backward(f64(dy), f64(x), np.zeros((96, 64, 1, 1, 1)))
+    assert max_rel(a[0], want_dw) <= BF16 and max_rel(a[1], want_db) <= BF16
+
+
+STAGES = [(32, 64, 128), (64, 32, 128), (64, 192, 64), (192, 64, 64), (128, 512, 32), (512, 128, 32)]
+
+
+@pytest.mark.parametrize("cin,cout,size", STAGES)
+def test_stage_shapes_against_torch_fp32(cin, cout, size):
+    """MedNeXt-B expand / project shapes (configs[2]/[3]) vs PyTorch fp32 on the
+    same bf16 inputs: forward, input gradient, weight and bias gradients."""
+    print(f"[pw stage] {cin}->{cout} @ {size}^3", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(cin + cout)
+    x = torch.randn(1, cin, size, size, size, generator=gen, device=DEV).bfloat16()
+    w = (torch.randn(cout, cin, 1, 1, 1, generator=gen, device=DEV) * cin**-0.5).bfloat16()
+    b = torch.randn(cout, generator=gen, device=DEV).bfloat16()
+    dy = torch.randn(1, cout, size, size, size, generator=gen, device=DEV).bfloat16()
+    xf, wf, bf_ = (t.float().requires_grad_() for t in (x, w, b))
+    yf = F.conv3d(xf, wf, bf_)
+    rdx, rdw, rdb = torch.autograd.grad(yf, (xf, wf, bf_), dy.float())
+    y = hip_ops.pointwise_conv(x, w, b)
+    dx = hip_ops.pointwise_conv(dy, w, transpose=True)
+    dw, db = hip_ops.pointwise_weight_grad(dy, x)
+    assert max_rel(y, yf) <= BF16
+    assert max_rel(dx, rdx) <= BF16
+    assert max_rel(dw, rdw) <= BF16
+    assert max_rel(db, rdb) <= BF16
+
+
+@pytest.mark.parametrize("residual", [True, False])
+def test_fused_mlp_expansion_matches_unfused_fp32(residual):
+    """mlp_expansion = project(GELU(expand(x))) + residual, fwd + bwd, vs the
+    same composition in fp32 PyTorch on the bf16-rounded operands."""
+    gen = torch.Generator(device=DEV).manual_seed(2)
+    c, r, s = 32, 2, 32
+    x = torch.randn(1, c, s, s, s, generator=gen, device=DEV).bfloat16()
+    res = torch.randn(1, c, s, s, s, generator=gen, device=DEV).bfloat16()
+    w1 = (torch.randn(r * c, c, 1, 1, 1, generator=gen, device=DEV) * c**-0.5).bfloat16()
+    b1 = (torch.randn(r * c, generator=gen, device=DEV) * 0.1).bfloat16()
+    w2 = (torch.randn(c, r * c, 1, 1, 1, generator=gen, device=DEV) * (r * c) ** -0.5).bfloat16()
+    b2 = (torch.randn(c, generator=gen, device=DEV) * 0.1).bfloat16()
+    leaves = [t.clone().requires_grad_() for t in (x, w1, b1, w2, b2, res)]
+    out, _h = hip_ops.mlp_expansion(*leaves[:5], leaves[5] if residual else None)
+    ref_leaves = [t.float().requires_grad_() for t in (x, w1, b1, w2, b2, res)]
+    xf, w1f, b1f, w2f, b2f, rf = ref_leaves
+    ref = F.conv3d(F.gelu(F.conv3d(xf, w1f, b1f)), w2f, b2f) + (rf if residual else 0)
+    assert max_rel(out, ref) <= BF16
+    g = torch.randn_like(ref).bfloat16()
+    inputs = leaves if residual else leaves[:5]
+    got = torch.autograd.grad(out, inputs, g)
+    want = torch.autograd.grad(ref, ref_leaves if residual else ref_leaves[:5], g.float())
+    for name, a, b in zip(["x", "w1", "b1", "w2", "b2", "res"], got, want):
+        assert max_rel(a, b) <= BF16, name
+
+
+def test_opcheck_pointwise_ops():
+    gen = torch.Generator(device=DEV).manual_seed(4)
+    x = torch.randn(1, 32, 2, 4, 8, generator=gen, device=DEV).bfloat16().requires_grad_()
+    w = (torch.randn(64, 32, 1, 1, 1, generator=gen, device=DEV) / 6).bfloat16().requires_grad_()
+    b = torch.randn(64, generator=gen, device=DEV).bfloat16().requires_grad_()
+    torch.library.opcheck(hip_ops.pointwise_conv3d, (x, w, b))
+    w2 = (torch.randn(32, 64, 1, 1, 1, generator=gen, device=DEV) / 8).bfloat16().requires_grad_()
+    res = torch.randn(1, 32, 2, 4, 8, generator=gen, device=DEV).bfloat16().requires_grad_()
+    torch.library.opcheck(hip_ops.mlp_expansion, (x, w, b, w2, None, res))
+
+
+def test_channels_above_512_are_rejected_and_not_selected():
+    """Stages 3-4 (1024 / 2048 hidden channels) exceed the 64 x 512 LDS weight
+    block: the tile policy does not select the kernel and the C ABI refuses it."""
+    from mednext_accel_amd.tiles import pointwise_supported
+
+    assert not pointwise_supported(256, 1024, 16**3)
+    assert pointwise_supported(128, 512, 32**3)
+    x = torch.randn(1, 1024, 2, 2, 8, device=DEV).bfloat16()
+    w = torch.randn(256, 1024, 1, 1, 1, device=DEV).bfloat16()
+    with pytest.raises(hip_ops._hip.HipLibraryError, match="above 512"):
+        hip_ops.pointwise_conv(x, w)
+
+
+def test_pointwise_argument_errors():
+    x = torch.randn(1, 32, 2, 2, 8, device=DEV).bfloat16()
+    w = torch.randn(64, 32, 1, 1, 1, device=DEV).bfloat16()
+    with pytest.raises(ValueError):
+        hip_ops.pointwise_conv(x.float(), w)  # dtype
+    with pytest.raises(ValueError):
+        hip_ops.pointwise_conv(x, torch.randn(64, 16, 1, 1, 1, device=DEV).bfloat16())  # channel mismatch
+    with pytest.raises(ValueError):
+        hip_ops.pointwise_conv(x.transpose(3, 4), w)  # non-contiguous
+    with pytest.raises(hip_ops._hip.HipLibraryError):
+        hip_ops.pointwise_conv(torch.randn(1, 16, 2, 2, 8, device=DEV).bfloat16(),
+                               torch.randn(64, 16, 1, 1, 1, device=DEV).bfloat16())  # K % 32
+    with pytest.raises(hip_ops._hip.HipLibraryError):
+        hip_ops.pointwise_conv(torch.randn(1, 32, 1, 1, 7, device=DEV).bfloat16(), w)  # V % 8
+    with pytest.raises(hip_ops._hip.HipLibraryError):
+        hip_ops.pointwise_conv(x, w, aux=None, epilogue=PW_EPILOGUE_BIAS_RESIDUAL)  # missing aux
