@@ -156,6 +156,19 @@ def _norm_descriptor(norm: nn.GroupNorm, *, role: str | None = None) -> Operator
     return OperatorDescriptor.normalization(family="group_norm3d", channels=norm.num_channels, role=role)
 
 
+def _gemm_guards(x: Tensor, cin: int, cout: int) -> bool:
+    """Execution-time guards of the matrix-core pointwise route: grad enabled,
+    batched contiguous NCDHW, and channel / voxel counts the kernels take."""
+    from .tiles import pointwise_supported
+
+    return (
+        torch.is_grad_enabled()
+        and x.ndim == 5
+        and x.is_contiguous()
+        and pointwise_supported(cin, cout, int(x.shape[2] * x.shape[3] * x.shape[4]))
+    )
+
+
 def _hip_ops():
     from . import hip_ops  # loads libmednext_hip.so; raises if it is missing
 
@@ -245,6 +258,10 @@ class AdaptivePointwise3d(_AdaptiveModule):
     def forward(self, x: Tensor) -> Tensor:
         context = _context_from_tensor(x, self.model_context, training=self.training)
         decision = self.resolver.resolve(self.descriptor, context, context.phase)
+        if decision.implementation == "hip_pointwise_gemm" and _gemm_guards(x, self.in_channels, self.out_channels):
+            dt = torch.bfloat16
+            bias = self.bias.to(dt) if self.bias is not None else None
+            return _hip_ops().pointwise_conv3d(x.to(dt), self.weight.to(dt), bias)
         if (
             decision.implementation == "pointwise_gemm_per_sample"
             and torch.is_grad_enabled()
@@ -350,18 +367,24 @@ class AdaptiveGroupNorm3d(_AdaptiveModule):
     def _reference(self, x: Tensor) -> Tensor:
         return F.group_norm(x, self.num_groups, self.weight, self.bias, self.eps)
 
-    def forward(self, x: Tensor) -> Tensor:
+    def forward(self, x: Tensor, out_dtype: torch.dtype | None = None) -> Tensor:
+        """``out_dtype`` (used by a fused block expansion that consumes the
+        result as bf16) overrides the output dtype; the values are the float32
+        result rounded once, exactly what the consumer's autocast cast makes."""
         if x.ndim != 5 or not x.is_contiguous() or not torch.is_grad_enabled():
-            return self._reference(x)
+            y = self._reference(x)
+            return y if out_dtype is None else y.to(out_dtype)
         context = _context_from_tensor(x, self.model_context, training=self.training)
         decision = self.resolver.resolve(self.descriptor, context, context.phase)
         if decision.implementation != "hip_group_norm":
-            return self._reference(x)
+            y = self._reference(x)
+            return y if out_dtype is None else y.to(out_dtype)
         hip_ops = _hip_ops()
         autocast = torch.is_autocast_enabled(x.device.type) and x.dtype != torch.float64
         # Autocast runs group_norm in float32 (input cast up, float32 result);
         # the kernel reads the low-precision input directly, which is exact.
-        out_dtype = torch.float32 if autocast else None
+        if out_dtype is None:
+            out_dtype = torch.float32 if autocast else None
         weight, bias = self.weight, self.bias
         if autocast:
             weight = weight.float() if weight is not None else None
@@ -371,6 +394,63 @@ class AdaptiveGroupNorm3d(_AdaptiveModule):
 
     def extra_repr(self) -> str:
         return f"{self.num_groups}, {self.num_channels}, eps={self.eps}, affine={self.affine}"
+
+
+class AdaptiveExpansion:
+    """Fused ``project(GELU(expand(h))) [+ residual]`` of one MedNeXt block.
+
+    Deliberately *not* an ``nn.Module``: it holds a reference to its block and
+    reads the block's own ``expand`` / ``project`` Parameters at call time, so
+    installing it changes neither ``parameters()`` nor the state-dict keys. The
+    block consults it (``MedNeXtBlock.forward``) before running its modules;
+    when ``applies`` is false the block runs exactly as without it.
+    """
+
+    def __init__(self, block: nn.Module, resolver: PolicyResolver, model_context: ModelOptimizationContext,
+                 *, role: str | None = None) -> None:
+        self.block = block
+        self.resolver = resolver
+        self.model_context = model_context
+        self.descriptor = OperatorDescriptor(
+            "mlp_expansion3d", "regular", block.expand.in_channels, block.project.out_channels, role=role
+        )
+
+    def applies(self, x: Tensor) -> bool:
+        """Decided from the block input: training with grad, bf16 autocast on an
+        AMD GPU and the policy selecting the fused kernel. Shapes are checked
+        separately (``supports``) on the expansion's own input."""
+        b = self.block
+        if not (b.training and torch.is_grad_enabled() and x.is_cuda and x.ndim == 5):
+            return False
+        context = _context_from_tensor(x, self.model_context, training=True)
+        if context.dtype != "bfloat16":
+            return False
+        return self.resolver.resolve(self.descriptor, context, "training").implementation == "hip_fused_expansion"
+
+    def supports(self, h: Tensor) -> bool:
+        """Shape check on the expansion's input (the depthwise output: halved
+        in down blocks, 2s-1 per dimension in up blocks)."""
+        from .tiles import pointwise_supported
+
+        b = self.block
+        v = int(h.shape[2] * h.shape[3] * h.shape[4])
+        return (
+            h.is_contiguous()
+            and pointwise_supported(b.expand.in_channels, b.expand.out_channels, v)
+            and pointwise_supported(b.expand.out_channels, b.project.out_channels, v)
+        )
+
+    def __call__(self, h: Tensor, residual: Tensor | None) -> Tensor:
+        b = self.block
+        dt = torch.bfloat16
+        w1, w2 = b.expand.weight.to(dt), b.project.weight.to(dt)
+        b1 = b.expand.bias.to(dt) if b.expand.bias is not None else None
+        b2 = b.project.bias.to(dt) if b.project.bias is not None else None
+        fuse_residual = residual is not None and residual.dtype == dt and residual.is_contiguous()
+        out, _h = _hip_ops().mlp_expansion(h.to(dt), w1, b1, w2, b2, residual if fuse_residual else None)
+        if residual is not None and not fuse_residual:
+            out = out + residual
+        return out
 
 
 def _pointwise_eligible(module: nn.Module) -> bool:
@@ -412,7 +492,10 @@ def install_adaptive_operators(
     model_context: ModelOptimizationContext,
     _prefix: str = "",
 ) -> int:
-    """Swap eligible children for wrappers in place; returns how many were swapped."""
+    """Swap eligible children for wrappers in place and attach a fused expansion
+    to each MedNeXt block; returns how many modules were swapped."""
+    from .blocks import MedNeXtBlock
+
     count = 0
     for name, child in list(model.named_children()):
         role = f"{_prefix}.{name}" if _prefix else name
@@ -427,4 +510,11 @@ def install_adaptive_operators(
             continue
         setattr(model, name, wrapper)
         count += 1
+    if isinstance(model, MedNeXtBlock) and _group_norm_wrapped(model):
+        # Plain attribute (not a submodule): parameters and keys are unchanged.
+        model.__dict__["fused_expansion"] = AdaptiveExpansion(model, resolver, model_context, role=_prefix or None)
     return count
+
+
+def _group_norm_wrapped(block: nn.Module) -> bool:
+    return isinstance(getattr(block, "norm", None), AdaptiveGroupNorm3d)

@@ -134,6 +134,37 @@ def _hip_group_norm(descriptor, context, phase: str) -> str | None:
     return None
 
 
+def _pointwise_geometry(descriptor) -> bool:
+    return (
+        descriptor.direction == "regular"
+        and descriptor.kernel_size == (1, 1, 1)
+        and descriptor.stride == (1, 1, 1)
+        and descriptor.padding == (0, 0, 0)
+        and descriptor.dilation == (1, 1, 1)
+        and descriptor.groups == 1
+    )
+
+
+def _hip_pointwise(descriptor, context, phase: str) -> str | None:
+    reason = _training_gpu(context, amd=True)
+    if reason is not None:
+        return reason
+    if context.dtype != "bfloat16":
+        return "implementation requires bfloat16"
+    if not _pointwise_geometry(descriptor):
+        return "implementation does not support this geometry"
+    return None
+
+
+def _hip_expansion(descriptor, context, phase: str) -> str | None:
+    reason = _training_gpu(context, amd=True)
+    if reason is not None:
+        return reason
+    if context.dtype != "bfloat16":
+        return "implementation requires bfloat16"
+    return None
+
+
 def _pointwise_gemm(descriptor, context, phase: str) -> str | None:
     if context.phase != "training":
         return "implementation requires training"
@@ -171,6 +202,8 @@ def default_implementation_registry(*, triton_available: bool | None = None) -> 
         ("hip_depthwise_dx", ("depthwise_conv3d",), ("backward_input",), "numerical", False, _hip_depthwise, _DW_GUARDS),
         ("hip_split_dw", ("depthwise_conv3d",), ("backward_weight",), "numerical", False, _hip_depthwise, _DW_GUARDS),
         ("hip_group_norm", ("group_norm3d",), ("training",), "numerical", False, _hip_group_norm, _TENSOR_GUARDS),
+        ("hip_pointwise_gemm", ("pointwise_conv3d",), ("training",), "numerical", False, _hip_pointwise, (*_TENSOR_GUARDS, "channels_supported")),
+        ("hip_fused_expansion", ("mlp_expansion3d",), ("training",), "numerical", False, _hip_expansion, (*_TENSOR_GUARDS, "channels_supported")),
         ("pointwise_gemm_per_sample", ("pointwise_conv3d",), ("training",), "numerical", False, _pointwise_gemm, _TENSOR_GUARDS),
         ("triton_depthwise_dx", ("depthwise_conv3d",), ("backward_input",), "numerical", False, _no_triton, _DW_GUARDS),
         ("triton_split_dw", ("depthwise_conv3d",), ("backward_weight",), "numerical", False, _no_triton, _DW_GUARDS),

@@ -110,6 +110,11 @@ class PolicyResolver:
         self.registry = registry or default_implementation_registry()
         self._warned: set[str] = set()
 
+    def __deepcopy__(self, memo):
+        # Policies are immutable; copies of a wrapped model share the resolver
+        # (and its warn-once state).
+        return self
+
     def context_layers(self, context: ExecutionContext) -> tuple[OptimizationPolicy, ...]:
         vendor = context.vendor
         if vendor is None:

@@ -125,7 +125,26 @@ def test_gfx950_policy_group_norm_and_pointwise():
     assert d.implementation == "hip_group_norm"
     assert d.parameters["splits"] == tiles.group_norm_splits(1, 32, 128**3)
     pw = _conv_descriptor(nn.Conv3d(32, 64, 1), role="encoder_stages.0.0.expand")
-    assert resolver.resolve(pw, ctx((128,) * 3), "training").implementation == "reference"
+    assert resolver.resolve(pw, ctx((128,) * 3), "training").implementation == "hip_pointwise_gemm"
+    assert resolver.resolve(pw, ctx((128,) * 3, dtype="float32"), "training").implementation == "reference"
+
+
+def test_fused_expansion_is_attached_without_touching_parameters():
+    from mednext_accel_amd import MedNeXtBlock
+    from mednext_accel_amd.adaptive import AdaptiveExpansion
+
+    block = MedNeXtBlock(spatial_dims=3, in_channels=32, out_channels=32, expansion_ratio=2, kernel_size=3)
+    params, keys = tuple(block.parameters()), tuple(block.state_dict())
+    install_adaptive_operators(block, resolver=PolicyRegistry().resolver(), model_context=MC)
+    fused = block.__dict__["fused_expansion"]
+    assert isinstance(fused, AdaptiveExpansion) and "fused_expansion" not in dict(block.named_children())
+    assert tuple(block.parameters()) == params and tuple(block.state_dict()) == keys
+    d = PolicyRegistry().resolver().resolve(fused.descriptor, ctx((128,) * 3), "training")
+    assert d.implementation == "hip_fused_expansion"
+    assert PolicyRegistry().resolver().resolve(fused.descriptor, ctx((128,) * 3, dtype="float32"), "training").implementation == "reference"
+    # On the CPU the block never takes the fused route.
+    assert not fused.applies(torch.randn(1, 32, 8, 8, 8))
+    copy.deepcopy(block)  # the plain attribute survives deep copies (checkpoint loaders use them)
 
 
 def test_strided_and_transposed_depthwise_stay_native():

@@ -36,6 +36,7 @@ DW_OP = "mednext_accel_amd::depthwise_conv3d_odd_regular"
 DX_OP = "mednext_accel_amd::depthwise_input_grad_odd_regular"
 DWG_OP = "mednext_accel_amd::depthwise_weight_grad_odd_regular"
 GN_OP = "mednext_accel_amd::group_norm_channels"
+MLP_OP = "mednext_accel_amd::mlp_expansion"
 
 
 class Observe(TorchDispatchMode):
@@ -186,7 +187,7 @@ def test_block_cfg2_bf16_autocast_matches_reference_block(channels, size, ratio)
         want = ref(x)
         with Observe() as seen:
             got = cand(y)
-    assert DW_OP in seen.ops and GN_OP in seen.ops
+    assert DW_OP in seen.ops and GN_OP in seen.ops and MLP_OP in seen.ops
     exact = truth(z)
     g = torch.randn_like(want)
     wants = torch.autograd.grad(want, (x, *ref.parameters()), g)
@@ -236,6 +237,7 @@ def test_base_training_step_128_bf16_matches_reference():
         losses.append(float(loss))
         if model is cand:
             assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops and GN_OP in seen.ops
+            assert MLP_OP in seen.ops
         del step
     assert abs(losses[0] - losses[1]) / abs(losses[1]) < BF16
     for (name, p), q in zip(cand.named_parameters(), ref.parameters(), strict=True):
