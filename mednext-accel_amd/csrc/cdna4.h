@@ -52,6 +52,18 @@ __device__ inline void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4
   __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, 0);
 }
 
+// MI355X dispatches workgroup i to XCD i % 8, and each XCD has its own L2.
+// Remapping (i % 8, i / 8) -> (i % 8) * (n / 8) + i / 8 hands every XCD a
+// contiguous run of tile indices, so neighbouring tiles (which share halo
+// cache lines) meet in one L2. Bijective on [0, 8 * (n / 8)); the < 8 tail
+// keeps its index.
+constexpr int kXcds = 8;
+__device__ inline int64_t xcd_swizzle(int64_t bid, int64_t nblocks) {
+  const int64_t per = nblocks / kXcds;
+  if (bid >= per * kXcds) return bid;
+  return (bid % kXcds) * per + bid / kXcds;
+}
+
 __device__ inline f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);

@@ -44,7 +44,7 @@ struct BlockPos {
 
 __device__ inline BlockPos block_pos(const MGeom& g) {
   BlockPos b;
-  int64_t bid = blockIdx.x;
+  int64_t bid = xcd_swizzle(blockIdx.x, gridDim.x);
   b.wt = static_cast<int>(bid % g.nWt);
   bid /= g.nWt;
   b.ht = static_cast<int>(bid % g.nHt);
@@ -235,186 +235,156 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
 // rows. Loads for plane i + PD are in flight (non-temporal) while plane i's
 // MFMAs run. Per-workgroup partials go to a fp32 workspace reduced in fixed
 // order afterwards.
-template <int K, int CT, int RT>
-struct WgradLayout {
+// ------------------------------------------------------------- weight grad
+//
+// dW[kd][kh][kw] = sum_v x[d+kd-P][h+kh-P][w+kw-P] * dy[d][h][w], dB = sum_v dy.
+//
+// Each wave owns a block of RB = 17 - K grad_output rows and one 32-column
+// unit; per x plane t its MFMA products are
+//   C_{kw,kd}[i][j] += sum_{32 w} x[t][r0-P+i][w+kw-P] * dy[t-kd+P][r0+j][w]
+// (i = 0..15 x rows, j < RB dy rows), so every row pair meets once and tap kh
+// is the diagonal i - j = kh of C_{kw,kd}: K*K MFMAs per plane and unit, no
+// tap-shifted operand copies. A workgroup (4 waves = NU units x 4/NU row
+// blocks) stages each x and dy plane through LDS with row-contiguous 16-byte
+// loads (double-buffered, one barrier per plane); a wave reads its x rows
+// once per plane (16 bytes + the dwords either side, from which the K column
+// shifts are formed in registers) and only the newly entering dy plane, the
+// K most recent dy fragments rotating in registers. dB is summed from each
+// dy fragment as it enters. At the end the accumulator tiles go through LDS
+// and the diagonals are summed there.
+template <int K, int NU>
+struct WgradTile {
   static constexpr int P = K / 2;
-  static constexpr int TH = 16 * RT, TW = 16 * CT;
-  static constexpr int LR = TH + 2 * P;         // x rows: h = th0 - P + r
-  static constexpr int XROW = TW + 8;           // elements; 4 dwords mod 32 dwords
-  static constexpr int XCOPY_RAW = LR * XROW;   // elements per shifted copy
-  // copy stride == 12 dwords (24 elements) mod 64 elements
-  static constexpr int XCOPY = XCOPY_RAW + ((24 - XCOPY_RAW % 64) % 64 + 64) % 64;
-  static constexpr int XBUF = K * XCOPY;        // elements per plane buffer
-  static constexpr int DSLOT = TH * TW + 8;     // dy slot stride (elements)
-  static constexpr int RING = K + 1;
-  static constexpr int XDUMMY = 2 * XBUF;       // K x 8 elements for chunkless threads
-  static constexpr int RING_OFF = XDUMMY + 8 * K;
-  static constexpr int DDUMMY = RING_OFF + RING * DSLOT;
-  static constexpr size_t bytes = static_cast<size_t>(DDUMMY + 8) * 2;
+  static constexpr int RB = 16 - 2 * P;           // grad_output rows per wave
+  static constexpr int NRB = 4 / NU;               // row blocks per workgroup
+  static constexpr int COLS = 32 * NU;             // columns per workgroup
+  static constexpr int DROWS = RB * NRB;           // grad_output rows per workgroup
+  static constexpr int XROWS = DROWS + 2 * P;      // x rows per workgroup
+  static constexpr int XPITCH = COLS + 24;         // [w0-8, w0+COLS+8) + pad
+  static constexpr int DPITCH = COLS + 24;
+  static constexpr int XBUF = XROWS * XPITCH;      // elements
+  static constexpr int DBUF = DROWS * DPITCH;
+  static constexpr int XCPR = COLS / 8 + 2;        // 16-byte chunks per x row (with halo chunks)
+  static constexpr int DCPR = COLS / 8;
+  static constexpr int NXC = (XROWS * XCPR + kThreads - 1) / kThreads;
+  static constexpr int NDC = (DROWS * DCPR + kThreads - 1) / kThreads;
+  static constexpr int TILES_PER_ROUND = 3;        // accumulator tiles reduced per LDS round
+  static constexpr size_t LOOP_BYTES = (2 * static_cast<size_t>(XBUF) + 2 * DBUF + 16) * 2;
+  static constexpr size_t RED_BYTES = static_cast<size_t>(4) * TILES_PER_ROUND * 256 * 4;
+  static constexpr size_t BYTES = LOOP_BYTES > RED_BYTES ? LOOP_BYTES : RED_BYTES;
 };
 
-template <int K, int CT, int RT, int PD>
+struct WGeom {
+  int C, D, H, W;
+  int TD;              // grad_output planes per D-chunk
+  int nDc, nRBG, nCG;  // D-chunks, row-block groups, column groups per (n, c)
+  int nRB, nCU;        // row blocks (nRBG * 4 / NU) and 32-column units (nCG * NU)
+};
+
+template <int K, int NU, int PD>
 __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* __restrict__ x,
                                                                  const bf16_t* __restrict__ dy,
                                                                  float* __restrict__ partial,
-                                                                 MGeom g, int splits) {
-  using L = WgradLayout<K, CT, RT>;
-  constexpr int P = K / 2;
-  constexpr int K2 = K * K;
-  constexpr int K3 = K2 * K;
-  constexpr int MB = (K2 + 1 + 15) / 16;  // taps plus the all-ones row
-  constexpr int TH = L::TH, TW = L::TW, LR = L::LR;
-  constexpr int XCPR = TW / 8;  // 8-element chunks per row
-  constexpr int XCHUNKS = LR * XCPR;
-  constexpr int NXC = (XCHUNKS + kThreads - 1) / kThreads;
-  constexpr int DCHUNKS = TH * XCPR;
-  constexpr int NDC = (DCHUNKS + kThreads - 1) / kThreads;
-  constexpr int UPR = TW / 32;  // 32-column MFMA units per row
-  constexpr int ROWS_PER_WAVE = TH / 4;
-  constexpr int RING = L::RING;
-  static_assert(P <= 2, "the fill builds column shifts of at most 2");
+                                                                 WGeom g, int splits) {
+  using T = WgradTile<K, NU>;
+  constexpr int P = T::P, RB = T::RB, K2 = K * K, K3 = K2 * K;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-
-  const BlockPos bp = block_pos(g);
   uint16_t* const lds = reinterpret_cast<uint16_t*>(smem_raw);
-  uint16_t* const ring = lds + L::RING_OFF;  // [RING][DSLOT]
-  const int th0 = bp.ht * TH, tw0 = bp.wt * TW, d0 = bp.dc * g.TD;
+  uint16_t* const dlds = lds + 2 * T::XBUF;
+  uint16_t* const dummy = dlds + 2 * T::DBUF;  // 16-byte sink for threads without a chunk
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n16 = lane & 15, q = lane >> 4;
+  int64_t rest = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int cg = static_cast<int>(rest % g.nCG);
+  rest /= g.nCG;
+  const int rbg = static_cast<int>(rest % g.nRBG);
+  rest /= g.nRBG;
+  const int dc = static_cast<int>(rest % g.nDc);
+  const int64_t nc = rest / g.nDc;
+  const int c = static_cast<int>(nc % g.C);
+  const int64_t n = nc / g.C;
+  const int r0 = rbg * T::DROWS, w0 = cg * T::COLS, d0 = dc * g.TD;
+  const int dend = min(d0 + g.TD, g.D);
   const int64_t plane = static_cast<int64_t>(g.H) * g.W;
-  const uint16_t* __restrict__ xnc = reinterpret_cast<const uint16_t*>(x) + bp.nc * g.D * plane;
-  const uint16_t* __restrict__ dync = reinterpret_cast<const uint16_t*>(dy) + bp.nc * g.D * plane;
-  const __amdgpu_buffer_rsrc_t xr = slab_rsrc(xnc, static_cast<uint32_t>(g.D * plane * 2));
-  const __amdgpu_buffer_rsrc_t dr = slab_rsrc(dync, static_cast<uint32_t>(g.D * plane * 2));
-  const int nplanes = g.TD + K - 1;
+  const uint32_t plane_bytes = static_cast<uint32_t>(plane * 2);
+  const __amdgpu_buffer_rsrc_t xr =
+      slab_rsrc(reinterpret_cast<const uint16_t*>(x) + nc * g.D * plane, static_cast<uint32_t>(g.D) * plane_bytes);
+  const __amdgpu_buffer_rsrc_t dr =
+      slab_rsrc(reinterpret_cast<const uint16_t*>(dy) + nc * g.D * plane, static_cast<uint32_t>(g.D) * plane_bytes);
 
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int n16 = lane & 15;
-  const int q = lane >> 4;
-
-  // Fill coordinates, the same for every plane. A chunk is x[w .. w+7] of one
-  // row (w = tw0 + 8*ch); the shifted copies also need the dwords just before
-  // (x[w-2], x[w-1]) and after (x[w+8], x[w+9]). Offsets are bytes inside a
-  // plane (-1: outside it). Threads without a chunk write dummy LDS slots.
-  int x_main[NXC], x_prev[NXC], x_next[NXC], x_lds[NXC], x_step[NXC];
+  // Fill chunks (same for every plane): x rows r0-P .. r0+DROWS+P-1, columns
+  // [w0-8, w0+COLS+8) in 8-element chunks; dy rows r0 .. r0+DROWS-1, columns
+  // [w0, w0+COLS). Byte offsets inside a plane, -1 outside it.
+  int xg[T::NXC], xl[T::NXC], dg[T::NDC], dl[T::NDC];
 #pragma unroll
-  for (int u = 0; u < NXC; ++u) {
+  for (int u = 0; u < T::NXC; ++u) {
     const int e = threadIdx.x + u * kThreads;
-    x_main[u] = x_prev[u] = x_next[u] = -1;
-    x_lds[u] = L::XDUMMY;
-    x_step[u] = 8;  // dummy: copies at consecutive 16-byte slots
-    if (e < XCHUNKS) {
-      const int r = e / XCPR;
-      const int ch = e - r * XCPR;
-      const int h = th0 - P + r;
-      const int w = tw0 + 8 * ch;
-      x_lds[u] = r * L::XROW + 8 * ch;
-      x_step[u] = L::XCOPY;
-      if (h >= 0 && h < g.H) {
-        const int pos = h * g.W + w;
-        if (w < g.W) x_main[u] = 2 * pos;
-        if (w >= 8 && w - 8 < g.W) x_prev[u] = 2 * (pos - 2);
-        if (w + 8 < g.W) x_next[u] = 2 * (pos + 8);
-      }
+    xg[u] = -1;
+    xl[u] = -1;
+    if (e < T::XROWS * T::XCPR) {
+      const int r = e / T::XCPR, ch = e - r * T::XCPR;
+      const int h = r0 - P + r, w = w0 - 8 + 8 * ch;
+      xl[u] = r * T::XPITCH + 8 * ch;
+      if (h >= 0 && h < g.H && w >= 0 && w < g.W) xg[u] = 2 * (h * g.W + w);
     }
   }
-  int d_off[NDC], d_lds[NDC];
 #pragma unroll
-  for (int u = 0; u < NDC; ++u) {
+  for (int u = 0; u < T::NDC; ++u) {
     const int e = threadIdx.x + u * kThreads;
-    d_off[u] = -1;
-    d_lds[u] = -1;  // -1: dummy slot
-    if (e < DCHUNKS) {
-      const int r = e / XCPR;
-      const int ch = e - r * XCPR;
-      const int h = th0 + r;
-      const int w = tw0 + 8 * ch;
-      d_lds[u] = r * TW + 8 * ch;
-      if (h < g.H && w < g.W) d_off[u] = 2 * (h * g.W + w);
+    dg[u] = -1;
+    dl[u] = -1;
+    if (e < T::DROWS * T::DCPR) {
+      const int r = e / T::DCPR, ch = e - r * T::DCPR;
+      const int h = r0 + r, w = w0 + 8 * ch;
+      dl[u] = r * T::DPITCH + 8 * ch;
+      if (h < g.H && w < g.W) dg[u] = 2 * (h * g.W + w);
     }
   }
 
+  // Step s: x plane t = d0 - P + s, and grad_output plane t + P (which enters
+  // the ring); each is zero outside its valid range.
+  const int nsteps = (dend - d0) + 2 * P;
   struct Pre {
-    uint4 xv[NXC];
-    uint32_t pw[NXC];
-    uint32_t nw[NXC];
-    uint4 dv[NDC];
+    uint4 xv[T::NXC];
+    uint4 dv[T::NDC];
   };
-  // Plane j of this workgroup: x plane d0 - P + j and grad_output plane d0 + j.
-  auto load = [&](int j, Pre& p) {
-    const int di = d0 - P + j;
-    const bool xok = j < nplanes && di >= 0 && di < g.D;
-    const uint32_t xbase = static_cast<uint32_t>(xok ? di : 0) * static_cast<uint32_t>(plane * 2);
+  auto load = [&](int s, Pre& p) {
+    const int t = d0 - P + s;
+    const bool xok = s < nsteps && t >= 0 && t < g.D;
+    const uint32_t xb = static_cast<uint32_t>(xok ? t : 0) * plane_bytes;
+    const int td = t + P;
+    const bool dok = s < nsteps && td >= d0 && td < dend;
+    const uint32_t dbo = static_cast<uint32_t>(dok ? td : 0) * plane_bytes;
 #pragma unroll
-    for (int u = 0; u < NXC; ++u) {
-      p.xv[u] = buf_load16(xr, xok && x_main[u] >= 0 ? xbase + x_main[u] : kOob);
-      p.pw[u] = buf_load4(xr, xok && x_prev[u] >= 0 ? xbase + x_prev[u] : kOob);
-      p.nw[u] = buf_load4(xr, xok && x_next[u] >= 0 ? xbase + x_next[u] : kOob);
-    }
-    const bool dok = j < g.TD && d0 + j < g.D;
-    const uint32_t dbase = static_cast<uint32_t>(dok ? d0 + j : 0) * static_cast<uint32_t>(plane * 2);
+    for (int u = 0; u < T::NXC; ++u) p.xv[u] = buf_load16(xr, xok && xg[u] >= 0 ? xb + xg[u] : kOob);
 #pragma unroll
-    for (int u = 0; u < NDC; ++u) {
-      p.dv[u] = buf_load16_nt(dr, dok && d_off[u] >= 0 ? dbase + d_off[u] : kOob);
-    }
+    for (int u = 0; u < T::NDC; ++u) p.dv[u] = buf_load16_nt(dr, dok && dg[u] >= 0 ? dbo + dg[u] : kOob);
   };
-  auto store = [&](int i, const Pre& p) {
-    uint16_t* const buf = lds + (i & 1) * L::XBUF;
+  auto store = [&](int s, const Pre& p) {
+    uint16_t* const xb = lds + (s & 1) * T::XBUF;
+    uint16_t* const db = dlds + (s & 1) * T::DBUF;
 #pragma unroll
-    for (int u = 0; u < NXC; ++u) {
-      // Words of x[w-2 .. w+9]: e[0] = (x[w-2], x[w-1]), e[1..4] = the chunk,
-      // e[5] = (x[w+8], x[w+9]). Copy s (shift s - P) starts at x[w + s - P].
-      const uint32_t e[6] = {p.pw[u], p.xv[u].x, p.xv[u].y, p.xv[u].z, p.xv[u].w, p.nw[u]};
-      uint16_t* const dst = (x_lds[u] == L::XDUMMY ? lds : buf) + x_lds[u];
+    for (int u = 0; u < T::NXC; ++u) *reinterpret_cast<uint4*>(xl[u] >= 0 ? xb + xl[u] : dummy) = p.xv[u];
 #pragma unroll
-      for (int cs = 0; cs < K; ++cs) {
-        const int sh = cs - P;  // -2..2 elements
-        uint4 v;
-        if (sh % 2 == 0) {
-          const int b = 1 + sh / 2;
-          v = make_uint4(e[b], e[b + 1], e[b + 2], e[b + 3]);
-        } else {
-          // Odd shift: word j = (x[w+sh+2j], x[w+sh+2j+1]) is the high half
-          // of e[b+j] and the low half of e[b+j+1].
-          const int b = sh < 0 ? 0 : 1;
-          v = make_uint4(__builtin_amdgcn_alignbit(e[b + 1], e[b], 16),
-                         __builtin_amdgcn_alignbit(e[b + 2], e[b + 1], 16),
-                         __builtin_amdgcn_alignbit(e[b + 3], e[b + 2], 16),
-                         __builtin_amdgcn_alignbit(e[b + 4], e[b + 3], 16));
-        }
-        *reinterpret_cast<uint4*>(dst + cs * x_step[u]) = v;
-      }
-    }
-    uint16_t* const slot = ring + (i % RING) * L::DSLOT;
-#pragma unroll
-    for (int u = 0; u < NDC; ++u) {
-      uint16_t* const dst = d_lds[u] < 0 ? lds + L::DDUMMY : slot + d_lds[u];
-      *reinterpret_cast<uint4*>(dst) = p.dv[u];
-    }
+    for (int u = 0; u < T::NDC; ++u) *reinterpret_cast<uint4*>(dl[u] >= 0 ? db + dl[u] : dummy) = p.dv[u];
   };
 
-  // Zero the grad_output ring (planes before the first and past the last are zero).
-  for (int e = threadIdx.x; e < RING * L::DSLOT / 8; e += kThreads) {
-    reinterpret_cast<uint4*>(ring)[e] = make_uint4(0u, 0u, 0u, 0u);
-  }
-  __syncthreads();
+  // This wave: unit u0 (32 columns), row block j0 of the workgroup.
+  const int u0 = wave % NU, j0 = wave / NU;
+  const int a_row = (j0 * RB + n16) * T::XPITCH + 8 + 32 * u0 + 8 * q;  // x row j0*RB + n16 (tile row = x row - r0 + P)
+  const bool b_ok = n16 < RB;
+  const int b_row = (j0 * RB + (b_ok ? n16 : 0)) * T::DPITCH + 32 * u0 + 8 * q;
 
-  // Per-lane operand geometry and the constant rows of A.
-  int a_off[MB];
-  bool a_ok[MB];
-  uint4 av[MB];
+  f32x4_t acc[K][K];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int m = 16 * mb + n16;
-    a_ok[mb] = m < K2;
-    const int kh = a_ok[mb] ? m / K : 0;
-    const int kw = a_ok[mb] ? m - kh * K : 0;
-    a_off[mb] = kw * L::XCOPY + (wave * ROWS_PER_WAVE + kh) * L::XROW + 8 * q;
-    const uint32_t fill = m == K2 ? 0x3F803F80u : 0u;  // bf16 ones for the bias row
-    av[mb] = make_uint4(fill, fill, fill, fill);
-  }
-  const bool b_ok = n16 < K;
-  const int b_off = wave * ROWS_PER_WAVE * TW + 8 * q;
-  uint4 bv = make_uint4(0u, 0u, 0u, 0u);
+  for (int a = 0; a < K; ++a)
+#pragma unroll
+    for (int b = 0; b < K; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  uint4 ring[K];  // ring[kd] = dy fragment of plane t - kd + P
+#pragma unroll
+  for (int kd = 0; kd < K; ++kd) ring[kd] = make_uint4(0u, 0u, 0u, 0u);
+  float dbias = 0.f;
 
   Pre pre[PD];
   {
@@ -426,83 +396,89 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
   for (int j = 1; j <= PD; ++j) load(j, pre[(j - 1) % PD]);
   __syncthreads();
 
-  f32x4_t acc[UPR][MB];
+  for (int s0 = 0; s0 < nsteps; s0 += PD) {
 #pragma unroll
-  for (int u = 0; u < UPR; ++u)
+    for (int jj = 0; jj < PD; ++jj) {
+      const int st = s0 + jj;
+      if (st >= nsteps) break;
+      load(st + PD, pre[(jj + PD - 1) % PD]);
+      const uint16_t* const xb = lds + (st & 1) * T::XBUF;
+      const uint16_t* const db = dlds + (st & 1) * T::DBUF;
+      uint4 bnew = make_uint4(0u, 0u, 0u, 0u);
+      if (b_ok) bnew = lds_read16(db + b_row);
+      const uint4 xm = lds_read16(xb + a_row);
+      const uint32_t xp = *reinterpret_cast<const uint32_t*>(xb + a_row - 2);
+      const uint32_t xn = *reinterpret_cast<const uint32_t*>(xb + a_row + 8);
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[u][mb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  for (int i0 = 0; i0 < nplanes; i0 += PD) {
+      for (int kd = K - 1; kd > 0; --kd) ring[kd] = ring[kd - 1];
+      ring[0] = bnew;
+      dbias += (bf16_lo(bnew.x) + bf16_hi(bnew.x)) + (bf16_lo(bnew.y) + bf16_hi(bnew.y)) +
+               (bf16_lo(bnew.z) + bf16_hi(bnew.z)) + (bf16_lo(bnew.w) + bf16_hi(bnew.w));
+      // Words of x[col-2 .. col+9]; shift sh = kw - P selects x[col+sh .. col+sh+7].
+      const uint32_t e[6] = {xp, xm.x, xm.y, xm.z, xm.w, xn};
 #pragma unroll
-    for (int s = 0; s < PD; ++s) {
-      const int i = i0 + s;
-      if (i >= nplanes) break;
-      load(i + PD, pre[(s + PD - 1) % PD]);
-      const uint16_t* const xb = lds + (i & 1) * L::XBUF;
-      // Lane n reads grad_output plane i - n; slots of planes < 0 hold zeros.
-      const int o = i - n16;
-      const uint16_t* const bslot = ring + ((o % RING + RING) % RING) * L::DSLOT + b_off;
-#pragma unroll
-      for (int rr = 0; rr < ROWS_PER_WAVE; ++rr) {
-        // Operands of the row's UPR units first, then UPR independent MFMA
-        // chains (one accumulator set per unit).
-        uint4 bvs[UPR];
-        uint4 avs[UPR][MB];
-#pragma unroll
-        for (int u = 0; u < UPR; ++u) {
-          bvs[u] = bv;
-          if (b_ok) bvs[u] = lds_read16(bslot + rr * TW + 32 * u);
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) {
-            avs[u][mb] = av[mb];
-            if (a_ok[mb]) avs[u][mb] = lds_read16(xb + a_off[mb] + rr * L::XROW + 32 * u);
-          }
+      for (int kw = 0; kw < K; ++kw) {
+        const int sh = kw - P;
+        uint4 av;
+        if (sh % 2 == 0) {
+          const int b = 1 + sh / 2;
+          av = make_uint4(e[b], e[b + 1], e[b + 2], e[b + 3]);
+        } else {
+          const int b = sh < 0 ? 0 : 1;  // |sh| == 1
+          av = make_uint4(__builtin_amdgcn_alignbit(e[b + 1], e[b], 16),
+                          __builtin_amdgcn_alignbit(e[b + 2], e[b + 1], 16),
+                          __builtin_amdgcn_alignbit(e[b + 3], e[b + 2], 16),
+                          __builtin_amdgcn_alignbit(e[b + 4], e[b + 3], 16));
         }
 #pragma unroll
-        for (int u = 0; u < UPR; ++u)
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-            acc[u][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                __builtin_bit_cast(bf16x8_t, avs[u][mb]), __builtin_bit_cast(bf16x8_t, bvs[u]),
-                acc[u][mb], 0, 0, 0);
+        for (int kd = 0; kd < K; ++kd) acc[kw][kd] = mfma16x16x32(av, ring[kd], acc[kw][kd]);
       }
-      store(i + 1, pre[s % PD]);
+      store(st + 1, pre[jj % PD]);
       __syncthreads();
     }
   }
 
-  // Reduce the four waves' tiles in a fixed order. Tap t = kd*k^2 + m sits at
-  // C[m][kd]; the bias gradient at C[k^2][0].
-  float* red = reinterpret_cast<float*>(smem_raw);  // reuse LDS: [4][MB][256]
+  // Diagonal sums through LDS, TILES_PER_ROUND accumulator tiles per round.
+  // Tile (kw, kd) of wave w: red[(w * TILES + tile) * 256 + i * 16 + j] = C[i][j];
+  // tap (kd, kh, kw) = sum_{j < RB} C[j + kh][j].
+  const int64_t rb = static_cast<int64_t>(rbg) * T::NRB + j0;
+  const int64_t cu = static_cast<int64_t>(cg) * NU + u0;
+  const int64_t split = ((n * g.nDc + dc) * g.nRB + rb) * g.nCU + cu;
+  float* const out = partial + static_cast<int64_t>(c) * (K3 + 1) * splits;
+  float* const red = reinterpret_cast<float*>(smem_raw);
+  constexpr int TPR = T::TILES_PER_ROUND;
+  const float dbt = wave_sum(dbias);
+  if (lane == 0) out[static_cast<int64_t>(K3) * splits + split] = dbt;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    f32x4_t sum = acc[0][mb];
+  for (int base = 0; base < K2; base += TPR) {
 #pragma unroll
-    for (int u = 1; u < UPR; ++u) sum += acc[u][mb];
+    for (int tt = 0; tt < TPR; ++tt) {
+      const int tile = base + tt;
+      if (tile < K2) {
+        const int kw = tile / K, kd = tile % K;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[(wave * MB + mb) * 256 + (4 * q + r) * 16 + n16] = sum[r];
-  }
-  __syncthreads();
-  const int64_t split =
-      ((static_cast<int64_t>(bp.n) * g.nDc + bp.dc) * g.nHt + bp.ht) * g.nWt + bp.wt;
-  for (int t = threadIdx.x; t < K3 + 1; t += kThreads) {
-    int m, kd;
-    if (t < K3) {
-      kd = t / K2;
-      m = t - kd * K2;
-    } else {
-      kd = 0;
-      m = K2;
+        for (int r = 0; r < 4; ++r) red[(wave * TPR + tt) * 256 + (4 * q + r) * 16 + n16] = acc[kw][kd][r];
+      }
     }
-    const int mb = m >> 4;
-    const int idx = (m & 15) * 16 + kd;
-    const float v = red[(0 * MB + mb) * 256 + idx] + red[(1 * MB + mb) * 256 + idx] +
-                    red[(2 * MB + mb) * 256 + idx] + red[(3 * MB + mb) * 256 + idx];
-    partial[(static_cast<int64_t>(bp.c) * (K3 + 1) + t) * splits + split] = v;
+    __syncthreads();
+    // One thread per (wave, tile, kh) sums RB diagonal entries in order.
+    for (int e = threadIdx.x; e < 4 * TPR * K; e += kThreads) {
+      const int w = e / (TPR * K), rem = e % (TPR * K), tt = rem / K, kh = rem % K;
+      const int tile = base + tt;
+      if (tile < K2) {
+        const int kw = tile / K, kd = tile % K;
+        const float* tp = red + (w * TPR + tt) * 256;
+        float v = 0.f;
+        for (int j = 0; j < RB; ++j) v += tp[(j + kh) * 16 + j];
+        const int64_t wrb = static_cast<int64_t>(rbg) * T::NRB + w / NU;
+        const int64_t wcu = static_cast<int64_t>(cg) * NU + w % NU;
+        const int64_t wsplit = ((n * g.nDc + dc) * g.nRB + wrb) * g.nCU + wcu;
+        out[static_cast<int64_t>(kd * K2 + kh * K + kw) * splits + wsplit] = v;
+      }
+    }
+    __syncthreads();
   }
 }
-
-// ------------------------------------------------------------------ host side
 
 int make_geom(int64_t c, int64_t d, int64_t h, int64_t w, int tile_cols, int depth_chunk,
               MGeom* g) {
@@ -552,41 +528,41 @@ int launch_stencil_ct(const void* x, const void* wt, const void* bias, void* y, 
 }
 
 
-template <int K, int CT, int RT>
-size_t wgrad_lds_bytes() {
-  constexpr int MB = (K * K + 1 + 15) / 16;
-  constexpr size_t red = static_cast<size_t>(4 * MB * 256) * 4;
-  return WgradLayout<K, CT, RT>::bytes > red ? WgradLayout<K, CT, RT>::bytes : red;
-}
-
-template <int K, int CT>
-int launch_wgrad(const void* x, const void* dy, float* partial, const MGeom& g, int64_t blocks,
-                 int splits, hipStream_t st) {
+template <int K, int NU>
+int launch_wgrad(const void* x, const void* dy, float* partial, const WGeom& g, int64_t blocks, int splits,
+                 hipStream_t st) {
   constexpr int PD = 2;
-  constexpr int RT = 1;
-  const size_t lds = wgrad_lds_bytes<K, CT, RT>();
-  hipLaunchKernelGGL((dw_mfma_wgrad_kernel<K, CT, RT, PD>), dim3(static_cast<unsigned>(blocks)),
-                     dim3(kThreads), lds, st, static_cast<const bf16_t*>(x),
-                     static_cast<const bf16_t*>(dy), partial, g, splits);
+  const size_t lds = WgradTile<K, NU>::BYTES;
+  hipLaunchKernelGGL((dw_mfma_wgrad_kernel<K, NU, PD>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds,
+                     st, static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(dy), partial, g, splits);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }
 
-// Weight-gradient workgroups cover 16 full rows (16 * RT with RT = 1).
-constexpr int kWgradRows = 16;
-
 int plan_wgrad(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int tile_cols,
-               int depth_chunk, MGeom* g, int64_t* blocks, int* splits) {
+               int depth_chunk, WGeom* g, int64_t* blocks, int* splits) {
   MEDNEXT_CHECK_ARG(dw_mfma_supported(d, h, w, k) && w % 32 == 0,
                     "MFMA wgrad needs k in {3,5}, W % 32 == 0, H >= 32 and a slab < 2 GiB");
   MEDNEXT_CHECK_ARG(tile_cols == 32 || tile_cols == 64 || tile_cols == 128,
-                    "MFMA wgrad tile_w must be 32, 64 or 128");
-  int st = make_geom(c, d, h, w, tile_cols, depth_chunk, g);
-  if (st != MEDNEXT_STATUS_OK) return st;
-  g->nHt = static_cast<int>(cdiv(h, kWgradRows));
-  *blocks = n * c * g->nDc * g->nHt * g->nWt;
-  MEDNEXT_CHECK_ARG(*blocks < (int64_t(1) << 31), "grid too large");
-  *splits = static_cast<int>(n * g->nDc * g->nHt * g->nWt);
+                    "MFMA wgrad tile_w (columns per workgroup) must be 32, 64 or 128");
+  MEDNEXT_CHECK_ARG(depth_chunk >= 1, "depth_chunk must be >= 1");
+  const int nu = tile_cols / 32;
+  const int rb = 16 - 2 * (k / 2);
+  g->C = static_cast<int>(c);
+  g->D = static_cast<int>(d);
+  g->H = static_cast<int>(h);
+  g->W = static_cast<int>(w);
+  g->TD = static_cast<int>(depth_chunk < d ? depth_chunk : d);
+  g->nDc = static_cast<int>(cdiv(d, g->TD));
+  g->nRBG = static_cast<int>(cdiv(h, static_cast<int64_t>(rb) * (4 / nu)));
+  g->nCG = static_cast<int>(cdiv(w, tile_cols));
+  g->nRB = g->nRBG * (4 / nu);
+  g->nCU = g->nCG * nu;
+  const int64_t per_channel = static_cast<int64_t>(g->nDc) * g->nRBG * g->nCG;
+  *blocks = n * c * per_channel;
+  const int64_t sp = n * static_cast<int64_t>(g->nDc) * g->nRB * g->nCU;
+  MEDNEXT_CHECK_ARG(*blocks < (int64_t(1) << 31) && sp < (int64_t(1) << 31), "grid too large");
+  *splits = static_cast<int>(sp);
   return MEDNEXT_STATUS_OK;
 }
 
@@ -621,33 +597,31 @@ int dw_mfma_stencil(const void* x, const void* weight, const void* bias, void* y
 
 int dw_mfma_wgrad_splits(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k,
                          int tile_cols, int depth_chunk) {
-  MGeom g{};
+  WGeom g{};
   int64_t blocks = 0;
   int splits = 0;
-  if (plan_wgrad(n, c, d, h, w, k, tile_cols, depth_chunk, &g, &blocks, &splits) !=
-      MEDNEXT_STATUS_OK)
-    return 0;
+  if (plan_wgrad(n, c, d, h, w, k, tile_cols, depth_chunk, &g, &blocks, &splits) != MEDNEXT_STATUS_OK) return 0;
   return splits;
 }
 
 int dw_mfma_wgrad(const void* x, const void* dy, float* partial, int64_t n, int64_t c, int64_t d,
                   int64_t h, int64_t w, int k, int tile_cols, int depth_chunk, hipStream_t st) {
-  MGeom g{};
+  WGeom g{};
   int64_t blocks = 0;
   int splits = 0;
-  int status = plan_wgrad(n, c, d, h, w, k, tile_cols, depth_chunk, &g, &blocks, &splits);
+  const int status = plan_wgrad(n, c, d, h, w, k, tile_cols, depth_chunk, &g, &blocks, &splits);
   if (status != MEDNEXT_STATUS_OK) return status;
   if (k == 3) {
     switch (tile_cols) {
-      case 32: return launch_wgrad<3, 2>(x, dy, partial, g, blocks, splits, st);
-      case 64: return launch_wgrad<3, 4>(x, dy, partial, g, blocks, splits, st);
-      default: return launch_wgrad<3, 8>(x, dy, partial, g, blocks, splits, st);
+      case 32: return launch_wgrad<3, 1>(x, dy, partial, g, blocks, splits, st);
+      case 64: return launch_wgrad<3, 2>(x, dy, partial, g, blocks, splits, st);
+      default: return launch_wgrad<3, 4>(x, dy, partial, g, blocks, splits, st);
     }
   }
   switch (tile_cols) {
-    case 32: return launch_wgrad<5, 2>(x, dy, partial, g, blocks, splits, st);
-    case 64: return launch_wgrad<5, 4>(x, dy, partial, g, blocks, splits, st);
-    default: return launch_wgrad<5, 8>(x, dy, partial, g, blocks, splits, st);
+    case 32: return launch_wgrad<5, 1>(x, dy, partial, g, blocks, splits, st);
+    case 64: return launch_wgrad<5, 2>(x, dy, partial, g, blocks, splits, st);
+    default: return launch_wgrad<5, 4>(x, dy, partial, g, blocks, splits, st);
   }
 }
 

@@ -360,20 +360,35 @@ __global__ __launch_bounds__(kPwThreads) void pw_wgrad_kernel(const bf16_t* __re
   }
 }
 
-// dW / dB = fixed-order fp64 sum of the per-split partials.
-__global__ void pw_wgrad_finish_kernel(const float* __restrict__ partial, bf16_t* __restrict__ dw,
-                                       bf16_t* __restrict__ db, int64_t mk, int64_t m, int64_t slots,
-                                       int64_t stride) {
-  const int64_t e = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x;
-  if (e >= mk + m) return;
-  if (e >= mk && db == nullptr) return;
+// dW / dB = fixed-order fp64 sum of the per-split partials. A block reduces
+// kFinOut outputs; its kFinGroups thread groups each sum every kFinGroups-th
+// slot, and the group sums are added in group order.
+constexpr int kFinOut = 32;
+constexpr int kFinGroups = 8;
+
+__global__ __launch_bounds__(kFinOut* kFinGroups) void pw_wgrad_finish_kernel(
+    const float* __restrict__ partial, bf16_t* __restrict__ dw, bf16_t* __restrict__ db, int64_t mk, int64_t m,
+    int64_t slots, int64_t stride) {
+  __shared__ double part[kFinGroups][kFinOut];
+  const int lo = threadIdx.x % kFinOut, grp = threadIdx.x / kFinOut;
+  const int64_t e = blockIdx.x * static_cast<int64_t>(kFinOut) + lo;
+  const bool live = e < mk + m && (e < mk || db != nullptr);
   double s = 0.0;
-  for (int64_t t = 0; t < slots; ++t) s += partial[t * stride + e];
-  const uint16_t v = f32_to_bf16(static_cast<float>(s));
-  if (e < mk) {
-    dw[e].bits = v;
-  } else {
-    db[e - mk].bits = v;
+  if (live) {
+    for (int64_t t = grp; t < slots; t += kFinGroups) s += partial[t * stride + e];
+  }
+  part[grp][lo] = s;
+  __syncthreads();
+  if (grp == 0 && live) {
+    double total = 0.0;
+#pragma unroll
+    for (int g = 0; g < kFinGroups; ++g) total += part[g][lo];
+    const uint16_t v = f32_to_bf16(static_cast<float>(total));
+    if (e < mk) {
+      dw[e].bits = v;
+    } else {
+      db[e - mk].bits = v;
+    }
   }
 }
 
@@ -491,7 +506,8 @@ extern "C" int32_t mednext_pointwise_wgrad(const void* grad_output, const void* 
   }
   MEDNEXT_CHECK_LAUNCH();
   const int64_t total = m * k + m;
-  hipLaunchKernelGGL(pw_wgrad_finish_kernel, dim3(static_cast<unsigned>(cdiv(total, 256))), dim3(256), 0, s,
+  hipLaunchKernelGGL(pw_wgrad_finish_kernel, dim3(static_cast<unsigned>(cdiv(total, kFinOut))),
+                     dim3(kFinOut * kFinGroups), 0, s,
                      part, static_cast<bf16_t*>(grad_weight), static_cast<bf16_t*>(grad_bias), m * k, m,
                      n * g.splits, g.stride);
   MEDNEXT_CHECK_LAUNCH();

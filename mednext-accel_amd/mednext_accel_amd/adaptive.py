@@ -105,8 +105,24 @@ def _effective_dtype(x: Tensor) -> torch.dtype:
     return x.dtype
 
 
+_CONTEXTS: dict[tuple, ExecutionContext] = {}
+
+
 def _context_from_tensor(x: Tensor, model_context: ModelOptimizationContext, *, training: bool) -> ExecutionContext:
     export = torch.jit.is_tracing() or torch.onnx.is_in_onnx_export()
+    if not export and not torch.compiler.is_compiling():
+        # Contexts are immutable and depend only on these facts: build each once.
+        key = (model_context, tuple(x.shape), x.dtype, x.device, _effective_dtype(x), training)
+        hit = _CONTEXTS.get(key)
+        if hit is None:
+            hit = _build_context(x, model_context, training=training, export=False)
+            if len(_CONTEXTS) < 65536:
+                _CONTEXTS[key] = hit
+        return hit
+    return _build_context(x, model_context, training=training, export=export)
+
+
+def _build_context(x: Tensor, model_context: ModelOptimizationContext, *, training: bool, export: bool) -> ExecutionContext:
     sm, vram, arch = None, 0, None
     if x.device.type == "cuda" and not export:
         sm, vram, arch = device_facts(x.device.index if x.device.index is not None else torch.cuda.current_device())

@@ -109,6 +109,10 @@ class PolicyResolver:
         self.external = external
         self.registry = registry or default_implementation_registry()
         self._warned: set[str] = set()
+        # Decisions are pure functions of (descriptor, context, phase) for a
+        # fixed set of layers, so they are memoised: wrappers resolve on every
+        # forward and this keeps that off the step's critical path.
+        self._memo: dict[tuple[OperatorDescriptor, ExecutionContext, str], PolicyDecision] = {}
 
     def __deepcopy__(self, memo):
         # Policies are immutable; copies of a wrapped model share the resolver
@@ -149,6 +153,19 @@ class PolicyResolver:
         return self.warn_for_target("nvidia" if sm is not None else None, sm)
 
     def resolve(self, descriptor: OperatorDescriptor, context: ExecutionContext, phase: str) -> PolicyDecision:
+        if torch.compiler.is_compiling():
+            # Traced once into the graph; the memo is for eager calls.
+            return self._resolve(descriptor, context, phase)
+        key = (descriptor, context, phase)
+        hit = self._memo.get(key)
+        if hit is not None:
+            return hit
+        decision = self._resolve(descriptor, context, phase)
+        if len(self._memo) < 65536:
+            self._memo[key] = decision
+        return decision
+
+    def _resolve(self, descriptor: OperatorDescriptor, context: ExecutionContext, phase: str) -> PolicyDecision:
         if context.vendor is None:
             return PolicyDecision(
                 descriptor, phase, "reference", {}, "reference", "context-guard", "guard",

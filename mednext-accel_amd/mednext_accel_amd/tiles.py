@@ -108,17 +108,23 @@ def _depth_chunk(d: int, slabs: int, kernel_size: int, target: int = TARGET_WORK
 # Workgroups a matrix-core depthwise launch aims for, per (phase kind, k). The
 # forward / input-grad kernel holds two 16x(tile_w) accumulator rows per wave and
 # runs at 2 workgroups per CU (k=3) or 1 (k=5, larger LDS halo), so it wants
-# long D-runs and ~1-2 workgroups per CU; the weight-grad kernel is lighter and
-# prefers ~4 per CU. Measured on MI355X at the MedNeXt stage shapes
-# (C32 128^3, C64 64^3, C128 32^3; k=3 and 5): these targets reproduce the best
-# depth_chunk of a sweep over {4..64} within run-to-run noise.
+# long D-runs and ~1-2 workgroups per CU. The weight-grad kernel (4 waves of
+# 16 - (k-1) grad_output rows x 32 columns each) wants ~2-2.5 per CU. Measured
+# on MI355X at the MedNeXt stage shapes (C32 128^3, C64 64^3, C128 32^3; k=3
+# and 5): these targets reproduce the best depth_chunk of a sweep over
+# {8..64} within run-to-run noise.
 MFMA_TARGET_WORKGROUPS = {
     ("stencil", 3): 2 * CU_COUNT,
     ("stencil", 5): CU_COUNT,
-    ("weight_grad", 3): 4 * CU_COUNT,
+    ("weight_grad", 3): 5 * CU_COUNT // 2,
     ("weight_grad", 5): 2 * CU_COUNT,
 }
-MFMA_WGRAD_ROWS = 16
+
+
+def mfma_wgrad_rows(kernel_size: int, tile_w: int) -> int:
+    """grad_output rows per weight-grad workgroup: 4 / (tile_w / 32) waves
+    stacked vertically, each covering 16 - (k - 1) rows."""
+    return (16 - (kernel_size - 1)) * (4 // (tile_w // 32))
 
 
 def depthwise_recipe(
@@ -131,10 +137,10 @@ def depthwise_recipe(
 ) -> list[int]:
     """Default ``[engine, tile_w, depth_chunk]`` for one depthwise phase on gfx950.
 
-    bf16 shapes the matrix-core kernels take use them. Forward / input-grad:
-    ``tile_w = min(128, W)`` columns x 32 rows per workgroup. Weight-grad: full
-    rows of 64 columns (k=3) or up to 128 (k=5) x 16 rows. The D-run per
-    workgroup is the longest that still yields ``MFMA_TARGET_WORKGROUPS``.
+    bf16 shapes the matrix-core kernels take use them, with ``tile_w = min(128,
+    W)`` columns per workgroup: forward / input-grad tiles are 32 rows high,
+    weight-grad tiles ``mfma_wgrad_rows(k, tile_w)``. The D-run per workgroup is
+    the longest that still yields ``MFMA_TARGET_WORKGROUPS``.
     Everything else runs the VALU stencil with the widest tile the plane allows
     (up to 64 columns) and a D-run that yields TARGET_WORKGROUPS workgroups. In
     both cases at least 4 planes (2(k-1) for k=5) per workgroup, so re-read
@@ -144,14 +150,13 @@ def depthwise_recipe(
         raise ValueError(f"phase must be one of {PHASES}")
     d, h, w = spatial
     if dtype == "bfloat16" and mfma_supported(spatial, kernel_size, phase):
-        if phase == "weight_grad":
-            cap = 64 if kernel_size == 3 else 128
-            rows, kind = MFMA_WGRAD_ROWS, "weight_grad"
-        else:
-            cap, rows, kind = 128, MFMA_TILE_ROWS, "stencil"
         tile_w = 32
-        while tile_w < cap and tile_w * 2 <= w:
+        while tile_w < 128 and tile_w * 2 <= w:
             tile_w *= 2
+        if phase == "weight_grad":
+            rows, kind = mfma_wgrad_rows(kernel_size, tile_w), "weight_grad"
+        else:
+            rows, kind = MFMA_TILE_ROWS, "stencil"
         slabs = batch * channels * _cdiv(h, rows) * _cdiv(w, tile_w)
         target = MFMA_TARGET_WORKGROUPS[(kind, kernel_size)]
         return [ENGINE_MFMA, tile_w, _depth_chunk(d, slabs, kernel_size, target)]
@@ -203,9 +208,10 @@ def pointwise_blocks(batch: int, k: int, m: int, voxels: int) -> int:
 
 
 def pointwise_wgrad_splits(batch: int, k: int, m: int, voxels: int) -> int:
-    """V-splits per sample for pw_wgrad_kernel: ~4 workgroups per CU over the
-    grid, each wave doing at least four 32-voxel steps."""
+    """V-splits per sample for pw_wgrad_kernel: ~2 workgroups per CU over the
+    grid (the kernel keeps 3 resident), each wave doing at least four 32-voxel
+    steps. Fewer splits also keep the fixed-order finish pass small."""
     steps = _cdiv(voxels, PW_WG_STEP)
     tiles = max(1, batch * _cdiv(m, PW_WG_TILE) * _cdiv(k, PW_WG_TILE))
-    wanted = _cdiv(TARGET_WORKGROUPS, tiles)
+    wanted = _cdiv(2 * CU_COUNT, tiles)
     return max(1, min(wanted, _cdiv(steps, 4 * 4), 65535))

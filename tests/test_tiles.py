@@ -20,7 +20,7 @@ def test_depthwise_recipe_invariants(channels, size, k, dtype, phase):
     if engine == tiles.ENGINE_MFMA:
         assert dtype == "bfloat16" and tiles.mfma_supported((size,) * 3, k, phase)
         assert tile_w in (32, 64, 128) and tile_w <= max(32, size)
-        rows = tiles.MFMA_WGRAD_ROWS if phase == "weight_grad" else tiles.MFMA_TILE_ROWS
+        rows = tiles.mfma_wgrad_rows(k, tile_w) if phase == "weight_grad" else tiles.MFMA_TILE_ROWS
         wgs = channels * -(-size // rows) * -(-size // tile_w) * -(-size // depth_chunk)
         kind = "weight_grad" if phase == "weight_grad" else "stencil"
         target = tiles.MFMA_TARGET_WORKGROUPS[(kind, k)]
@@ -58,6 +58,8 @@ def test_mfma_stage0_recipes_match_measured_best():
     """C32 128^3 bf16 (the headline shape): the sweep-best launch shapes."""
     r = tiles.depthwise_recipe
     assert r(1, 32, (128,) * 3, 3, "bfloat16", "forward") == [tiles.ENGINE_MFMA, 128, 32]
-    assert r(1, 32, (128,) * 3, 3, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 64, 64]
+    assert r(1, 32, (128,) * 3, 3, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 128, 64]
+    assert r(1, 32, (128,) * 3, 5, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 128, 64]
+    assert r(1, 64, (64,) * 3, 3, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 64, 16]
     assert r(1, 32, (128,) * 3, 5, "bfloat16", "forward") == [tiles.ENGINE_MFMA, 128, 64]
     assert r(1, 64, (64,) * 3, 3, "bfloat16", "input_grad") == [tiles.ENGINE_MFMA, 64, 16]
