@@ -17,8 +17,10 @@
 // Memory pipeline. Input planes are double-buffered in LDS; the global loads
 // for plane i + PD are issued (into one of PD register sets) before plane i's
 // MFMAs, so PD planes per workgroup are in flight while the matrix cores run.
-// The compiler waits only for the set being stored. PD divides k so every
-// register-set index is static under the k-fold unroll.
+// The compiler waits only for the set being stored. The plane loop is
+// unrolled by lcm(k, PD), so every register-set and accumulator index is
+// static. For k = 3 finished output planes leave through an LDS staging tile
+// as whole rows (16-byte stores).
 //
 // Buffer helpers and the MFMA lane layout: cdna4.h.
 #include "cdna4.h"
@@ -30,6 +32,10 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRT = 2;  // 16-row tiles per workgroup plane (32 rows)
+
+constexpr bool stencil_stages_output(int k) { return k == 3; }
+constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
+constexpr int lcm_int(int a, int b) { return a / gcd_int(a, b) * b; }
 
 struct MGeom {
   int C, D, H, W;
@@ -76,7 +82,20 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   constexpr int NCHUNK = LR * CPR;
   constexpr int NCH = (NCHUNK + kThreads - 1) / kThreads;
   constexpr int TPW = kRT * CT / 4;  // tiles per wave
-  static_assert(K % PD == 0, "prefetch depth must divide k");
+  // k = 3: finished output planes are staged through LDS and written as whole
+  // rows, 16 bytes per lane (an MFMA tile row holds only 4 consecutive
+  // outputs per lane, i.e. 16 rows x 32-byte pieces per store instruction).
+  // k = 5 keeps the direct 8-byte stores: its LDS and register footprint
+  // already bound occupancy, and measured faster that way.
+  constexpr bool STAGE = stencil_stages_output(K);
+  constexpr int OC = TW + 8;           // output staging row pitch (elements)
+  constexpr int OBUF = TH * OC;
+  constexpr int OCH = TH * (TW / 8);   // 16-byte output chunks per plane
+  constexpr int NOC = (OCH + kThreads - 1) / kThreads;
+  // The plane loop is unrolled by U = lcm(K, PD) so that both the rotating
+  // accumulator slot (plane mod K) and the prefetch register set (plane mod
+  // PD) are compile-time indices.
+  constexpr int U = lcm_int(K, PD);
   extern __shared__ __align__(16) unsigned char smem_raw[];
   uint16_t* lds = reinterpret_cast<uint16_t*>(smem_raw);
 
@@ -166,9 +185,9 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   for (int j = 1; j <= PD; ++j) load_plane(j, pre[(j - 1) % PD]);
   __syncthreads();
 
-  for (int q0 = 0; q0 < nplanes; q0 += K) {
+  for (int q0 = 0; q0 < nplanes; q0 += U) {
 #pragma unroll
-    for (int s = 0; s < K; ++s) {
+    for (int s = 0; s < U; ++s) {
       const int i = q0 + s;
       if (i >= nplanes) break;
       load_plane(i + PD, pre[(s + PD - 1) % PD]);
@@ -177,6 +196,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
       const int cs = (s + 1) % K;
       const bool write_o = o >= 0 && o < g.TD && d0 + o < g.D;
       const uint32_t obase = static_cast<uint32_t>(write_o ? d0 + o : 0) * static_cast<uint32_t>(plane * 2);
+      uint16_t* const obuf = lds + 2 * LR * LC + 8 + (i & 1) * OBUF;
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int tile = wave + 4 * t;
@@ -194,20 +214,40 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
           }
         }
         {
-          const int h = th0 + 16 * ty + n16;
-          const int w = tw0 + 16 * tx + 4 * q;
-          const bool ok = write_o && h < g.H && w < g.W;
-          const uint32_t off = ok ? obase + static_cast<uint32_t>(2 * (h * g.W + w)) : kOob;
           const f32x4_t a = acc[cs][t];
           const bf16x4_t packed = {static_cast<__bf16>(a[0] + b0), static_cast<__bf16>(a[1] + b0),
                                    static_cast<__bf16>(a[2] + b0), static_cast<__bf16>(a[3] + b0)};
-          const u32x2_t words = __builtin_bit_cast(u32x2_t, packed);
-          buf_store8(yr, off, words[0], words[1]);
+          if constexpr (STAGE) {
+            *reinterpret_cast<bf16x4_t*>(obuf + (16 * ty + n16) * OC + 16 * tx + 4 * q) = packed;
+          } else {
+            const int h = th0 + 16 * ty + n16;
+            const int w = tw0 + 16 * tx + 4 * q;
+            const bool ok = write_o && h < g.H && w < g.W;
+            const uint32_t off = ok ? obase + static_cast<uint32_t>(2 * (h * g.W + w)) : kOob;
+            const u32x2_t words = __builtin_bit_cast(u32x2_t, packed);
+            buf_store8(yr, off, words[0], words[1]);
+          }
         }
         acc[cs][t] = acc_init;
       }
       store_plane(lds + ((i + 1) & 1) * LR * LC, pre[s % PD]);
       __syncthreads();
+      if constexpr (STAGE) {
+        // Row-contiguous store of the plane this step completed. Buffer i & 1
+        // is next written at step i + 2, after the barrier that ends step i + 1.
+        if (write_o) {
+#pragma unroll
+          for (int u = 0; u < NOC; ++u) {
+            const int e = threadIdx.x + u * kThreads;
+            if (e < OCH) {
+              const int r = e / (TW / 8), ch = e - r * (TW / 8);
+              const int h = th0 + r, w = tw0 + 8 * ch;
+              const uint32_t off = (h < g.H && w < g.W) ? obase + static_cast<uint32_t>(2 * (h * g.W + w)) : kOob;
+              buf_store16(yr, off, *reinterpret_cast<const uint4*>(obuf + r * OC + 8 * ch));
+            }
+          }
+        }
+      }
     }
   }
 }
@@ -500,7 +540,8 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
                    int64_t blocks, hipStream_t st) {
   constexpr int P = K / 2;
   // two plane buffers + one dummy 16-byte slot for threads without a fill chunk
-  constexpr size_t lds = (static_cast<size_t>(2) * (16 * kRT + 2 * P) * (16 * CT + 16) + 8) * 2;
+  constexpr size_t stage = stencil_stages_output(K) ? static_cast<size_t>(2) * (16 * kRT) * (16 * CT + 8) : 0;
+  constexpr size_t lds = (static_cast<size_t>(2) * (16 * kRT + 2 * P) * (16 * CT + 16) + 8 + stage) * 2;
   auto px = static_cast<const bf16_t*>(x);
   auto pw = static_cast<const bf16_t*>(wt);
   auto pb = static_cast<const bf16_t*>(bias);
@@ -519,7 +560,7 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
 template <int K, bool FLIP>
 int launch_stencil_ct(const void* x, const void* wt, const void* bias, void* y, const MGeom& g,
                       int tile_cols, int64_t blocks, hipStream_t st) {
-  constexpr int PD = K == 3 ? 3 : 1;
+  constexpr int PD = K == 3 ? 3 : 2;
   switch (tile_cols) {
     case 32: return launch_stencil<K, FLIP, 2, PD>(x, wt, bias, y, g, blocks, st);
     case 64: return launch_stencil<K, FLIP, 4, PD>(x, wt, bias, y, g, blocks, st);

@@ -120,8 +120,14 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise ValueError(f"unsupported dtype {dtype}") from error
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(tensor: torch.Tensor) -> int:
-    """hipStream_t of PyTorch's current stream on the tensor's device."""
+    """hipStream_t of PyTorch's current stream on the tensor's device (the raw
+    query avoids building a Stream object on every launch)."""
+    if _raw_stream is not None:
+        return _raw_stream(tensor.device.index if tensor.device.index is not None else torch.cuda.current_device())
     return torch.cuda.current_stream(tensor.device).cuda_stream
 
 

@@ -17,6 +17,8 @@ launch raises.
 
 from __future__ import annotations
 
+import functools
+
 import torch
 from torch import Tensor
 
@@ -43,6 +45,13 @@ def _check_device(*tensors: Tensor) -> None:
 
 def _check_recipe(recipe) -> tuple[int, int, int]:
     if recipe is None or len(recipe) != 3:
+        raise ValueError("recipe must be [engine, tile_w, depth_chunk]")
+    return _checked_recipe(tuple(int(v) for v in recipe))
+
+
+@functools.lru_cache(maxsize=4096)
+def _checked_recipe(recipe: tuple[int, int, int]) -> tuple[int, int, int]:
+    if len(recipe) != 3:
         raise ValueError("recipe must be [engine, tile_w, depth_chunk]")
     engine, tile_w, depth_chunk = (int(v) for v in recipe)
     if engine == ENGINE_VALU:
@@ -157,9 +166,7 @@ def depthwise_weight_grad(
         return grad_weight.zero_(), grad_bias.zero_()
     code = _hip.dtype_code(x.dtype)
     lib = _hip.load()
-    nbytes = lib.mednext_depthwise3d_wgrad_workspace_bytes(
-        n, c, d, h, w, kernel_size, code, engine, tile_w, depth_chunk
-    )
+    nbytes = _wgrad_workspace_bytes(n, c, d, h, w, kernel_size, code, engine, tile_w, depth_chunk)
     if nbytes == 0:
         raise _hip.HipLibraryError(f"wgrad workspace query failed: {_hip.last_error()}")
     workspace = torch.empty((nbytes,), device=x.device, dtype=torch.uint8)
@@ -172,6 +179,11 @@ def depthwise_weight_grad(
         "mednext_depthwise3d_wgrad",
     )
     return grad_weight, grad_bias
+
+
+@functools.lru_cache(maxsize=4096)
+def _wgrad_workspace_bytes(*args: int) -> int:
+    return int(_hip.load().mednext_depthwise3d_wgrad_workspace_bytes(*args))
 
 
 def _stats_dtype(x: Tensor) -> torch.dtype:

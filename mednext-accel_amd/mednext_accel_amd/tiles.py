@@ -9,6 +9,7 @@ keeping per-workgroup halo overheads small.
 
 from __future__ import annotations
 
+import functools
 from dataclasses import dataclass
 
 CU_COUNT = 256
@@ -89,6 +90,7 @@ MFMA_TILE_ROWS = 32  # two 16-row MFMA tiles per workgroup
 PHASES = ("forward", "input_grad", "weight_grad")
 
 
+@functools.lru_cache(maxsize=4096)
 def mfma_supported(spatial: tuple[int, int, int], kernel_size: int, phase: str) -> bool:
     """Shapes the bf16 matrix-core kernels take (mirrors depthwise_mfma.hip)."""
     d, h, w = spatial
@@ -127,6 +129,7 @@ def mfma_wgrad_rows(kernel_size: int, tile_w: int) -> int:
     return (16 - (kernel_size - 1)) * (4 // (tile_w // 32))
 
 
+@functools.lru_cache(maxsize=4096)
 def depthwise_recipe(
     batch: int,
     channels: int,
@@ -167,6 +170,7 @@ def depthwise_recipe(
     return [ENGINE_VALU, tile_w, _depth_chunk(d, plan.workgroups, kernel_size)]
 
 
+@functools.lru_cache(maxsize=4096)
 def group_norm_splits(batch: int, channels: int, spatial_volume: int) -> int:
     """Chunks per (n, c) row: enough workgroups to fill the chip, >= 4096 elements each."""
     rows = max(1, batch * channels)
@@ -184,6 +188,7 @@ PW_WG_STEP = 32  # voxels per pw_wgrad MFMA step
 PW_WG_TILE = 64
 
 
+@functools.lru_cache(maxsize=4096)
 def pointwise_supported(in_channels: int, out_channels: int, voxels: int) -> bool:
     """Shapes the bf16 matrix-core pointwise kernels take (mirrors pointwise.hip).
 
@@ -196,6 +201,7 @@ def pointwise_supported(in_channels: int, out_channels: int, voxels: int) -> boo
     return fwd and dgrad and voxels % 8 == 0 and small
 
 
+@functools.lru_cache(maxsize=4096)
 def pointwise_blocks(batch: int, k: int, m: int, voxels: int) -> int:
     """Workgroups per (sample, 64-row block) for pw_fwd_kernel: one resident
     workgroup per CU across the grid (the kernel runs one wave per SIMD), each
@@ -207,6 +213,7 @@ def pointwise_blocks(batch: int, k: int, m: int, voxels: int) -> int:
     return max(1, min(wanted, _cdiv(chunks, 4 * 2)))
 
 
+@functools.lru_cache(maxsize=4096)
 def pointwise_wgrad_splits(batch: int, k: int, m: int, voxels: int) -> int:
     """V-splits per sample for pw_wgrad_kernel: ~2 workgroups per CU over the
     grid (the kernel keeps 3 resident), each wave doing at least four 32-voxel
