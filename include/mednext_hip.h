@@ -126,6 +126,40 @@ int32_t mednext_group_norm_bwd(const void* grad_output, int32_t dy_dtype, const 
                                int64_t spatial, int32_t splits, void* workspace,
                                size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------- depthwise s2
+ * Stride-2, padding k/2 depthwise maps between a full-resolution tensor `big`
+ * [N][C][Db][Hb][Wb] and a half-resolution tensor `small` [N][C][Ds][Hs][Ws]
+ * (any sizes; out-of-range taps read zero), k in {1,3,5}, weight [C,1,k,k,k]
+ * and bias [C] in the tensors' dtype, fp32 accumulation (fp64 for fp64):
+ *   gather:  small[o] = bias + sum_t w[t] big[2o + t - k/2]
+ *   scatter: big[i]   = bias + sum_{o,t: 2o + t - k/2 = i} w[t] small[o]
+ *   wgrad:   grad_weight[t] = sum_{n,o} big[2o + t - k/2] small[o],
+ *            grad_bias = sum_{n,o} small[o]
+ * The MedNeXt down block's Conv3d(stride 2) is gather (forward), scatter
+ * (input gradient, bias NULL) and wgrad(big = x, small = grad_output); the up
+ * block's ConvTranspose3d(stride 2), whose output is 2s - 1 per dimension, is
+ * scatter (forward), gather (input gradient) and wgrad(big = grad_output,
+ * small = x) for the weight (its bias gradient is the sum of grad_output).
+ * Replace the reference's F.conv3d / F.conv_transpose3d forwards and their
+ * backward kernels (src/mednext_accel/ops/_triton/depthwise.py:206-268,
+ * :516-546, :654-719 stride-2; :86-156, :722-850 transposed). */
+int32_t mednext_depthwise3d_s2_gather(const void* big, const void* weight, const void* bias,
+                                      void* small_out, int64_t n, int64_t c, int64_t db,
+                                      int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws,
+                                      int32_t kernel_size, int32_t dtype, void* stream);
+int32_t mednext_depthwise3d_s2_scatter(const void* small, const void* weight, const void* bias,
+                                       void* big_out, int64_t n, int64_t c, int64_t db,
+                                       int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws,
+                                       int32_t kernel_size, int32_t dtype, void* stream);
+size_t mednext_depthwise3d_s2_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t db, int64_t hb,
+                                                    int64_t wb, int64_t ds, int64_t hs, int64_t ws,
+                                                    int32_t kernel_size, int32_t dtype);
+int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* grad_weight,
+                                     void* grad_bias, void* workspace, size_t workspace_bytes,
+                                     int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb,
+                                     int64_t ds, int64_t hs, int64_t ws, int32_t kernel_size,
+                                     int32_t dtype, void* stream);
+
 /* ------------------------------------------------------------------ pointwise
  * 1x1x1 convolution as a per-sample GEMM on bf16 matrix cores (fp32
  * accumulate): x [N][K][V], y [N][M][V] (V = D*H*W voxels), weight [M][K]

@@ -557,6 +557,263 @@ int launch_wgrad(const void* x, const void* dy, void* dw, void* db, void* ws, co
   }
 }
 
+
+// ------------------------------------------------------------------ stride 2
+//
+// The MedNeXt down block's depthwise conv (stride 2, padding k/2) and the up
+// block's depthwise transposed conv (stride 2, padding k/2, no output
+// padding) are three index maps between a full-resolution ("big") tensor and
+// a half-resolution ("small") one, per channel and with zero padding:
+//   gather   small[o] = b + sum_t w[t] * big[2o + t - P]        (down forward;
+//                                                                 up input-grad)
+//   scatter  big[i]   = b + sum_{o,t: 2o+t-P = i} w[t] * small[o] (down input-grad;
+//                                                                 up forward)
+//   reduce   dW[t] = sum_o big[2o + t - P] * small[o], dB = sum_o small[o]
+//            (down weight-grad with big = x, small = dy; up weight-grad with
+//            big = dy, small = x)
+// They carry ~k^3/8 FLOP per big element, so they are VALU kernels bound by
+// memory; accumulation is fp32 (fp64 for fp64 tensors).
+struct S2Geom {
+  int64_t total;  // outputs of this launch
+  int C;
+  int Db, Hb, Wb;  // big
+  int Ds, Hs, Ws;  // small
+};
+
+template <typename T, typename Acc, int K, bool BIAS>
+__global__ __launch_bounds__(256) void s2_gather_kernel(const T* __restrict__ big, const T* __restrict__ w,
+                                                        const T* __restrict__ b, T* __restrict__ out, S2Geom g) {
+  constexpr int P = K / 2;
+  const int64_t big_vol = static_cast<int64_t>(g.Db) * g.Hb * g.Wb;
+  for (int64_t idx = blockIdx.x * 256ll + threadIdx.x; idx < g.total; idx += gridDim.x * 256ll) {
+    int64_t r = idx;
+    const int ow = static_cast<int>(r % g.Ws);
+    r /= g.Ws;
+    const int oh = static_cast<int>(r % g.Hs);
+    r /= g.Hs;
+    const int od = static_cast<int>(r % g.Ds);
+    const int64_t nc = r / g.Ds;
+    const int c = static_cast<int>(nc % g.C);
+    const T* bp = big + nc * big_vol;
+    const T* wp = w + static_cast<int64_t>(c) * K * K * K;
+    Acc acc = BIAS ? Cvt<T, Acc>::load(b[c]) : Acc(0);
+#pragma unroll
+    for (int kd = 0; kd < K; ++kd) {
+      const int id = 2 * od + kd - P;
+      if (id < 0 || id >= g.Db) continue;
+#pragma unroll
+      for (int kh = 0; kh < K; ++kh) {
+        const int ih = 2 * oh + kh - P;
+        if (ih < 0 || ih >= g.Hb) continue;
+        const T* row = bp + (static_cast<int64_t>(id) * g.Hb + ih) * g.Wb;
+#pragma unroll
+        for (int kw = 0; kw < K; ++kw) {
+          const int iw = 2 * ow + kw - P;
+          if (iw < 0 || iw >= g.Wb) continue;
+          acc += Cvt<T, Acc>::load(wp[(kd * K + kh) * K + kw]) * Cvt<T, Acc>::load(row[iw]);
+        }
+      }
+    }
+    out[idx] = Cvt<T, Acc>::store(acc);
+  }
+}
+
+template <typename T, typename Acc, int K, bool BIAS>
+__global__ __launch_bounds__(256) void s2_scatter_kernel(const T* __restrict__ small, const T* __restrict__ w,
+                                                         const T* __restrict__ b, T* __restrict__ out, S2Geom g) {
+  constexpr int P = K / 2;
+  const int64_t small_vol = static_cast<int64_t>(g.Ds) * g.Hs * g.Ws;
+  for (int64_t idx = blockIdx.x * 256ll + threadIdx.x; idx < g.total; idx += gridDim.x * 256ll) {
+    int64_t r = idx;
+    const int iw = static_cast<int>(r % g.Wb);
+    r /= g.Wb;
+    const int ih = static_cast<int>(r % g.Hb);
+    r /= g.Hb;
+    const int id = static_cast<int>(r % g.Db);
+    const int64_t nc = r / g.Db;
+    const int c = static_cast<int>(nc % g.C);
+    const T* sp = small + nc * small_vol;
+    const T* wp = w + static_cast<int64_t>(c) * K * K * K;
+    Acc acc = BIAS ? Cvt<T, Acc>::load(b[c]) : Acc(0);
+    // Taps t with 2o + t - P = i: t has the parity of i + P and o = (i + P - t) / 2.
+#pragma unroll
+    for (int kd = 0; kd < K; ++kd) {
+      const int td = id + P - kd;
+      if (td < 0 || (td & 1) || (td >> 1) >= g.Ds) continue;
+#pragma unroll
+      for (int kh = 0; kh < K; ++kh) {
+        const int th = ih + P - kh;
+        if (th < 0 || (th & 1) || (th >> 1) >= g.Hs) continue;
+        const T* row = sp + (static_cast<int64_t>(td >> 1) * g.Hs + (th >> 1)) * g.Ws;
+#pragma unroll
+        for (int kw = 0; kw < K; ++kw) {
+          const int tw = iw + P - kw;
+          if (tw < 0 || (tw & 1) || (tw >> 1) >= g.Ws) continue;
+          acc += Cvt<T, Acc>::load(wp[(kd * K + kh) * K + kw]) * Cvt<T, Acc>::load(row[tw >> 1]);
+        }
+      }
+    }
+    out[idx] = Cvt<T, Acc>::store(acc);
+  }
+}
+
+// One block per (n, c, voxel range of the small tensor); per-block partials
+// [C][K^3 + 1][splits] (split = n * blocks_per_channel + range) for the
+// fixed-order finish kernel.
+template <typename T, typename Acc, int K>
+__global__ __launch_bounds__(256) void s2_wgrad_kernel(const T* __restrict__ big, const T* __restrict__ small,
+                                                       Acc* __restrict__ partial, S2Geom g, int bpc,
+                                                       int64_t per_block, int splits) {
+  constexpr int P = K / 2;
+  constexpr int K3 = K * K * K;
+  __shared__ Acc red[4][K3 + 1];
+  const int64_t nc = blockIdx.x / bpc;
+  const int j = static_cast<int>(blockIdx.x - nc * bpc);
+  const int c = static_cast<int>(nc % g.C);
+  const int64_t n = nc / g.C;
+  const int64_t small_vol = static_cast<int64_t>(g.Ds) * g.Hs * g.Ws;
+  const int64_t big_vol = static_cast<int64_t>(g.Db) * g.Hb * g.Wb;
+  const T* bp = big + nc * big_vol;
+  const T* sp = small + nc * small_vol;
+  const int64_t v0 = j * per_block;
+  const int64_t v1 = v0 + per_block < small_vol ? v0 + per_block : small_vol;
+  Acc acc[K3 + 1];
+#pragma unroll
+  for (int t = 0; t <= K3; ++t) acc[t] = Acc(0);
+  for (int64_t v = v0 + threadIdx.x; v < v1; v += 256) {
+    int64_t r = v;
+    const int ow = static_cast<int>(r % g.Ws);
+    r /= g.Ws;
+    const int oh = static_cast<int>(r % g.Hs);
+    const int od = static_cast<int>(r / g.Hs);
+    const Acc s = Cvt<T, Acc>::load(sp[v]);
+    acc[K3] += s;
+#pragma unroll
+    for (int kd = 0; kd < K; ++kd) {
+      const int id = 2 * od + kd - P;
+      if (id < 0 || id >= g.Db) continue;
+#pragma unroll
+      for (int kh = 0; kh < K; ++kh) {
+        const int ih = 2 * oh + kh - P;
+        if (ih < 0 || ih >= g.Hb) continue;
+        const T* row = bp + (static_cast<int64_t>(id) * g.Hb + ih) * g.Wb;
+#pragma unroll
+        for (int kw = 0; kw < K; ++kw) {
+          const int iw = 2 * ow + kw - P;
+          if (iw < 0 || iw >= g.Wb) continue;
+          acc[(kd * K + kh) * K + kw] += Cvt<T, Acc>::load(row[iw]) * s;
+        }
+      }
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int t = 0; t <= K3; ++t) {
+    const Acc tot = wave_sum(acc[t]);
+    if (lane == 0) red[wave][t] = tot;
+  }
+  __syncthreads();
+  const int64_t split = n * bpc + j;
+  for (int t = threadIdx.x; t <= K3; t += 256) {
+    partial[(static_cast<int64_t>(c) * (K3 + 1) + t) * splits + split] = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+  }
+}
+
+int s2_geom(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k,
+            int dtype, S2Geom* g) {
+  MEDNEXT_CHECK_ARG(dtype_ok(dtype), "unsupported dtype");
+  MEDNEXT_CHECK_ARG(k == 1 || k == 3 || k == 5, "kernel_size must be 1, 3 or 5");
+  MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && db >= 1 && hb >= 1 && wb >= 1 && ds >= 1 && hs >= 1 && ws >= 1,
+                    "shape must be positive");
+  const int64_t lim = int64_t(1) << 31;
+  MEDNEXT_CHECK_ARG(c < lim && db < lim && hb < lim && wb < lim && ds < lim && hs < lim && ws < lim,
+                    "each dimension must fit in int32");
+  MEDNEXT_CHECK_ARG(db * hb < lim && db * hb * wb < (int64_t(1) << 62) / (n * c), "tensor too large");
+  g->C = static_cast<int>(c);
+  g->Db = static_cast<int>(db);
+  g->Hb = static_cast<int>(hb);
+  g->Wb = static_cast<int>(wb);
+  g->Ds = static_cast<int>(ds);
+  g->Hs = static_cast<int>(hs);
+  g->Ws = static_cast<int>(ws);
+  g->total = 0;
+  return MEDNEXT_STATUS_OK;
+}
+
+unsigned s2_blocks(int64_t total) {
+  const int64_t b = cdiv(total, 256);
+  return static_cast<unsigned>(b < 65536 * 16 ? b : 65536 * 16);
+}
+
+template <typename T, int K, bool GATHER>
+int launch_s2_map_k(const void* in, const void* w, const void* b, void* out, S2Geom g, hipStream_t st) {
+  using Acc = typename AccOf<T>::type;
+  const unsigned blocks = s2_blocks(g.total);
+  auto pi = static_cast<const T*>(in);
+  auto pw = static_cast<const T*>(w);
+  auto pb = static_cast<const T*>(b);
+  auto po = static_cast<T*>(out);
+  if (GATHER) {
+    if (b != nullptr)
+      hipLaunchKernelGGL((s2_gather_kernel<T, Acc, K, true>), dim3(blocks), dim3(256), 0, st, pi, pw, pb, po, g);
+    else
+      hipLaunchKernelGGL((s2_gather_kernel<T, Acc, K, false>), dim3(blocks), dim3(256), 0, st, pi, pw, pb, po, g);
+  } else {
+    if (b != nullptr)
+      hipLaunchKernelGGL((s2_scatter_kernel<T, Acc, K, true>), dim3(blocks), dim3(256), 0, st, pi, pw, pb, po, g);
+    else
+      hipLaunchKernelGGL((s2_scatter_kernel<T, Acc, K, false>), dim3(blocks), dim3(256), 0, st, pi, pw, pb, po, g);
+  }
+  MEDNEXT_CHECK_LAUNCH();
+  return MEDNEXT_STATUS_OK;
+}
+
+template <bool GATHER>
+int s2_map_entry(const void* in, const void* w, const void* b, void* out, int64_t n, int64_t c, int64_t db,
+                 int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int32_t k, int32_t dtype, void* stream) {
+  MEDNEXT_CHECK_ARG(in != nullptr && w != nullptr && out != nullptr, "null tensor pointer");
+  S2Geom g;
+  if (int st = s2_geom(n, c, db, hb, wb, ds, hs, ws, k, dtype, &g)) return st;
+  g.total = GATHER ? n * c * ds * hs * ws : n * c * db * hb * wb;
+  auto s = static_cast<hipStream_t>(stream);
+#define MEDNEXT_S2_K(T)                                                          \
+  switch (k) {                                                                   \
+    case 1: return launch_s2_map_k<T, 1, GATHER>(in, w, b, out, g, s);           \
+    case 3: return launch_s2_map_k<T, 3, GATHER>(in, w, b, out, g, s);           \
+    default: return launch_s2_map_k<T, 5, GATHER>(in, w, b, out, g, s);          \
+  }
+  switch (dtype) {
+    case MEDNEXT_DTYPE_F32: MEDNEXT_S2_K(float)
+    case MEDNEXT_DTYPE_F64: MEDNEXT_S2_K(double)
+    case MEDNEXT_DTYPE_F16: MEDNEXT_S2_K(f16_t)
+    default: MEDNEXT_S2_K(bf16_t)
+  }
+#undef MEDNEXT_S2_K
+}
+
+// Blocks per (n, c) for the reduction: ~2048 blocks over the launch, at least
+// 1024 small voxels per block.
+void s2_wgrad_split(int64_t n, int64_t c, int64_t small_vol, int* bpc, int64_t* per_block) {
+  const int64_t want = cdiv(int64_t(2048), n * c);
+  const int64_t cap = cdiv(small_vol, int64_t(1024));
+  int64_t b = want < cap ? want : cap;
+  if (b < 1) b = 1;
+  *per_block = cdiv(small_vol, b);
+  *bpc = static_cast<int>(cdiv(small_vol, *per_block));
+}
+
+template <typename T, int K>
+int launch_s2_wgrad_k(const void* big, const void* small, void* dw, void* dbias, void* ws, const S2Geom& g,
+                      int64_t n, int bpc, int64_t per_block, hipStream_t st) {
+  using Acc = typename AccOf<T>::type;
+  const int splits = static_cast<int>(n * bpc);
+  auto part = static_cast<Acc*>(ws);
+  hipLaunchKernelGGL((s2_wgrad_kernel<T, Acc, K>), dim3(static_cast<unsigned>(n * g.C * bpc)), dim3(256), 0, st,
+                     static_cast<const T*>(big), static_cast<const T*>(small), part, g, bpc, per_block, splits);
+  MEDNEXT_CHECK_LAUNCH();
+  return launch_finish<T, Acc>(part, dw, dbias, g.C, splits, K * K * K, st);
+}
+
 }  // namespace
 }  // namespace mednext
 
@@ -652,4 +909,61 @@ extern "C" int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_out
       return launch_wgrad<bf16_t>(x, grad_output, grad_weight, grad_bias, workspace, pl,
                                   kernel_size, vec, s);
   }
+}
+
+extern "C" int32_t mednext_depthwise3d_s2_gather(const void* big, const void* weight, const void* bias,
+                                                 void* small_out, int64_t n, int64_t c, int64_t db, int64_t hb,
+                                                 int64_t wb, int64_t ds, int64_t hs, int64_t ws,
+                                                 int32_t kernel_size, int32_t dtype, void* stream) {
+  return s2_map_entry<true>(big, weight, bias, small_out, n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, stream);
+}
+
+extern "C" int32_t mednext_depthwise3d_s2_scatter(const void* small, const void* weight, const void* bias,
+                                                  void* big_out, int64_t n, int64_t c, int64_t db, int64_t hb,
+                                                  int64_t wb, int64_t ds, int64_t hs, int64_t ws,
+                                                  int32_t kernel_size, int32_t dtype, void* stream) {
+  return s2_map_entry<false>(small, weight, bias, big_out, n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, stream);
+}
+
+extern "C" size_t mednext_depthwise3d_s2_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t db, int64_t hb,
+                                                               int64_t wb, int64_t ds, int64_t hs, int64_t ws,
+                                                               int32_t kernel_size, int32_t dtype) {
+  S2Geom g;
+  if (s2_geom(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, &g) != MEDNEXT_STATUS_OK) return 0;
+  int bpc = 0;
+  int64_t per_block = 0;
+  s2_wgrad_split(n, c, ds * hs * ws, &bpc, &per_block);
+  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
+  return static_cast<size_t>(c * n * bpc * (k3 + 1) * acc_bytes_of(dtype));
+}
+
+extern "C" int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* grad_weight,
+                                                void* grad_bias, void* workspace, size_t workspace_bytes,
+                                                int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb,
+                                                int64_t ds, int64_t hs, int64_t ws, int32_t kernel_size,
+                                                int32_t dtype, void* stream) {
+  MEDNEXT_CHECK_ARG(big != nullptr && small != nullptr && grad_weight != nullptr, "null tensor pointer");
+  S2Geom g;
+  if (int st = s2_geom(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, &g)) return st;
+  int bpc = 0;
+  int64_t per_block = 0;
+  s2_wgrad_split(n, c, ds * hs * ws, &bpc, &per_block);
+  MEDNEXT_CHECK_ARG(n * c * bpc < (int64_t(1) << 31), "grid too large");
+  const size_t need =
+      mednext_depthwise3d_s2_wgrad_workspace_bytes(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype);
+  MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+  auto s = static_cast<hipStream_t>(stream);
+#define MEDNEXT_S2W_K(T)                                                                              \
+  switch (kernel_size) {                                                                              \
+    case 1: return launch_s2_wgrad_k<T, 1>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, per_block, s); \
+    case 3: return launch_s2_wgrad_k<T, 3>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, per_block, s); \
+    default: return launch_s2_wgrad_k<T, 5>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, per_block, s); \
+  }
+  switch (dtype) {
+    case MEDNEXT_DTYPE_F32: MEDNEXT_S2W_K(float)
+    case MEDNEXT_DTYPE_F64: MEDNEXT_S2W_K(double)
+    case MEDNEXT_DTYPE_F16: MEDNEXT_S2W_K(f16_t)
+    default: MEDNEXT_S2W_K(bf16_t)
+  }
+#undef MEDNEXT_S2W_K
 }

@@ -64,9 +64,16 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p),
     ),
+    "mednext_depthwise3d_s2_gather": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
+    "mednext_depthwise3d_s2_scatter": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
+    "mednext_depthwise3d_s2_wgrad_workspace_bytes": (c_size_t, (*(_i64,) * 8, _i32, _i32)),
+    "mednext_depthwise3d_s2_wgrad": (
+        _i32,
+        (_p, _p, _p, _p, _p, c_size_t, *(_i64,) * 8, _i32, _i32, _p),
+    ),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

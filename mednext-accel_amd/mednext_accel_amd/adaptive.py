@@ -319,6 +319,22 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
             )
         return F.conv3d(x, self.weight, self.bias, self.stride, self.padding, self.dilation, self.groups)
 
+    def _forward_stride2(self, x: Tensor, context: ExecutionContext) -> Tensor:
+        """Down-block (stride 2) and up-block (transposed, stride 2) routes: the
+        HIP op runs all three phases when any phase selects it."""
+        if self.stride != (2, 2, 2):
+            return self._reference(x)
+        impl = "hip_depthwise_transpose2" if self.transpose else "hip_depthwise_stride2"
+        if not any(d.implementation == impl for d in self.phase_decisions(context)):
+            return self._reference(x)
+        hip_ops = _hip_ops()
+        dtype = getattr(torch, context.dtype)
+        x = x.to(dtype)
+        weight = self.weight.to(dtype)
+        bias = self.bias.to(dtype) if self.bias is not None else None
+        op = hip_ops.depthwise_conv_transpose3d_stride2 if self.transpose else hip_ops.depthwise_conv3d_stride2
+        return op(x, weight, bias, self.kernel_size[0])
+
     def phase_decisions(self, context: ExecutionContext) -> tuple[PolicyDecision, PolicyDecision, PolicyDecision]:
         return tuple(self.resolver.resolve(self.descriptor, context, p) for p in ("forward", "backward_input", "backward_weight"))
 
@@ -329,11 +345,13 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
             or context.device_type != "cuda"
             or not torch.is_grad_enabled()
             or x.ndim != 5
-            or self.transpose
-            or self.stride != (1, 1, 1)
             or self.output_padding != (0, 0, 0)
             or not x.is_contiguous()
         ):
+            return self._reference(x)
+        if self.transpose or self.stride == (2, 2, 2):
+            return self._forward_stride2(x, context)
+        if self.stride != (1, 1, 1):
             return self._reference(x)
         fwd, dx, dw = self.phase_decisions(context)
         custom = [d.implementation != "reference" for d in (fwd, dx, dw)]

@@ -679,3 +679,185 @@ def _mlp_backward(ctx, grad_out, _grad_h):
 
 
 mlp_expansion.register_autograd(_mlp_backward, setup_context=_setup_mlp)
+
+
+# ------------------------------------------------------------ stride-2 depthwise
+
+
+def _check_s2(big_shape, small_shape, weight: Tensor, *tensors: Tensor) -> int:
+    _check_device(weight, *tensors)
+    for t in tensors:
+        if t.ndim != 5 or not t.is_contiguous():
+            raise ValueError("contiguous NCDHW tensors are required")
+        if t.dtype != weight.dtype:
+            raise ValueError("tensors and weight must share a dtype")
+    if weight.ndim != 5 or weight.shape[1] != 1 or len(set(weight.shape[2:])) != 1:
+        raise ValueError("weight must have shape [C, 1, K, K, K]")
+    k = int(weight.shape[2])
+    if k % 2 == 0 or k not in SUPPORTED_KERNELS:
+        raise ValueError(f"kernel_size must be one of {SUPPORTED_KERNELS}")
+    if big_shape[:2] != small_shape[:2] or big_shape[1] != weight.shape[0]:
+        raise ValueError("batch / channel mismatch")
+    return k
+
+
+def _s2_dims(big_shape, small_shape) -> tuple[int, ...]:
+    n, c, db, hb, wb = (int(v) for v in big_shape)
+    ds, hs, ws = (int(v) for v in small_shape[2:])
+    return n, c, db, hb, wb, ds, hs, ws
+
+
+def depthwise_s2_gather(big: Tensor, weight: Tensor, bias: Tensor | None, small_spatial) -> Tensor:
+    """small[o] = bias + sum_t w[t] big[2o + t - k/2]."""
+    out = big.new_empty((big.shape[0], big.shape[1], *small_spatial))
+    k = _check_s2(big.shape, out.shape, weight, big)
+    if bias is not None and (bias.shape != (big.shape[1],) or bias.dtype != big.dtype):
+        raise ValueError("bias must be [C] in the input's dtype")
+    _hip.check(
+        _hip.load().mednext_depthwise3d_s2_gather(
+            big.data_ptr(), weight.contiguous().data_ptr(), _hip.ptr(bias.contiguous() if bias is not None else None),
+            out.data_ptr(), *_s2_dims(big.shape, out.shape), k, _hip.dtype_code(big.dtype), _hip.stream_of(big),
+        ),
+        "mednext_depthwise3d_s2_gather",
+    )
+    return out
+
+
+def depthwise_s2_scatter(small: Tensor, weight: Tensor, bias: Tensor | None, big_spatial) -> Tensor:
+    """big[i] = bias + sum_{o,t: 2o + t - k/2 = i} w[t] small[o]."""
+    out = small.new_empty((small.shape[0], small.shape[1], *big_spatial))
+    k = _check_s2(out.shape, small.shape, weight, small)
+    if bias is not None and (bias.shape != (small.shape[1],) or bias.dtype != small.dtype):
+        raise ValueError("bias must be [C] in the input's dtype")
+    _hip.check(
+        _hip.load().mednext_depthwise3d_s2_scatter(
+            small.data_ptr(), weight.contiguous().data_ptr(), _hip.ptr(bias.contiguous() if bias is not None else None),
+            out.data_ptr(), *_s2_dims(out.shape, small.shape), k, _hip.dtype_code(small.dtype), _hip.stream_of(small),
+        ),
+        "mednext_depthwise3d_s2_scatter",
+    )
+    return out
+
+
+def depthwise_s2_wgrad(big: Tensor, small: Tensor, kernel_size: int) -> tuple[Tensor, Tensor]:
+    """(dW [C,1,k,k,k], sum of ``small`` per channel [C]) with
+    dW[t] = sum_{n,o} big[2o + t - k/2] small[o]."""
+    if kernel_size % 2 == 0 or kernel_size not in SUPPORTED_KERNELS:
+        raise ValueError(f"kernel_size must be one of {SUPPORTED_KERNELS}")
+    weight_like = big.new_empty((big.shape[1], 1, kernel_size, kernel_size, kernel_size))
+    _check_s2(big.shape, small.shape, weight_like, big, small)
+    dims = _s2_dims(big.shape, small.shape)
+    code = _hip.dtype_code(big.dtype)
+    lib = _hip.load()
+    nbytes = int(lib.mednext_depthwise3d_s2_wgrad_workspace_bytes(*dims, kernel_size, code))
+    if nbytes == 0:
+        raise _hip.HipLibraryError(f"s2 wgrad workspace query failed: {_hip.last_error()}")
+    ws = torch.empty((nbytes,), device=big.device, dtype=torch.uint8)
+    dw = weight_like
+    ds = big.new_empty((big.shape[1],))
+    _hip.check(
+        lib.mednext_depthwise3d_s2_wgrad(
+            big.data_ptr(), small.data_ptr(), dw.data_ptr(), ds.data_ptr(), ws.data_ptr(), nbytes, *dims,
+            kernel_size, code, _hip.stream_of(big),
+        ),
+        "mednext_depthwise3d_s2_wgrad",
+    )
+    return dw, ds
+
+
+def strided_spatial(shape) -> list[int]:
+    """Output size of the stride-2, padding k//2 conv: (s - 1) // 2 + 1."""
+    return [(int(s) - 1) // 2 + 1 for s in shape]
+
+
+@torch.library.custom_op("mednext_accel_amd::depthwise_s2_gather", mutates_args=())
+def depthwise_s2_gather_op(big: Tensor, weight: Tensor, small_spatial: list[int]) -> Tensor:
+    return depthwise_s2_gather(big.contiguous(), weight, None, small_spatial)
+
+
+@depthwise_s2_gather_op.register_fake
+def _(big, weight, small_spatial):
+    return big.new_empty((big.shape[0], big.shape[1], *small_spatial))
+
+
+@torch.library.custom_op("mednext_accel_amd::depthwise_s2_scatter", mutates_args=())
+def depthwise_s2_scatter_op(small: Tensor, weight: Tensor, big_spatial: list[int]) -> Tensor:
+    return depthwise_s2_scatter(small.contiguous(), weight, None, big_spatial)
+
+
+@depthwise_s2_scatter_op.register_fake
+def _(small, weight, big_spatial):
+    return small.new_empty((small.shape[0], small.shape[1], *big_spatial))
+
+
+@torch.library.custom_op("mednext_accel_amd::depthwise_s2_wgrad", mutates_args=())
+def depthwise_s2_wgrad_op(big: Tensor, small: Tensor, kernel_size: int) -> tuple[Tensor, Tensor]:
+    return depthwise_s2_wgrad(big.contiguous(), small.contiguous(), kernel_size)
+
+
+@depthwise_s2_wgrad_op.register_fake
+def _(big, small, kernel_size):
+    c = big.shape[1]
+    return big.new_empty((c, 1, kernel_size, kernel_size, kernel_size)), big.new_empty((c,))
+
+
+@torch.library.custom_op("mednext_accel_amd::depthwise_conv3d_stride2", mutates_args=())
+def depthwise_conv3d_stride2(x: Tensor, weight: Tensor, bias: Tensor | None, kernel_size: int) -> Tensor:
+    """Depthwise Conv3d, stride 2, padding k//2 (the MedNeXt down block;
+    reference ops/_triton/depthwise.py:654-719), all phases in HIP."""
+    return depthwise_s2_gather(x.contiguous(), weight, bias, strided_spatial(x.shape[2:]))
+
+
+@depthwise_conv3d_stride2.register_fake
+def _(x, weight, bias, kernel_size):
+    return x.new_empty((x.shape[0], x.shape[1], *strided_spatial(x.shape[2:])))
+
+
+def _setup_s2(ctx, inputs, output):
+    x, weight, bias, kernel_size = inputs
+    ctx.save_for_backward(x, weight)
+    ctx.has_bias = bias is not None
+    ctx.kernel_size = kernel_size
+
+
+def _s2_backward(ctx, grad_output):
+    x, weight = ctx.saved_tensors
+    grad_output = grad_output.contiguous()
+    need_x, need_w, need_b = ctx.needs_input_grad[:3]
+    dx = depthwise_s2_scatter_op(grad_output, weight, list(x.shape[2:])) if need_x else None
+    dw = db = None
+    if need_w or (need_b and ctx.has_bias):
+        dw, db = depthwise_s2_wgrad_op(x, grad_output, ctx.kernel_size)
+    return dx, dw if need_w else None, db if (need_b and ctx.has_bias) else None, None
+
+
+depthwise_conv3d_stride2.register_autograd(_s2_backward, setup_context=_setup_s2)
+
+
+@torch.library.custom_op("mednext_accel_amd::depthwise_conv_transpose3d_stride2", mutates_args=())
+def depthwise_conv_transpose3d_stride2(x: Tensor, weight: Tensor, bias: Tensor | None, kernel_size: int) -> Tensor:
+    """Depthwise ConvTranspose3d, stride 2, padding k//2, no output padding (the
+    MedNeXt up block; reference ops/_triton/depthwise.py:768-850): output 2s - 1
+    per dimension, all phases in HIP."""
+    return depthwise_s2_scatter(x.contiguous(), weight, bias, [2 * int(s) - 1 for s in x.shape[2:]])
+
+
+@depthwise_conv_transpose3d_stride2.register_fake
+def _(x, weight, bias, kernel_size):
+    return x.new_empty((x.shape[0], x.shape[1], *(2 * s - 1 for s in x.shape[2:])))
+
+
+def _t2_backward(ctx, grad_output):
+    x, weight = ctx.saved_tensors
+    grad_output = grad_output.contiguous()
+    need_x, need_w, need_b = ctx.needs_input_grad[:3]
+    dx = depthwise_s2_gather_op(grad_output, weight, list(x.shape[2:])) if need_x else None
+    dw = depthwise_s2_wgrad_op(grad_output, x, ctx.kernel_size)[0] if need_w else None
+    db = None
+    if need_b and ctx.has_bias:
+        db = grad_output.sum(dim=(0, 2, 3, 4), dtype=torch.float64 if x.dtype == torch.float64 else torch.float32)
+        db = db.to(x.dtype)
+    return dx, dw, db, None
+
+
+depthwise_conv_transpose3d_stride2.register_autograd(_t2_backward, setup_context=_setup_s2)

@@ -14,6 +14,7 @@ from __future__ import annotations
 
 from collections.abc import Callable
 from dataclasses import dataclass
+from functools import partial
 from typing import TYPE_CHECKING, Literal
 
 if TYPE_CHECKING:
@@ -125,6 +126,25 @@ def _hip_depthwise(descriptor, context, phase: str) -> str | None:
     return None
 
 
+def _hip_depthwise_stride2(descriptor, context, phase: str, *, direction: str) -> str | None:
+    reason = _training_gpu(context, amd=True)
+    if reason is not None:
+        return reason
+    k = descriptor.kernel_size
+    if (
+        k is None
+        or descriptor.direction != direction
+        or k != (k[0],) * 3
+        or k[0] not in HIP_DEPTHWISE_KERNELS
+        or descriptor.stride != (2, 2, 2)
+        or descriptor.padding != (k[0] // 2,) * 3
+        or descriptor.dilation != (1, 1, 1)
+        or not descriptor.groups == descriptor.in_channels == descriptor.out_channels
+    ):
+        return "implementation does not support this geometry"
+    return None
+
+
 def _hip_group_norm(descriptor, context, phase: str) -> str | None:
     reason = _training_gpu(context, amd=True)
     if reason is not None:
@@ -201,6 +221,8 @@ def default_implementation_registry(*, triton_available: bool | None = None) -> 
         ("hip_depthwise_fwd", ("depthwise_conv3d",), ("forward",), "numerical", False, _hip_depthwise, _DW_GUARDS),
         ("hip_depthwise_dx", ("depthwise_conv3d",), ("backward_input",), "numerical", False, _hip_depthwise, _DW_GUARDS),
         ("hip_split_dw", ("depthwise_conv3d",), ("backward_weight",), "numerical", False, _hip_depthwise, _DW_GUARDS),
+        ("hip_depthwise_stride2", ("depthwise_conv3d",), ("forward", "backward_input", "backward_weight"), "numerical", False, partial(_hip_depthwise_stride2, direction="downsample"), _DW_GUARDS),
+        ("hip_depthwise_transpose2", ("depthwise_conv_transpose3d",), ("forward", "backward_input", "backward_weight"), "numerical", False, partial(_hip_depthwise_stride2, direction="transpose"), _DW_GUARDS),
         ("hip_group_norm", ("group_norm3d",), ("training",), "numerical", False, _hip_group_norm, _TENSOR_GUARDS),
         ("hip_pointwise_gemm", ("pointwise_conv3d",), ("training",), "numerical", False, _hip_pointwise, (*_TENSOR_GUARDS, "channels_supported")),
         ("hip_fused_expansion", ("mlp_expansion3d",), ("training",), "numerical", False, _hip_expansion, (*_TENSOR_GUARDS, "channels_supported")),

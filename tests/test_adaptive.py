@@ -147,13 +147,19 @@ def test_fused_expansion_is_attached_without_touching_parameters():
     copy.deepcopy(block)  # the plain attribute survives deep copies (checkpoint loaders use them)
 
 
-def test_strided_and_transposed_depthwise_stay_native():
+def test_strided_and_transposed_depthwise_select_hip():
     resolver = PolicyRegistry().resolver()
     down = _conv_descriptor(nn.Conv3d(32, 32, 3, stride=2, padding=1, groups=32), role="downsamples.0.depthwise")
     up = _conv_descriptor(nn.ConvTranspose3d(64, 64, 3, stride=2, padding=1, groups=64), role="upsamples.0.depthwise")
-    for desc in (down, up):
+    for desc, impl in ((down, "hip_depthwise_stride2"), (up, "hip_depthwise_transpose2")):
         for phase in ("forward", "backward_input", "backward_weight"):
-            assert resolver.resolve(desc, ctx((64,) * 3), phase).implementation == "reference"
+            assert resolver.resolve(desc, ctx((64,) * 3), phase).implementation == impl
+            assert resolver.resolve(desc, ctx((64,) * 3, training=False), phase).implementation == "reference"
+    # Geometries the kernels do not take stay native.
+    k7 = _conv_descriptor(nn.Conv3d(8, 8, 7, stride=2, padding=3, groups=8), role=None)
+    pad0 = _conv_descriptor(nn.Conv3d(8, 8, 3, stride=2, padding=0, groups=8), role=None)
+    for desc in (k7, pad0):
+        assert resolver.resolve(desc, ctx((32,) * 3), "forward").implementation == "reference"
 
 
 def test_context_guards():

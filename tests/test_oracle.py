@@ -199,3 +199,57 @@ def test_pointwise_oracle_is_not_transposed():
     rdx, rdw = torch.autograd.grad(F.conv3d(xt, wt), (xt, wt), _t(dy))
     np.testing.assert_allclose(dx, rdx.numpy(), rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(dw, rdw.numpy(), rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------------ stride 2
+
+
+@pytest.mark.parametrize("k", [1, 3, 5])
+@pytest.mark.parametrize("shape", [(2, 3, 5, 6, 7), (1, 2, 8, 8, 8), (1, 1, 3, 9, 4)])
+def test_strided_oracle_matches_torch_float64(k, shape):
+    rng = np.random.default_rng(k * 13 + shape[-1])
+    c = shape[1]
+    x, w, b = rng.standard_normal(shape), rng.standard_normal((c, 1, k, k, k)), rng.standard_normal(c)
+    xt, wt, bt = (torch.tensor(a, requires_grad=True) for a in (x, w, b))
+    yt = F.conv3d(xt, wt, bt, stride=2, padding=k // 2, groups=c)
+    assert yt.shape[2:] == odw.strided_output_shape(shape[2:])
+    dy = rng.standard_normal(yt.shape)
+    gx, gw, gb = torch.autograd.grad(yt, (xt, wt, bt), torch.tensor(dy))
+    np.testing.assert_allclose(odw.strided_forward(x, w, b), yt.detach().numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(odw.strided_input_grad(dy, w, shape[2:]), gx.numpy(), rtol=1e-12, atol=1e-12)
+    dw, db = odw.strided_weight_grad(x, dy, k)
+    np.testing.assert_allclose(dw, gw.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(db, gb.numpy(), rtol=1e-12, atol=1e-12)
+    # The transposed conv (MedNeXt up block): forward, dX and dW.
+    s = rng.standard_normal((shape[0], c) + tuple(max(1, v // 2) for v in shape[2:]))
+    st_, wt2 = torch.tensor(s, requires_grad=True), torch.tensor(w, requires_grad=True)
+    yt2 = F.conv_transpose3d(st_, wt2, torch.tensor(b), stride=2, padding=k // 2, groups=c)
+    np.testing.assert_allclose(odw.transposed_forward(s, w, b), yt2.detach().numpy(), rtol=1e-12, atol=1e-12)
+    g2 = rng.standard_normal(yt2.shape)
+    gs, gw2 = torch.autograd.grad(yt2, (st_, wt2), torch.tensor(g2))
+    np.testing.assert_allclose(odw.strided_forward(g2, w), gs.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(odw.strided_weight_grad(g2, s, k)[0], gw2.numpy(), rtol=1e-12, atol=1e-12)
+
+
+def test_strided_oracle_brute_force_and_adjoint():
+    """Brute-force loops, and <forward(a), b> == <a, input_grad(b)> (the scatter
+    is the adjoint of the gather), which fixes the transposed relation without
+    any library."""
+    rng = np.random.default_rng(77)
+    for k in (3, 5):
+        x = rng.standard_normal((1, 2, 5, 4, 7))
+        w = rng.standard_normal((2, 1, k, k, k))
+        b = rng.standard_normal(2)
+        np.testing.assert_allclose(odw.strided_forward(x, w, b), odw.strided_forward_loops(x, w, b), rtol=1e-12)
+        y = odw.strided_forward(x, w)
+        g = rng.standard_normal(y.shape)
+        lhs = float((y * g).sum())
+        rhs = float((x * odw.strided_input_grad(g, w, x.shape[2:])).sum())
+        assert abs(lhs - rhs) <= 1e-10 * max(1.0, abs(lhs))
+        # dW is the derivative of <forward(x; w), g> with respect to w.
+        dw, _ = odw.strided_weight_grad(x, g, k)
+        eps = 1e-6
+        e = np.zeros_like(w)
+        e[1, 0, 1, 0, 2] = eps
+        num = ((odw.strided_forward(x, w + e) - odw.strided_forward(x, w - e)) * g).sum() / (2 * eps)
+        assert abs(num - dw[1, 0, 1, 0, 2]) <= 1e-6 * max(1.0, abs(num))
