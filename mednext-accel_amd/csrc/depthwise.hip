@@ -13,9 +13,11 @@
 // kernel keeps a k-plane ring of grad_output values in registers instead and
 // accumulates k^3 tap sums per thread, reduced per workgroup into a fp32/fp64
 // partial and then summed over workgroups in a fixed order (deterministic).
+#include "cdna4.h"
 #include "common.h"
 #include "depthwise_mfma.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace mednext {
@@ -573,162 +575,340 @@ int launch_wgrad(const void* x, const void* dy, void* dw, void* db, void* ws, co
 //            big = dy, small = x)
 // They carry ~k^3/8 FLOP per big element, so they are VALU kernels bound by
 // memory; accumulation is fp32 (fp64 for fp64 tensors).
-struct S2Geom {
-  int64_t total;  // outputs of this launch
+//
+// Work decomposition: a wave owns one "task" at a time, a run of up to 64
+// consecutive elements of one row of the lane domain: small rows for gather
+// and reduce; for scatter, rows of 2x2x2 big-voxel cells, so that every lane
+// of every task uses the same taps. Narrow rows pack 64 / Wl rows into one
+// task. Tasks never cross a channel slab, so the channel and its weights are
+// wave-uniform; task -> row decoding uses 32-bit multiply-high division. All
+// loads go through per-slab buffer resources with masked lanes pointed out of
+// range (they read zero), so a task issues its loads without branches. A wave
+// walks a contiguous run of tasks, so big rows shared by neighbouring output
+// rows hit in L1/L2.
+
+// n / d for n < 2^31 by multiply-high (the round-up method: Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994).
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+FastDiv make_fastdiv(uint32_t d) {
+  uint32_t s = 0;
+  while ((uint64_t(1) << s) < d) ++s;
+  const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << s) - d)) / d + 1;
+  return FastDiv{d, static_cast<uint32_t>(m), s};
+}
+
+__device__ inline uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.m) + n) >> f.s; }
+
+struct S2Dims {
   int C;
   int Db, Hb, Wb;  // big
   int Ds, Hs, Ws;  // small
+  int Wd;          // lane-domain row width (columns, or column pairs for scatter)
+  uint32_t rows;   // lane-domain rows per slab
+  int Wl, lshift;  // lanes per row (power of two <= 64) and its log2
+  int rpw, nseg;   // rows per task, tasks per row
+  uint32_t tpc;    // tasks per (n, c) slab
+  uint32_t tasks;  // tasks over the launch
+  uint32_t per;    // tasks per wave (gather / scatter) or per workgroup (reduce)
+  FastDiv f_tpc, f_nseg, f_Hd, f_C;
 };
+
+struct TaskPos {
+  uint32_t nc;
+  int c;
+  int d, h, col;  // lane-domain plane, row, column
+  bool valid;
+};
+
+__device__ inline TaskPos task_pos(const S2Dims& g, uint32_t nc, uint32_t t, int lane) {
+  TaskPos p;
+  p.nc = nc;
+  p.c = static_cast<int>(nc - fdiv(nc, g.f_C) * static_cast<uint32_t>(g.C));
+  const uint32_t rt = fdiv(t, g.f_nseg);
+  const uint32_t seg = t - rt * static_cast<uint32_t>(g.nseg);
+  const uint32_t row = rt * static_cast<uint32_t>(g.rpw) + static_cast<uint32_t>(lane >> g.lshift);
+  p.col = static_cast<int>(seg) * g.Wl + (lane & (g.Wl - 1));
+  p.valid = row < g.rows && p.col < g.Wd;
+  const uint32_t r = row < g.rows ? row : 0u;
+  const uint32_t d = fdiv(r, g.f_Hd);
+  p.d = static_cast<int>(d);
+  p.h = static_cast<int>(r - d * g.f_Hd.d);
+  return p;
+}
+
+template <typename T, typename Acc, int K>
+__device__ inline void load_taps(const T* __restrict__ w, int c, Acc (&wv)[K * K * K]) {
+  const T* wc = w + static_cast<int64_t>(c) * K * K * K;
+#pragma unroll
+  for (int t = 0; t < K * K * K; ++t) wv[t] = Cvt<T, Acc>::load(wc[t]);
+}
+
+// One element through a raw buffer resource; `ok == false` reads the
+// out-of-range offset, which returns zero. Keeping every load unconditional
+// lets a task issue all of its loads back to back.
+template <typename T>
+struct BufIo;
+template <>
+struct BufIo<float> {
+  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  }
+  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+  }
+};
+template <>
+struct BufIo<double> {
+  __device__ static double ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+  }
+  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, double v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, off, 0, 0);
+  }
+};
+template <>
+struct BufIo<f16_t> {
+  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return static_cast<float>(__builtin_bit_cast(f16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+  }
+  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<f16_t>(v)), r, off, 0, 0);
+  }
+};
+template <>
+struct BufIo<bf16_t> {
+  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+  }
+  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), r, off, 0, 0);
+  }
+};
+
+template <typename T>
+__device__ inline uint32_t boff(bool ok, int elem) {
+  return ok ? static_cast<uint32_t>(elem) * static_cast<uint32_t>(sizeof(T)) : kOob;
+}
+
+template <typename T>
+__device__ inline __amdgpu_buffer_rsrc_t s2_rsrc(const T* base, uint32_t slab, int64_t vol) {
+  return slab_rsrc(base + slab * vol, static_cast<uint32_t>(vol * static_cast<int64_t>(sizeof(T))));
+}
 
 template <typename T, typename Acc, int K, bool BIAS>
 __global__ __launch_bounds__(256) void s2_gather_kernel(const T* __restrict__ big, const T* __restrict__ w,
-                                                        const T* __restrict__ b, T* __restrict__ out, S2Geom g) {
+                                                        const T* __restrict__ b, T* __restrict__ out, S2Dims g) {
   constexpr int P = K / 2;
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = blockIdx.x * 4u + static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+  const uint32_t t0 = wave * g.per;
+  const uint32_t t1 = min(t0 + g.per, g.tasks);
   const int64_t big_vol = static_cast<int64_t>(g.Db) * g.Hb * g.Wb;
-  for (int64_t idx = blockIdx.x * 256ll + threadIdx.x; idx < g.total; idx += gridDim.x * 256ll) {
-    int64_t r = idx;
-    const int ow = static_cast<int>(r % g.Ws);
-    r /= g.Ws;
-    const int oh = static_cast<int>(r % g.Hs);
-    r /= g.Hs;
-    const int od = static_cast<int>(r % g.Ds);
-    const int64_t nc = r / g.Ds;
-    const int c = static_cast<int>(nc % g.C);
-    const T* bp = big + nc * big_vol;
-    const T* wp = w + static_cast<int64_t>(c) * K * K * K;
-    Acc acc = BIAS ? Cvt<T, Acc>::load(b[c]) : Acc(0);
+  const int64_t small_vol = static_cast<int64_t>(g.Ds) * g.Hs * g.Ws;
+  Acc wv[K * K * K];
+  Acc bias = Acc(0);
+  int wc = -1;
+  for (uint32_t task = t0; task < t1; ++task) {
+    const uint32_t nc = fdiv(task, g.f_tpc);
+    const TaskPos p = task_pos(g, nc, task - nc * g.tpc, lane);
+    if (p.c != wc) {
+      load_taps<T, Acc, K>(w, p.c, wv);
+      if (BIAS) bias = Cvt<T, Acc>::load(b[p.c]);
+      wc = p.c;
+    }
+    const __amdgpu_buffer_rsrc_t br = s2_rsrc(big, nc, big_vol);
+    Acc v[K * K * K];
 #pragma unroll
     for (int kd = 0; kd < K; ++kd) {
-      const int id = 2 * od + kd - P;
-      if (id < 0 || id >= g.Db) continue;
+      const int id = 2 * p.d + kd - P;
+      const bool okd = p.valid && static_cast<unsigned>(id) < static_cast<unsigned>(g.Db);
 #pragma unroll
       for (int kh = 0; kh < K; ++kh) {
-        const int ih = 2 * oh + kh - P;
-        if (ih < 0 || ih >= g.Hb) continue;
-        const T* row = bp + (static_cast<int64_t>(id) * g.Hb + ih) * g.Wb;
+        const int ih = 2 * p.h + kh - P;
+        const bool okh = okd && static_cast<unsigned>(ih) < static_cast<unsigned>(g.Hb);
+        const int rowoff = (id * g.Hb + ih) * g.Wb;
 #pragma unroll
         for (int kw = 0; kw < K; ++kw) {
-          const int iw = 2 * ow + kw - P;
-          if (iw < 0 || iw >= g.Wb) continue;
-          acc += Cvt<T, Acc>::load(wp[(kd * K + kh) * K + kw]) * Cvt<T, Acc>::load(row[iw]);
+          const int iw = 2 * p.col + kw - P;
+          const bool ok = okh && static_cast<unsigned>(iw) < static_cast<unsigned>(g.Wb);
+          v[(kd * K + kh) * K + kw] = BufIo<T>::ld(br, boff<T>(ok, rowoff + iw));
         }
       }
     }
-    out[idx] = Cvt<T, Acc>::store(acc);
+    Acc acc = bias;
+#pragma unroll
+    for (int t = 0; t < K * K * K; ++t) acc += wv[t] * v[t];
+    const __amdgpu_buffer_rsrc_t orr = s2_rsrc(out, nc, small_vol);
+    BufIo<T>::st(orr, boff<T>(p.valid, (p.d * g.Hs + p.h) * g.Ws + p.col), acc);
   }
 }
 
+// Scatter by 2x2x2 cells: lane (jd, jh, m) of the cell domain produces big
+// voxels (2jd + ed, 2jh + eh, 2m + ew), e in {0, 1}. Tap k reaches big index
+// 2j + e from small index j + a with a = (e + P - k) / 2 when e + P - k is
+// even, so the cell reads the small block j + a, a in [-(P / 2), (P + 1) / 2],
+// and every (e, a) -> k pairing is fixed at compile time.
 template <typename T, typename Acc, int K, bool BIAS>
 __global__ __launch_bounds__(256) void s2_scatter_kernel(const T* __restrict__ small, const T* __restrict__ w,
-                                                         const T* __restrict__ b, T* __restrict__ out, S2Geom g) {
+                                                         const T* __restrict__ b, T* __restrict__ out, S2Dims g) {
   constexpr int P = K / 2;
+  constexpr int AMIN = -(P / 2), AMAX = (P + 1) / 2, NA = AMAX - AMIN + 1;
+  const int lane = threadIdx.x & 63;
+  const uint32_t wave = blockIdx.x * 4u + static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+  const uint32_t t0 = wave * g.per;
+  const uint32_t t1 = min(t0 + g.per, g.tasks);
+  const int64_t big_vol = static_cast<int64_t>(g.Db) * g.Hb * g.Wb;
   const int64_t small_vol = static_cast<int64_t>(g.Ds) * g.Hs * g.Ws;
-  for (int64_t idx = blockIdx.x * 256ll + threadIdx.x; idx < g.total; idx += gridDim.x * 256ll) {
-    int64_t r = idx;
-    const int iw = static_cast<int>(r % g.Wb);
-    r /= g.Wb;
-    const int ih = static_cast<int>(r % g.Hb);
-    r /= g.Hb;
-    const int id = static_cast<int>(r % g.Db);
-    const int64_t nc = r / g.Db;
-    const int c = static_cast<int>(nc % g.C);
-    const T* sp = small + nc * small_vol;
-    const T* wp = w + static_cast<int64_t>(c) * K * K * K;
-    Acc acc = BIAS ? Cvt<T, Acc>::load(b[c]) : Acc(0);
-    // Taps t with 2o + t - P = i: t has the parity of i + P and o = (i + P - t) / 2.
+  Acc wv[K * K * K];
+  Acc bias = Acc(0);
+  int wc = -1;
+  for (uint32_t task = t0; task < t1; ++task) {
+    const uint32_t nc = fdiv(task, g.f_tpc);
+    const TaskPos p = task_pos(g, nc, task - nc * g.tpc, lane);
+    if (p.c != wc) {
+      load_taps<T, Acc, K>(w, p.c, wv);
+      if (BIAS) bias = Cvt<T, Acc>::load(b[p.c]);
+      wc = p.c;
+    }
+    const __amdgpu_buffer_rsrc_t sr = s2_rsrc(small, nc, small_vol);
+    Acc s[NA][NA][NA];
 #pragma unroll
-    for (int kd = 0; kd < K; ++kd) {
-      const int td = id + P - kd;
-      if (td < 0 || (td & 1) || (td >> 1) >= g.Ds) continue;
+    for (int ad = 0; ad < NA; ++ad) {
+      const int sd = p.d + AMIN + ad;
+      const bool okd = p.valid && static_cast<unsigned>(sd) < static_cast<unsigned>(g.Ds);
 #pragma unroll
-      for (int kh = 0; kh < K; ++kh) {
-        const int th = ih + P - kh;
-        if (th < 0 || (th & 1) || (th >> 1) >= g.Hs) continue;
-        const T* row = sp + (static_cast<int64_t>(td >> 1) * g.Hs + (th >> 1)) * g.Ws;
+      for (int ah = 0; ah < NA; ++ah) {
+        const int sh = p.h + AMIN + ah;
+        const bool okh = okd && static_cast<unsigned>(sh) < static_cast<unsigned>(g.Hs);
+        const int rowoff = (sd * g.Hs + sh) * g.Ws;
 #pragma unroll
-        for (int kw = 0; kw < K; ++kw) {
-          const int tw = iw + P - kw;
-          if (tw < 0 || (tw & 1) || (tw >> 1) >= g.Ws) continue;
-          acc += Cvt<T, Acc>::load(wp[(kd * K + kh) * K + kw]) * Cvt<T, Acc>::load(row[tw >> 1]);
+        for (int aw = 0; aw < NA; ++aw) {
+          const int sw = p.col + AMIN + aw;
+          const bool ok = okh && static_cast<unsigned>(sw) < static_cast<unsigned>(g.Ws);
+          s[ad][ah][aw] = BufIo<T>::ld(sr, boff<T>(ok, rowoff + sw));
         }
       }
     }
-    out[idx] = Cvt<T, Acc>::store(acc);
+    const __amdgpu_buffer_rsrc_t orr = s2_rsrc(out, nc, big_vol);
+#pragma unroll
+    for (int ed = 0; ed < 2; ++ed) {
+      const int bd = 2 * p.d + ed;
+#pragma unroll
+      for (int eh = 0; eh < 2; ++eh) {
+        const int bh = 2 * p.h + eh;
+#pragma unroll
+        for (int ew = 0; ew < 2; ++ew) {
+          const int bw = 2 * p.col + ew;
+          Acc acc = bias;
+#pragma unroll
+          for (int ad = 0; ad < NA; ++ad) {
+            const int kd = ed + P - 2 * (AMIN + ad);
+            if (kd < 0 || kd >= K) continue;
+#pragma unroll
+            for (int ah = 0; ah < NA; ++ah) {
+              const int kh = eh + P - 2 * (AMIN + ah);
+              if (kh < 0 || kh >= K) continue;
+#pragma unroll
+              for (int aw = 0; aw < NA; ++aw) {
+                const int kw = ew + P - 2 * (AMIN + aw);
+                if (kw < 0 || kw >= K) continue;
+                acc += wv[(kd * K + kh) * K + kw] * s[ad][ah][aw];
+              }
+            }
+          }
+          const bool ok = p.valid && bd < g.Db && bh < g.Hb && bw < g.Wb;
+          BufIo<T>::st(orr, boff<T>(ok, (bd * g.Hb + bh) * g.Wb + bw), acc);
+        }
+      }
+    }
   }
 }
 
-// One block per (n, c, voxel range of the small tensor); per-block partials
-// [C][K^3 + 1][splits] (split = n * blocks_per_channel + range) for the
-// fixed-order finish kernel.
+// One workgroup per (n, c, run of tasks); its four waves split the run. Per
+// workgroup fp32 (fp64) partials [C][K^3 + 1][splits], split = n * bpc + j,
+// summed by the fixed-order finish kernel.
 template <typename T, typename Acc, int K>
 __global__ __launch_bounds__(256) void s2_wgrad_kernel(const T* __restrict__ big, const T* __restrict__ small,
-                                                       Acc* __restrict__ partial, S2Geom g, int bpc,
-                                                       int64_t per_block, int splits) {
+                                                       Acc* __restrict__ partial, S2Dims g, int bpc, int splits) {
   constexpr int P = K / 2;
   constexpr int K3 = K * K * K;
   __shared__ Acc red[4][K3 + 1];
-  const int64_t nc = blockIdx.x / bpc;
-  const int j = static_cast<int>(blockIdx.x - nc * bpc);
-  const int c = static_cast<int>(nc % g.C);
-  const int64_t n = nc / g.C;
-  const int64_t small_vol = static_cast<int64_t>(g.Ds) * g.Hs * g.Ws;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t nc = blockIdx.x / static_cast<uint32_t>(bpc);
+  const uint32_t j = blockIdx.x - nc * static_cast<uint32_t>(bpc);
+  const uint32_t b0 = j * g.per;
+  const uint32_t b1 = min(b0 + g.per, g.tpc);
+  const uint32_t q = (b1 - b0 + 3u) / 4u;
+  const uint32_t t0 = min(b0 + wave * q, b1);
+  const uint32_t t1 = min(t0 + q, b1);
   const int64_t big_vol = static_cast<int64_t>(g.Db) * g.Hb * g.Wb;
-  const T* bp = big + nc * big_vol;
-  const T* sp = small + nc * small_vol;
-  const int64_t v0 = j * per_block;
-  const int64_t v1 = v0 + per_block < small_vol ? v0 + per_block : small_vol;
+  const int64_t small_vol = static_cast<int64_t>(g.Ds) * g.Hs * g.Ws;
+  const __amdgpu_buffer_rsrc_t br = s2_rsrc(big, nc, big_vol);
+  const __amdgpu_buffer_rsrc_t sr = s2_rsrc(small, nc, small_vol);
   Acc acc[K3 + 1];
 #pragma unroll
   for (int t = 0; t <= K3; ++t) acc[t] = Acc(0);
-  for (int64_t v = v0 + threadIdx.x; v < v1; v += 256) {
-    int64_t r = v;
-    const int ow = static_cast<int>(r % g.Ws);
-    r /= g.Ws;
-    const int oh = static_cast<int>(r % g.Hs);
-    const int od = static_cast<int>(r / g.Hs);
-    const Acc s = Cvt<T, Acc>::load(sp[v]);
-    acc[K3] += s;
+  for (uint32_t t = t0; t < t1; ++t) {
+    const TaskPos p = task_pos(g, nc, t, lane);
+    const Acc s = BufIo<T>::ld(sr, boff<T>(p.valid, (p.d * g.Hs + p.h) * g.Ws + p.col));
+    Acc v[K3];
 #pragma unroll
     for (int kd = 0; kd < K; ++kd) {
-      const int id = 2 * od + kd - P;
-      if (id < 0 || id >= g.Db) continue;
+      const int id = 2 * p.d + kd - P;
+      const bool okd = p.valid && static_cast<unsigned>(id) < static_cast<unsigned>(g.Db);
 #pragma unroll
       for (int kh = 0; kh < K; ++kh) {
-        const int ih = 2 * oh + kh - P;
-        if (ih < 0 || ih >= g.Hb) continue;
-        const T* row = bp + (static_cast<int64_t>(id) * g.Hb + ih) * g.Wb;
+        const int ih = 2 * p.h + kh - P;
+        const bool okh = okd && static_cast<unsigned>(ih) < static_cast<unsigned>(g.Hb);
+        const int rowoff = (id * g.Hb + ih) * g.Wb;
 #pragma unroll
         for (int kw = 0; kw < K; ++kw) {
-          const int iw = 2 * ow + kw - P;
-          if (iw < 0 || iw >= g.Wb) continue;
-          acc[(kd * K + kh) * K + kw] += Cvt<T, Acc>::load(row[iw]) * s;
+          const int iw = 2 * p.col + kw - P;
+          const bool ok = okh && static_cast<unsigned>(iw) < static_cast<unsigned>(g.Wb);
+          v[(kd * K + kh) * K + kw] = BufIo<T>::ld(br, boff<T>(ok, rowoff + iw));
         }
       }
     }
+    acc[K3] += s;
+#pragma unroll
+    for (int t2 = 0; t2 < K3; ++t2) acc[t2] += v[t2] * s;
   }
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int t = 0; t <= K3; ++t) {
     const Acc tot = wave_sum(acc[t]);
     if (lane == 0) red[wave][t] = tot;
   }
   __syncthreads();
+  const int64_t n = nc / static_cast<uint32_t>(g.C);
+  const int c = static_cast<int>(nc - n * g.C);
   const int64_t split = n * bpc + j;
   for (int t = threadIdx.x; t <= K3; t += 256) {
     partial[(static_cast<int64_t>(c) * (K3 + 1) + t) * splits + split] = ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
   }
 }
 
-int s2_geom(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k,
-            int dtype, S2Geom* g) {
+constexpr int kS2MaxWaves = 16384;  // gather / scatter: ~8 resident waves per SIMD over two rounds
+constexpr int kS2WgradBlocks = 2048;
+
+enum S2Domain { kSmallDomain = 0, kBigCellDomain = 1 };
+
+// Validates the shapes and lays out the lane domain. Every index the kernels
+// form stays below 2^31: per-slab volumes, rows and task counts are checked.
+int s2_plan(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k,
+            int dtype, S2Domain dom, S2Dims* g) {
   MEDNEXT_CHECK_ARG(dtype_ok(dtype), "unsupported dtype");
   MEDNEXT_CHECK_ARG(k == 1 || k == 3 || k == 5, "kernel_size must be 1, 3 or 5");
   MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && db >= 1 && hb >= 1 && wb >= 1 && ds >= 1 && hs >= 1 && ws >= 1,
                     "shape must be positive");
   const int64_t lim = int64_t(1) << 31;
-  MEDNEXT_CHECK_ARG(c < lim && db < lim && hb < lim && wb < lim && ds < lim && hs < lim && ws < lim,
-                    "each dimension must fit in int32");
-  MEDNEXT_CHECK_ARG(db * hb < lim && db * hb * wb < (int64_t(1) << 62) / (n * c), "tensor too large");
+  const int64_t esz = acc_bytes_of(dtype) == 8 ? 8 : (dtype == MEDNEXT_DTYPE_F32 ? 4 : 2);
+  MEDNEXT_CHECK_ARG(db * hb * wb * esz < lim && ds * hs * ws * esz < lim,
+                    "each (n, c) slab must be smaller than 2 GiB");
+  MEDNEXT_CHECK_ARG(n * c < lim, "n * c must be below 2^31");
   g->C = static_cast<int>(c);
   g->Db = static_cast<int>(db);
   g->Hb = static_cast<int>(hb);
@@ -736,19 +916,52 @@ int s2_geom(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int64_t ds
   g->Ds = static_cast<int>(ds);
   g->Hs = static_cast<int>(hs);
   g->Ws = static_cast<int>(ws);
-  g->total = 0;
+  const int64_t dd = dom == kSmallDomain ? ds : cdiv(db, 2);
+  const int64_t hd = dom == kSmallDomain ? hs : cdiv(hb, 2);
+  const int64_t wd = dom == kSmallDomain ? ws : cdiv(wb, 2);
+  int wl = 1, lshift = 0;
+  while (wl < 64 && wl < wd) {
+    wl *= 2;
+    ++lshift;
+  }
+  g->Wd = static_cast<int>(wd);
+  g->rows = static_cast<uint32_t>(dd * hd);
+  g->Wl = wl;
+  g->lshift = lshift;
+  g->rpw = 64 / wl;
+  g->nseg = static_cast<int>(cdiv(wd, wl));
+  const int64_t tpc = cdiv(dd * hd, g->rpw) * g->nseg;
+  MEDNEXT_CHECK_ARG(n * c * tpc < lim, "too many row tasks");
+  g->tpc = static_cast<uint32_t>(tpc);
+  g->tasks = static_cast<uint32_t>(n * c * tpc);
+  g->f_tpc = make_fastdiv(g->tpc);
+  g->f_nseg = make_fastdiv(static_cast<uint32_t>(g->nseg));
+  g->f_Hd = make_fastdiv(static_cast<uint32_t>(hd));
+  g->f_C = make_fastdiv(static_cast<uint32_t>(c));
+  g->per = 1;
   return MEDNEXT_STATUS_OK;
 }
 
-unsigned s2_blocks(int64_t total) {
-  const int64_t b = cdiv(total, 256);
-  return static_cast<unsigned>(b < 65536 * 16 ? b : 65536 * 16);
+// Gather / scatter grid: up to kS2MaxWaves waves, each walking `per` tasks.
+unsigned s2_map_blocks(S2Dims* g) {
+  const int64_t waves = std::min<int64_t>(g->tasks, kS2MaxWaves);
+  g->per = static_cast<uint32_t>(cdiv(g->tasks, waves));
+  return static_cast<unsigned>(cdiv(cdiv(g->tasks, g->per), 4));
+}
+
+// Reduce grid: ~kS2WgradBlocks workgroups, at least 8 tasks each.
+void s2_wgrad_split(int64_t n, S2Dims* g, int* bpc) {
+  const int64_t want = cdiv(int64_t(kS2WgradBlocks), n * g->C);
+  const int64_t cap = cdiv(g->tpc, int64_t(8));
+  const int64_t b = std::max<int64_t>(1, std::min(want, cap));
+  g->per = static_cast<uint32_t>(cdiv(g->tpc, b));
+  *bpc = static_cast<int>(cdiv(g->tpc, g->per));
 }
 
 template <typename T, int K, bool GATHER>
-int launch_s2_map_k(const void* in, const void* w, const void* b, void* out, S2Geom g, hipStream_t st) {
+int launch_s2_map_k(const void* in, const void* w, const void* b, void* out, S2Dims g, hipStream_t st) {
   using Acc = typename AccOf<T>::type;
-  const unsigned blocks = s2_blocks(g.total);
+  const unsigned blocks = s2_map_blocks(&g);
   auto pi = static_cast<const T*>(in);
   auto pw = static_cast<const T*>(w);
   auto pb = static_cast<const T*>(b);
@@ -772,9 +985,9 @@ template <bool GATHER>
 int s2_map_entry(const void* in, const void* w, const void* b, void* out, int64_t n, int64_t c, int64_t db,
                  int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int32_t k, int32_t dtype, void* stream) {
   MEDNEXT_CHECK_ARG(in != nullptr && w != nullptr && out != nullptr, "null tensor pointer");
-  S2Geom g;
-  if (int st = s2_geom(n, c, db, hb, wb, ds, hs, ws, k, dtype, &g)) return st;
-  g.total = GATHER ? n * c * ds * hs * ws : n * c * db * hb * wb;
+  S2Dims g;
+  if (int st = s2_plan(n, c, db, hb, wb, ds, hs, ws, k, dtype, GATHER ? kSmallDomain : kBigCellDomain, &g))
+    return st;
   auto s = static_cast<hipStream_t>(stream);
 #define MEDNEXT_S2_K(T)                                                          \
   switch (k) {                                                                   \
@@ -791,25 +1004,14 @@ int s2_map_entry(const void* in, const void* w, const void* b, void* out, int64_
 #undef MEDNEXT_S2_K
 }
 
-// Blocks per (n, c) for the reduction: ~2048 blocks over the launch, at least
-// 1024 small voxels per block.
-void s2_wgrad_split(int64_t n, int64_t c, int64_t small_vol, int* bpc, int64_t* per_block) {
-  const int64_t want = cdiv(int64_t(2048), n * c);
-  const int64_t cap = cdiv(small_vol, int64_t(1024));
-  int64_t b = want < cap ? want : cap;
-  if (b < 1) b = 1;
-  *per_block = cdiv(small_vol, b);
-  *bpc = static_cast<int>(cdiv(small_vol, *per_block));
-}
-
 template <typename T, int K>
-int launch_s2_wgrad_k(const void* big, const void* small, void* dw, void* dbias, void* ws, const S2Geom& g,
-                      int64_t n, int bpc, int64_t per_block, hipStream_t st) {
+int launch_s2_wgrad_k(const void* big, const void* small, void* dw, void* dbias, void* ws, const S2Dims& g,
+                      int64_t n, int bpc, hipStream_t st) {
   using Acc = typename AccOf<T>::type;
   const int splits = static_cast<int>(n * bpc);
   auto part = static_cast<Acc*>(ws);
   hipLaunchKernelGGL((s2_wgrad_kernel<T, Acc, K>), dim3(static_cast<unsigned>(n * g.C * bpc)), dim3(256), 0, st,
-                     static_cast<const T*>(big), static_cast<const T*>(small), part, g, bpc, per_block, splits);
+                     static_cast<const T*>(big), static_cast<const T*>(small), part, g, bpc, splits);
   MEDNEXT_CHECK_LAUNCH();
   return launch_finish<T, Acc>(part, dw, dbias, g.C, splits, K * K * K, st);
 }
@@ -928,11 +1130,10 @@ extern "C" int32_t mednext_depthwise3d_s2_scatter(const void* small, const void*
 extern "C" size_t mednext_depthwise3d_s2_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t db, int64_t hb,
                                                                int64_t wb, int64_t ds, int64_t hs, int64_t ws,
                                                                int32_t kernel_size, int32_t dtype) {
-  S2Geom g;
-  if (s2_geom(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, &g) != MEDNEXT_STATUS_OK) return 0;
+  S2Dims g;
+  if (s2_plan(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, kSmallDomain, &g) != MEDNEXT_STATUS_OK) return 0;
   int bpc = 0;
-  int64_t per_block = 0;
-  s2_wgrad_split(n, c, ds * hs * ws, &bpc, &per_block);
+  s2_wgrad_split(n, &g, &bpc);
   const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
   return static_cast<size_t>(c * n * bpc * (k3 + 1) * acc_bytes_of(dtype));
 }
@@ -943,21 +1144,20 @@ extern "C" int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* sma
                                                 int64_t ds, int64_t hs, int64_t ws, int32_t kernel_size,
                                                 int32_t dtype, void* stream) {
   MEDNEXT_CHECK_ARG(big != nullptr && small != nullptr && grad_weight != nullptr, "null tensor pointer");
-  S2Geom g;
-  if (int st = s2_geom(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, &g)) return st;
+  S2Dims g;
+  if (int st = s2_plan(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, kSmallDomain, &g)) return st;
   int bpc = 0;
-  int64_t per_block = 0;
-  s2_wgrad_split(n, c, ds * hs * ws, &bpc, &per_block);
+  s2_wgrad_split(n, &g, &bpc);
   MEDNEXT_CHECK_ARG(n * c * bpc < (int64_t(1) << 31), "grid too large");
   const size_t need =
       mednext_depthwise3d_s2_wgrad_workspace_bytes(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype);
   MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
   auto s = static_cast<hipStream_t>(stream);
-#define MEDNEXT_S2W_K(T)                                                                              \
-  switch (kernel_size) {                                                                              \
-    case 1: return launch_s2_wgrad_k<T, 1>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, per_block, s); \
-    case 3: return launch_s2_wgrad_k<T, 3>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, per_block, s); \
-    default: return launch_s2_wgrad_k<T, 5>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, per_block, s); \
+#define MEDNEXT_S2W_K(T)                                                                            \
+  switch (kernel_size) {                                                                            \
+    case 1: return launch_s2_wgrad_k<T, 1>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, s); \
+    case 3: return launch_s2_wgrad_k<T, 3>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, s); \
+    default: return launch_s2_wgrad_k<T, 5>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, s); \
   }
   switch (dtype) {
     case MEDNEXT_DTYPE_F32: MEDNEXT_S2W_K(float)
