@@ -52,6 +52,13 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--train-size", type=int, default=128)
     ap.add_argument("--no-eager-step", action="store_true", help="time only the HIP-backed training step")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    ap.add_argument("--train-only", action="store_true", help="time only the MedNeXt-Base training step(s)")
+    ap.add_argument(
+        "--sweep",
+        action="store_true",
+        help="instead of the headline line, print one JSON line per kernel phase of the configs[1] stage sweep "
+        "(depthwise k3/k5 fwd, dX, dW; stride-2 maps; GroupNorm; pointwise GEMMs) and exit",
+    )
     ap.add_argument(
         "--copy-calibration",
         action="store_true",
@@ -61,7 +68,29 @@ def parse_args() -> argparse.Namespace:
     return ap.parse_args()
 
 
-def time_depthwise(args, torch, hip_ops):
+class GpuLead:
+    """Keeps the GPU busy while the host enqueues a timed region, so that HIP
+    event intervals measure kernel time rather than Python launch overhead.
+    torch.cuda._sleep spins for a number of GPU clock cycles; the rate is
+    calibrated once with events."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1 << 16)
+        torch.cuda.synchronize()
+        cycles = 1 << 22
+        start.record()
+        torch.cuda._sleep(cycles)
+        end.record()
+        torch.cuda.synchronize()
+        self.cycles_per_ms = cycles / max(1e-3, start.elapsed_time(end))
+
+    def __call__(self, ms: float) -> None:
+        self.torch.cuda._sleep(int(ms * self.cycles_per_ms))
+
+
+def time_depthwise(args, torch, hip_ops, lead: GpuLead):
     dev = torch.device("cuda:0")
     c, s, k = args.channels, args.size, args.kernel_size
     shape = (1, c, s, s, s)
@@ -106,11 +135,14 @@ def time_depthwise(args, torch, hip_ops):
     torch.cuda.synchronize()
     all_events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
     torch.cuda.synchronize()
+    # The GPU spins ~30 ms first, so the host has enqueued the timed steps
+    # before the first of them starts and the phase events bracket kernel time.
+    lead(30.0)
     wall0 = time.perf_counter()
     for i, ev in enumerate(all_events):
         step(i, ev)
+    enqueue = time.perf_counter() - wall0
     torch.cuda.synchronize()
-    wall = time.perf_counter() - wall0
     phase_ms = {
         "forward": [ev[0].elapsed_time(ev[1]) for ev in all_events],
         "input_grad": [ev[1].elapsed_time(ev[2]) for ev in all_events],
@@ -126,7 +158,7 @@ def time_depthwise(args, torch, hip_ops):
         "mean_ms": mean_ms,
         "median_us": median_us,
         "step_ms": step_ms,
-        "wall_ms_per_step": 1000.0 * wall / max(1, args.steps),
+        "host_enqueue_ms_per_step": 1000.0 * enqueue / max(1, args.steps),
         "gbs": 3 * bytes_per_phase / (step_ms * 1e-3) / 1e9,
     }
 
@@ -254,6 +286,139 @@ def cpu_baseline(args, torch):
         ),
     }
 
+STAGE_SHAPES = ((32, 128), (64, 64), (128, 32), (256, 16), (512, 8))
+# MedNeXt-Base expansion ratios of the encoder stages 0-4 (stage 4 = bottleneck).
+BASE_RATIOS = (2, 3, 4, 4, 4)
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 768 << 20  # rotate inputs over > 3x the 256 MiB Infinity Cache
+
+
+def _timed_launches(torch, lead: GpuLead, launch, sets: int, reps: int) -> float:
+    """Mean microseconds per launch of ``launch(i)`` over ``reps`` launches
+    bracketed by two events, inputs rotated over ``sets`` resident copies."""
+    for i in range(min(reps, 3)):
+        launch(i % sets)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    lead(20.0)
+    start.record()
+    for i in range(reps):
+        launch(i % sets)
+    end.record()
+    torch.cuda.synchronize()
+    return 1000.0 * start.elapsed_time(end) / reps
+
+
+def _emit(record: dict) -> None:
+    print(json.dumps(record), flush=True)
+
+
+def sweep(args, torch, hip_ops, lead: GpuLead) -> None:
+    """configs[1] stage sweep (depthwise k3/k5 fwd, dX, dW at every MedNeXt
+    stage shape, N=1, bf16) plus the other kernels of the training step at the
+    same shapes: stride-2 gather / scatter / reduce, GroupNorm forward and
+    backward, and the four pointwise GEMMs of a fused MedNeXt-Base block
+    expansion. One JSON line per kernel phase: mean microseconds per launch
+    (events around ``reps`` back-to-back launches, the GPU kept ahead of the
+    host), algorithmic bytes, GB/s and, for the GEMMs, TFLOP/s."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(1234)
+    reps = 40
+
+    def randn(*shape):
+        return torch.randn(shape, generator=gen, device=dev).bfloat16()
+
+    def record(op, shape, us, nbytes, flops=None, **extra):
+        rec = {"op": op, "shape": shape, "us": round(us, 2), "bytes": nbytes,
+               "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if flops is not None:
+            tf = flops / (us * 1e-6) / 1e12
+            rec.update(tflops=round(tf, 2), mfma_frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4))
+        rec.update(extra)
+        _emit(rec)
+
+    for (c, s), ratio in zip(STAGE_SHAPES, BASE_RATIOS):
+        e = c * s**3
+        nsets = max(1, min(24, -(-ROTATE_BYTES // (4 * e))))
+        xs = [randn(1, c, s, s, s) for _ in range(nsets)]
+        dys = [randn(1, c, s, s, s) for _ in range(nsets)]
+        shape = f"1x{c}x{s}^3"
+        for k in (3, 5):
+            bound = 1.0 / (k**3) ** 0.5
+            w = ((torch.rand(c, 1, k, k, k, generator=gen, device=dev) * 2 - 1) * bound).bfloat16()
+            b = ((torch.rand(c, generator=gen, device=dev) * 2 - 1) * bound).bfloat16()
+            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_forward(xs[i], w, b), nsets, reps)
+            record(f"depthwise_k{k}_forward", shape, us, 4 * e)
+            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_input_grad(dys[i], w), nsets, reps)
+            record(f"depthwise_k{k}_input_grad", shape, us, 4 * e)
+            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_weight_grad(xs[i], dys[i], k), nsets, reps)
+            record(f"depthwise_k{k}_weight_grad", shape, us, 4 * e)
+        if s >= 16:
+            # Stride-2 maps of the down block entering the next stage (C -> C at S -> S/2), k3.
+            small = hip_ops.strided_spatial((s, s, s))
+            es = c * small[0] * small[1] * small[2]
+            w3 = randn(c, 1, 3, 3, 3) * 0.2
+            smalls = [randn(1, c, *small) for _ in range(nsets)]
+            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_gather(xs[i], w3, None, small), nsets, reps)
+            record("depthwise_s2_k3_gather", shape, us, 2 * (e + es))
+            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_scatter(smalls[i], w3, None, (s, s, s)), nsets, reps)
+            record("depthwise_s2_k3_scatter", shape, us, 2 * (e + es))
+            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_wgrad(xs[i], smalls[i], 3), nsets, reps)
+            record("depthwise_s2_k3_wgrad", shape, us, 2 * (e + es))
+            del smalls
+        gamma = torch.ones(c, device=dev)
+        beta = torch.zeros(c, device=dev)
+        # Autocast form: bf16 in, fp32 out (forward); fp32 dy, bf16 x, bf16 dx (backward).
+        us = _timed_launches(torch, lead, lambda i: hip_ops.group_norm_forward(xs[i], gamma, beta, out_dtype=torch.float32), nsets, reps)
+        record("group_norm_forward_bf16_to_fp32", shape, us, 2 * e + 2 * e + 4 * e)
+        us = _timed_launches(torch, lead, lambda i: hip_ops.group_norm_forward(xs[i], gamma, beta, out_dtype=torch.bfloat16), nsets, reps)
+        record("group_norm_forward_bf16", shape, us, 2 * e + 2 * e + 2 * e)
+        _, mean, rstd = hip_ops.group_norm_forward(xs[0], gamma, beta)
+        dys32 = [t.float() for t in dys[: max(1, nsets // 2)]]
+        us = _timed_launches(
+            torch, lead, lambda i: hip_ops.group_norm_backward(dys32[i], xs[i], mean, rstd, gamma), len(dys32), reps
+        )
+        record("group_norm_backward_fp32dy", shape, us, 2 * (4 * e + 2 * e) + 2 * e)
+        del dys32
+        # Pointwise GEMMs of a fused block expansion C -> R*C -> C at this stage
+        # (stages whose hidden width exceeds the matrix-core kernel's K limit run
+        # PyTorch's GEMMs in the model and are not swept).
+        m = ratio * c
+        from mednext_accel_amd.tiles import pointwise_supported
+
+        if not pointwise_supported(c, m, s**3):
+            del xs, dys
+            torch.cuda.empty_cache()
+            continue
+        hs = [randn(1, m, s, s, s) for _ in range(max(1, nsets // ratio))]
+        nh = len(hs)
+        w1 = randn(m, c, 1, 1, 1) * 0.1
+        b1 = randn(m) * 0.1
+        w2 = randn(c, m, 1, 1, 1) * 0.1
+        b2 = randn(c) * 0.1
+        v = s**3
+        fl = 2 * m * c * v
+        P = hip_ops
+        us = _timed_launches(torch, lead, lambda i: P.pointwise_conv(xs[i % nh], w1, b1), nh, reps)
+        record("pointwise_expand_fwd", f"{shape} {c}->{m}", us, 2 * v * (c + m), fl)
+        us = _timed_launches(
+            torch, lead,
+            lambda i: P.pointwise_conv(hs[i], w2, b2, aux=xs[i], prologue=P.PW_PROLOGUE_GELU, epilogue=P.PW_EPILOGUE_BIAS_RESIDUAL),
+            nh, reps)
+        record("pointwise_project_fwd_gelu_residual", f"{shape} {m}->{c}", us, 2 * v * (m + 2 * c), fl)
+        us = _timed_launches(
+            torch, lead,
+            lambda i: P.pointwise_conv(dys[i], w2, aux=hs[i], epilogue=P.PW_EPILOGUE_GELU_GRAD, transpose=True), nh, reps)
+        record("pointwise_project_dgrad_gelu_grad", f"{shape} {c}->{m}", us, 2 * v * (c + 2 * m), fl)
+        us = _timed_launches(torch, lead, lambda i: P.pointwise_weight_grad(dys[i], hs[i], prologue=P.PW_PROLOGUE_GELU), nh, reps)
+        record("pointwise_project_wgrad_gelu", f"{shape} {m}x{c}", us, 2 * v * (m + c), fl)
+        us = _timed_launches(torch, lead, lambda i: P.pointwise_weight_grad(hs[i], xs[i]), nh, reps)
+        record("pointwise_expand_wgrad", f"{shape} {m}x{c}", us, 2 * v * (m + c), fl)
+        us = _timed_launches(torch, lead, lambda i: P.pointwise_conv(hs[i], w1, transpose=True), nh, reps)
+        record("pointwise_expand_dgrad", f"{shape} {m}->{c}", us, 2 * v * (m + c), fl)
+        del xs, dys, hs
+        torch.cuda.empty_cache()
+
 
 def main() -> int:
     args = parse_args()
@@ -271,7 +436,14 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
-    dw = time_depthwise(args, torch, hip_ops)
+    lead = GpuLead(torch)
+    if args.sweep:
+        sweep(args, torch, hip_ops, lead)
+        return 0
+    if args.train_only:
+        print(json.dumps({"train_step_hip": time_train_step(args, torch, "auto")}))
+        return 0
+    dw = time_depthwise(args, torch, hip_ops, lead)
     ceiling = time_copy_ceiling(torch)
     phase_us = {name: round(1000.0 * ms, 2) for name, ms in dw["mean_ms"].items()}
     dominant = max(dw["mean_ms"], key=dw["mean_ms"].get)
@@ -315,7 +487,7 @@ def main() -> int:
             "hbm_frac_of_peak": round(dw["gbs"] / HBM_PEAK_GBS, 4),
             "phase_us": phase_us,
             "phase_median_us": {k: round(v, 2) for k, v in dw["median_us"].items()},
-            "wall_ms_per_step": round(dw["wall_ms_per_step"], 4),
+            "host_enqueue_ms_per_step": round(dw["host_enqueue_ms_per_step"], 4),
             "copy_ceiling": ceiling,
         },
         "roofline": roofline,
