@@ -128,6 +128,74 @@ __device__ inline void store4<f16_t, float>(f16_t* __restrict__ p, const float i
   *reinterpret_cast<h4*>(p) = v;
 }
 
+// Eight consecutive elements as 16-byte vector accesses (one for 16-bit
+// types, two for fp32, four for fp64). The caller guarantees that the address
+// is aligned to 8 elements.
+template <typename T, typename Acc>
+__device__ inline void load8(const T* __restrict__ p, Acc (&out)[8]) {
+  load4<T, Acc>(p, out);
+  load4<T, Acc>(p + 4, out + 4);
+}
+template <>
+__device__ inline void load8<bf16_t, float>(const bf16_t* __restrict__ p, float (&out)[8]) {
+  const uint4 v = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+template <>
+__device__ inline void load8<f16_t, float>(const f16_t* __restrict__ p, float (&out)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 v = *reinterpret_cast<const h8*>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(v[i]);
+}
+template <typename T, typename Acc>
+__device__ inline void store8(T* __restrict__ p, const Acc (&in)[8]) {
+  store4<T, Acc>(p, in);
+  store4<T, Acc>(p + 4, in + 4);
+}
+template <>
+__device__ inline void store8<bf16_t, float>(bf16_t* __restrict__ p, const float (&in)[8]) {
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = static_cast<uint32_t>(f32_to_bf16(in[2 * i])) | (static_cast<uint32_t>(f32_to_bf16(in[2 * i + 1])) << 16);
+  *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+}
+template <>
+__device__ inline void store8<f16_t, float>(f16_t* __restrict__ p, const float (&in)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  h8 v;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) v[i] = static_cast<_Float16>(in[i]);
+  *reinterpret_cast<h8*>(p) = v;
+}
+
+// Element ranges of a row chunk that starts at global element `base` and has
+// `len` elements: a scalar head up to the next 8-element boundary, `nvec`
+// aligned 8-element vectors, then a scalar tail from `tail0`. Without
+// `vec_ok` (tensor pointers not 64-byte aligned) everything is scalar.
+struct RowSpan {
+  int64_t head, nvec, tail0, len;
+  __device__ int64_t scalar_count() const { return head + (len - tail0); }
+  __device__ int64_t scalar_index(int64_t i) const { return i < head ? i : tail0 + (i - head); }
+};
+__device__ inline RowSpan row_span(int64_t base, int64_t len, bool vec_ok) {
+  RowSpan s;
+  if (len < 0) len = 0;  // a trailing split past the row end is empty
+  int64_t h = vec_ok ? ((8 - (base & 7)) & 7) : len;
+  if (h > len) h = len;
+  s.head = h;
+  s.nvec = (len - h) >> 3;
+  s.tail0 = h + (s.nvec << 3);
+  s.len = len;
+  return s;
+}
+
 // Wave64 sum via cross-lane shuffles (fixed butterfly order: deterministic).
 template <typename Acc>
 __device__ inline Acc wave_sum(Acc v) {

@@ -89,33 +89,45 @@ __device__ inline void combine_row(const double* __restrict__ part, int64_t row,
   b = comb[1];
 }
 
+// Vector loops keep kUnroll 8-element vectors per thread in flight.
+constexpr int kUnroll = 4;
+
 template <typename Tx>
 __global__ __launch_bounds__(kThreads) void gn_stats_kernel(const Tx* __restrict__ x, int64_t v,
-                                                            int splits, int64_t chunk,
+                                                            int splits, int64_t chunk, bool vec_ok,
                                                             double* __restrict__ part) {
   using Acc = typename AccOf<Tx>::type;
   const Chunk ck = chunk_of_block(v, splits, chunk);
   const Tx* __restrict__ row = x + ck.row * v;
   const Acc shift = Cvt<Tx, Acc>::load(row[0]);
   Acc s1 = Acc(0), s2 = Acc(0);
-  const bool vec = ((v & 3) == 0) && ((chunk & 3) == 0);
-  if (vec) {
-    for (int64_t i = ck.begin + 4 * threadIdx.x; i < ck.end; i += 4 * blockDim.x) {
-      Acc e[4];
-      load4<Tx, Acc>(row + i, e);
+  const Tx* __restrict__ cp = row + ck.begin;
+  const RowSpan rs = row_span(ck.row * v + ck.begin, ck.end - ck.begin, vec_ok);
+  for (int64_t i = threadIdx.x; i < rs.scalar_count(); i += blockDim.x) {
+    const Acc d = Cvt<Tx, Acc>::load(cp[rs.scalar_index(i)]) - shift;
+    s1 += d;
+    s2 += d * d;
+  }
+  for (int64_t j0 = threadIdx.x; j0 < rs.nvec; j0 += kUnroll * blockDim.x) {
+    Acc e[kUnroll][8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const Acc d = e[j] - shift;
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = j0 + u * static_cast<int64_t>(blockDim.x);
+      if (j < rs.nvec) {
+        load8<Tx, Acc>(cp + rs.head + 8 * j, e[u]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) e[u][t] = shift;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const Acc d = e[u][t] - shift;
         s1 += d;
         s2 += d * d;
       }
-    }
-  } else {
-    for (int64_t i = ck.begin + threadIdx.x; i < ck.end; i += blockDim.x) {
-      const Acc d = Cvt<Tx, Acc>::load(row[i]) - shift;
-      s1 += d;
-      s2 += d * d;
-    }
   }
   double a = s1, b = s2;
   block_sum2(a, b);
@@ -129,7 +141,7 @@ template <typename Tx, typename Ty>
 __global__ __launch_bounds__(kThreads) void gn_apply_kernel(
     const Tx* __restrict__ x, const void* __restrict__ gamma, const void* __restrict__ beta,
     int pdtype, Ty* __restrict__ y, void* __restrict__ mean_out, void* __restrict__ rstd_out,
-    int64_t c, int64_t v, double eps, int splits, int64_t chunk, const double* __restrict__ part) {
+    int64_t c, int64_t v, double eps, int splits, int64_t chunk, bool vec_ok, const double* __restrict__ part) {
   using Acc = typename AccOf<Tx>::type;
   const Chunk ck = chunk_of_block(v, splits, chunk);
   const Tx* __restrict__ row = x + ck.row * v;
@@ -159,18 +171,28 @@ __global__ __launch_bounds__(kThreads) void gn_apply_kernel(
       static_cast<float*>(rstd_out)[ck.row] = static_cast<float>(rstd);
     }
   }
-  const bool vec = ((v & 3) == 0) && ((chunk & 3) == 0);
-  if (vec) {
-    for (int64_t i = ck.begin + 4 * threadIdx.x; i < ck.end; i += 4 * blockDim.x) {
-      Acc e[4];
-      load4<Tx, Acc>(row + i, e);
+  const Tx* __restrict__ cp = row + ck.begin;
+  Ty* __restrict__ op = out + ck.begin;
+  const RowSpan rs = row_span(ck.row * v + ck.begin, ck.end - ck.begin, vec_ok);
+  for (int64_t i = threadIdx.x; i < rs.scalar_count(); i += blockDim.x) {
+    const int64_t k = rs.scalar_index(i);
+    op[k] = Cvt<Ty, Acc>::store((Cvt<Tx, Acc>::load(cp[k]) - m_acc) * scale + offset);
+  }
+  for (int64_t j0 = threadIdx.x; j0 < rs.nvec; j0 += kUnroll * blockDim.x) {
+    Acc e[kUnroll][8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) e[j] = (e[j] - m_acc) * scale + offset;
-      store4<Ty, Acc>(out + i, e);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = j0 + u * static_cast<int64_t>(blockDim.x);
+      if (j < rs.nvec) load8<Tx, Acc>(cp + rs.head + 8 * j, e[u]);
     }
-  } else {
-    for (int64_t i = ck.begin + threadIdx.x; i < ck.end; i += blockDim.x) {
-      out[i] = Cvt<Ty, Acc>::store((Cvt<Tx, Acc>::load(row[i]) - m_acc) * scale + offset);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = j0 + u * static_cast<int64_t>(blockDim.x);
+      if (j < rs.nvec) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) e[u][t] = (e[u][t] - m_acc) * scale + offset;
+        store8<Ty, Acc>(op + rs.head + 8 * j, e[u]);
+      }
     }
   }
 }
@@ -183,7 +205,8 @@ __device__ inline double load_stat(const void* p, int64_t i) {
 template <typename Tdy, typename Tx>
 __global__ __launch_bounds__(kThreads) void gn_bwd_reduce_kernel(
     const Tdy* __restrict__ dy, const Tx* __restrict__ x, const void* __restrict__ mean,
-    const void* __restrict__ rstd, int64_t v, int splits, int64_t chunk, double* __restrict__ part) {
+    const void* __restrict__ rstd, int64_t v, int splits, int64_t chunk, bool vec_ok,
+    double* __restrict__ part) {
   using Acc = typename AccOf<Tx>::type;
   const Chunk ck = chunk_of_block(v, splits, chunk);
   const Tx* __restrict__ xr = x + ck.row * v;
@@ -191,24 +214,38 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_reduce_kernel(
   const Acc m = static_cast<Acc>(load_stat<Acc>(mean, ck.row));
   const Acc r = static_cast<Acc>(load_stat<Acc>(rstd, ck.row));
   Acc sa = Acc(0), sb = Acc(0);
-  const bool vec = ((v & 3) == 0) && ((chunk & 3) == 0);
-  if (vec) {
-    for (int64_t i = ck.begin + 4 * threadIdx.x; i < ck.end; i += 4 * blockDim.x) {
-      Acc xe[4], ge[4];
-      load4<Tx, Acc>(xr + i, xe);
-      load4<Tdy, Acc>(gr + i, ge);
+  const Tx* __restrict__ xp = xr + ck.begin;
+  const Tdy* __restrict__ gp = gr + ck.begin;
+  const RowSpan rs = row_span(ck.row * v + ck.begin, ck.end - ck.begin, vec_ok);
+  for (int64_t i = threadIdx.x; i < rs.scalar_count(); i += blockDim.x) {
+    const int64_t k = rs.scalar_index(i);
+    const Acc ge = Cvt<Tdy, Acc>::load(gp[k]);
+    sa += ge;
+    sb += ge * ((Cvt<Tx, Acc>::load(xp[k]) - m) * r);
+  }
+  for (int64_t j0 = threadIdx.x; j0 < rs.nvec; j0 += kUnroll * blockDim.x) {
+    Acc xe[kUnroll][8], ge[kUnroll][8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sa += ge[j];
-        sb += ge[j] * ((xe[j] - m) * r);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = j0 + u * static_cast<int64_t>(blockDim.x);
+      if (j < rs.nvec) {
+        load8<Tx, Acc>(xp + rs.head + 8 * j, xe[u]);
+        load8<Tdy, Acc>(gp + rs.head + 8 * j, ge[u]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          xe[u][t] = m;
+          ge[u][t] = Acc(0);
+        }
       }
     }
-  } else {
-    for (int64_t i = ck.begin + threadIdx.x; i < ck.end; i += blockDim.x) {
-      const Acc ge = Cvt<Tdy, Acc>::load(gr[i]);
-      sa += ge;
-      sb += ge * ((Cvt<Tx, Acc>::load(xr[i]) - m) * r);
-    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        sa += ge[u][t];
+        sb += ge[u][t] * ((xe[u][t] - m) * r);
+      }
   }
   double a = sa, b = sb;
   block_sum2(a, b);
@@ -222,7 +259,7 @@ template <typename Tdy, typename Tx>
 __global__ __launch_bounds__(kThreads) void gn_bwd_apply_kernel(
     const Tdy* __restrict__ dy, const Tx* __restrict__ x, const void* __restrict__ mean,
     const void* __restrict__ rstd, const void* __restrict__ gamma, int pdtype,
-    Tx* __restrict__ dx, int64_t c, int64_t v, int splits, int64_t chunk,
+    Tx* __restrict__ dx, int64_t c, int64_t v, int splits, int64_t chunk, bool vec_ok,
     const double* __restrict__ part, double* __restrict__ rows_out) {
   using Acc = typename AccOf<Tx>::type;
   const Chunk ck = chunk_of_block(v, splits, chunk);
@@ -246,21 +283,34 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_apply_kernel(
   const Acc kb = static_cast<Acc>(r * g * sb * inv_n);
   const Acc mf = static_cast<Acc>(m);
   const Acc rf = static_cast<Acc>(r);
-  const bool vec = ((v & 3) == 0) && ((chunk & 3) == 0);
-  if (vec) {
-    for (int64_t i = ck.begin + 4 * threadIdx.x; i < ck.end; i += 4 * blockDim.x) {
-      Acc xe[4], ge[4];
-      load4<Tx, Acc>(xr + i, xe);
-      load4<Tdy, Acc>(gr + i, ge);
+  const Tx* __restrict__ xp = xr + ck.begin;
+  const Tdy* __restrict__ gp = gr + ck.begin;
+  Tx* __restrict__ op = out + ck.begin;
+  const RowSpan rs = row_span(ck.row * v + ck.begin, ck.end - ck.begin, vec_ok);
+  for (int64_t i = threadIdx.x; i < rs.scalar_count(); i += blockDim.x) {
+    const int64_t k = rs.scalar_index(i);
+    const Acc xe = Cvt<Tx, Acc>::load(xp[k]);
+    const Acc ge = Cvt<Tdy, Acc>::load(gp[k]);
+    op[k] = Cvt<Tx, Acc>::store(k1 * (ge - ma) - ((xe - mf) * rf) * kb);
+  }
+  for (int64_t j0 = threadIdx.x; j0 < rs.nvec; j0 += kUnroll * blockDim.x) {
+    Acc xe[kUnroll][8], ge[kUnroll][8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xe[j] = k1 * (ge[j] - ma) - ((xe[j] - mf) * rf) * kb;
-      store4<Tx, Acc>(out + i, xe);
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = j0 + u * static_cast<int64_t>(blockDim.x);
+      if (j < rs.nvec) {
+        load8<Tx, Acc>(xp + rs.head + 8 * j, xe[u]);
+        load8<Tdy, Acc>(gp + rs.head + 8 * j, ge[u]);
+      }
     }
-  } else {
-    for (int64_t i = ck.begin + threadIdx.x; i < ck.end; i += blockDim.x) {
-      const Acc xe = Cvt<Tx, Acc>::load(xr[i]);
-      const Acc ge = Cvt<Tdy, Acc>::load(gr[i]);
-      out[i] = Cvt<Tx, Acc>::store(k1 * (ge - ma) - ((xe - mf) * rf) * kb);
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t j = j0 + u * static_cast<int64_t>(blockDim.x);
+      if (j < rs.nvec) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) xe[u][t] = k1 * (ge[u][t] - ma) - ((xe[u][t] - mf) * rf) * kb;
+        store8<Tx, Acc>(op + rs.head + 8 * j, xe[u]);
+      }
     }
   }
 }
@@ -285,8 +335,12 @@ bool dtype_ok(int d) { return d >= MEDNEXT_DTYPE_F32 && d <= MEDNEXT_DTYPE_BF16;
 
 int64_t chunk_len(int64_t v, int splits) {
   int64_t ch = cdiv(v, splits);
-  return cdiv(ch, 4) * 4;  // keep chunk starts 4-element aligned
+  return cdiv(ch, 8) * 8;  // chunk starts stay 8-element aligned relative to the row
 }
+
+// Vector accesses assume every tensor's base is 64-byte aligned (8 elements of
+// up to 8 bytes), so that global element index % 8 decides alignment.
+bool aligned64(const void* p) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & 63u) == 0; }
 
 size_t workspace_need(int64_t n, int64_t c, int splits) {
   return static_cast<size_t>(n * c * (static_cast<int64_t>(splits) + 1) * 2 * sizeof(double));
@@ -298,12 +352,13 @@ int gn_fwd_typed(const void* x, const void* gamma, const void* beta, int pdtype,
                  double* part, hipStream_t st) {
   const int64_t chunk = chunk_len(v, splits);
   const int64_t blocks = n * c * splits;
+  const bool vec_ok = aligned64(x) && aligned64(y);
   hipLaunchKernelGGL((gn_stats_kernel<Tx>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                     0, st, static_cast<const Tx*>(x), v, splits, chunk, part);
+                     0, st, static_cast<const Tx*>(x), v, splits, chunk, vec_ok, part);
   MEDNEXT_CHECK_LAUNCH();
   hipLaunchKernelGGL((gn_apply_kernel<Tx, Ty>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kThreads), 0, st, static_cast<const Tx*>(x), gamma, beta, pdtype,
-                     static_cast<Ty*>(y), mean, rstd, c, v, eps, splits, chunk, part);
+                     static_cast<Ty*>(y), mean, rstd, c, v, eps, splits, chunk, vec_ok, part);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }
@@ -315,14 +370,15 @@ int gn_bwd_typed(const void* dy, const void* x, const void* mean, const void* rs
   const int64_t chunk = chunk_len(v, splits);
   const int64_t blocks = n * c * splits;
   double* rows = part + n * c * splits * 2;
+  const bool vec_ok = aligned64(dy) && aligned64(x) && aligned64(dx);
   hipLaunchKernelGGL((gn_bwd_reduce_kernel<Tdy, Tx>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kThreads), 0, st, static_cast<const Tdy*>(dy),
-                     static_cast<const Tx*>(x), mean, rstd, v, splits, chunk, part);
+                     static_cast<const Tx*>(x), mean, rstd, v, splits, chunk, vec_ok, part);
   MEDNEXT_CHECK_LAUNCH();
   hipLaunchKernelGGL((gn_bwd_apply_kernel<Tdy, Tx>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kThreads), 0, st, static_cast<const Tdy*>(dy),
                      static_cast<const Tx*>(x), mean, rstd, gamma, pdtype, static_cast<Tx*>(dx),
-                     c, v, splits, chunk, part, rows);
+                     c, v, splits, chunk, vec_ok, part, rows);
   MEDNEXT_CHECK_LAUNCH();
   if (dgamma || dbeta) {
     hipLaunchKernelGGL(gn_param_grad_kernel, dim3(static_cast<unsigned>(cdiv(c, 256))),

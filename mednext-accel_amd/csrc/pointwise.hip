@@ -33,6 +33,7 @@
 // Mathematical Functions, eq. 7.1.26 (|error| <= 1.5e-7), far below the bf16
 // rounding the results get.
 #include <algorithm>
+#include <type_traits>
 
 #include "cdna4.h"
 #include "common.h"
@@ -41,16 +42,19 @@ namespace mednext {
 namespace {
 
 constexpr int kPwThreads = 256;  // 4 waves
-constexpr int kPwMT = 4;         // 16-row m-tiles per workgroup -> 64 output rows
-constexpr int kPwRows = 16 * kPwMT;
-constexpr int kChunk = 128;      // voxels per wave step (16 columns x 8 MFMAs)
-constexpr int kMaxK = 512;       // LDS weight block: 64 x K bf16 <= 64 KiB
+constexpr int kChunk = 128;      // voxels per wave task (16 MFMA columns x 8 MFMAs)
+constexpr int kMaxK = 2048;      // LDS weight block: 16 x 2048 bf16 = 64 KiB
+constexpr size_t kMaxWeightLds = 64 * 1024;
+constexpr int kResidentWgs = 2 * 256;  // two 4-wave workgroups per CU fill the chip
 
 struct PwGeom {
-  int K, M;          // GEMM reduction and output rows
-  uint32_t V;        // voxels per sample
-  int chunks;        // ceil(V / kChunk)
-  int wt;            // 1: weight stored [K][M] (A = W^T), 0: [M][K]
+  int K, M;
+  int ks;       // ceil(K / 32) slices of 32 channels
+  uint32_t V;
+  int chunks;   // ceil(V / kChunk)
+  int mgroups;  // ceil(M / (16 * MT))
+  int wgs;      // workgroups per (sample, row group)
+  int wt;       // 1: weight stored [K][M] (A = W^T), 0: [M][K]
 };
 
 __device__ inline float erf_as(float x) {
@@ -67,10 +71,20 @@ __device__ inline float erf_as(float x) {
 
 __device__ inline float gelu_f(float h) { return 0.5f * h * (1.0f + erf_as(h * 0.7071067811865476f)); }
 
-// d/dh of h * Phi(h) = Phi(h) + h * phi(h).
+// d/dh of h * Phi(h) = Phi(h) + h * phi(h); phi(h) = exp(-h^2 / 2) / sqrt(2 pi)
+// shares its exponential with the erf approximation.
 __device__ inline float gelu_grad_f(float h) {
-  const float cdf = 0.5f * (1.0f + erf_as(h * 0.7071067811865476f));
-  return fmaf(h * 0.3989422804014327f, __expf(-0.5f * h * h), cdf);
+  const float ax = fabsf(h) * 0.7071067811865476f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, ax, 1.0f));
+  float p = fmaf(1.061405429f, t, -1.453152027f);
+  p = fmaf(p, t, 1.421413741f);
+  p = fmaf(p, t, -0.284496736f);
+  p = fmaf(p, t, 0.254829592f);
+  p *= t;
+  const float e = __expf(-ax * ax);
+  const float erf_abs = 1.0f - p * e;
+  const float cdf = 0.5f + 0.5f * copysignf(erf_abs, h);
+  return fmaf(h * 0.3989422804014327f, e, cdf);
 }
 
 __device__ inline uint32_t gelu_word(uint32_t w) {
@@ -100,316 +114,751 @@ __device__ inline void transpose8x8(const uint4 (&raw)[8], uint4 (&bv)[8]) {
   }
 }
 
-// Weight block [m0, m0 + 64) x [0, K) into LDS in A-fragment order: fragment
-// (ks, mt) is 64 lanes x 16 bytes at ((ks * kPwMT + mt) * 64 + lane) * 16.
-__device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, const PwGeom& g, int m0) {
-  const int tid = threadIdx.x;
-  if (!g.wt) {
-    const int per_row = g.K / 8;
-    for (int p = tid; p < kPwRows * per_row; p += kPwThreads) {
-      const int r = p / per_row, k8 = (p % per_row) * 8;
-      const int m = m0 + r;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (m < g.M) v = *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(m) * g.K + k8);
-      const int ks = k8 / 32, q = (k8 % 32) / 8, mt = r / 16, c = r % 16;
-      *reinterpret_cast<uint4*>(lds + (((ks * kPwMT + mt) * 64) + q * 16 + c) * 8) = v;
-    }
-  } else {  // w is [K][M]: A[m][k] = w[k][m]
-    for (int p = tid; p < g.K * (kPwRows / 8); p += kPwThreads) {
-      const int k = p / (kPwRows / 8), mg = (p % (kPwRows / 8)) * 8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (m0 + mg < g.M) v = *reinterpret_cast<const uint4*>(w + static_cast<int64_t>(k) * g.M + m0 + mg);
-      const int ks = k / 32, q = (k % 32) / 8, i = k % 8;
+// Eight consecutive bf16 of one row starting at byte `off`, of which only the
+// first `nvalid` (< 8) exist: element loads, zeros for the rest. Used for the
+// last, partial 8-voxel group of a row when V % 8 != 0, so no access reaches
+// past the row.
+__device__ inline uint4 load_partial(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t nvalid) {
+  uint32_t wds[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int r = mg + jj, mt = r / 16, c = r % 16;
-        const uint32_t wd = word(v, jj / 2);
-        lds[(((ks * kPwMT + mt) * 64) + q * 16 + c) * 8 + i] = static_cast<uint16_t>((jj & 1) ? (wd >> 16) : wd);
-      }
+  for (uint32_t e = 0; e < 8; ++e) {
+    if (e < nvalid) {
+      const uint32_t b = __builtin_amdgcn_raw_buffer_load_b16(r, off + 2u * e, 0, 0);
+      wds[e / 2] |= b << (16u * (e & 1u));
+    }
+  }
+  return make_uint4(wds[0], wds[1], wds[2], wds[3]);
+}
+__device__ inline void store_partial(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t nvalid, uint4 v) {
+#pragma unroll
+  for (uint32_t e = 0; e < 8; ++e) {
+    if (e < nvalid) {
+      const uint32_t wd = word(v, static_cast<int>(e / 2));
+      __builtin_amdgcn_raw_buffer_store_b16(static_cast<unsigned short>(wd >> (16u * (e & 1u))), r, off + 2u * e,
+                                            0, 0);
     }
   }
 }
 
-template <int PRO, int EPI>
-__global__ __launch_bounds__(kPwThreads) void pw_fwd_kernel(const bf16_t* __restrict__ x,
-                                                            const bf16_t* __restrict__ w,
-                                                            const bf16_t* __restrict__ bias,
-                                                            const bf16_t* __restrict__ aux,
-                                                            bf16_t* __restrict__ y, PwGeom g) {
+// One 8-voxel group of a row: a 16-byte load when all 8 voxels exist (the
+// address is only 2-byte aligned when V % 8 != 0), element loads for the
+// partial last group, zeros past the row (nvalid == 0 reads the out-of-range
+// offset).
+__device__ inline uint4 load_group(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t nvalid) {
+  if (nvalid >= 8u) return buf_load16(r, off);
+  if (nvalid == 0u) return buf_load16(r, kOob);
+  return load_partial(r, off, nvalid);
+}
+__device__ inline void store_group(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t nvalid, uint4 v) {
+  if (nvalid >= 8u) {
+    buf_store16(r, off, v);
+  } else if (nvalid > 0u) {
+    store_partial(r, off, nvalid, v);
+  }
+}
+
+// Weight rows [m0, m0 + 16 MT) x [0, 32 KS) into LDS in A-fragment order
+// (KS = ceil(K / 32)): fragment (ks, mt) is 64 lanes x 16 bytes at
+// ((ks * MT + mt) * 64 + lane) * 16; entries outside [0, M) x [0, K) are zero.
+// 16-byte global reads when whole 8-element groups exist, element reads
+// otherwise (only for small, odd-shaped weights).
+template <int MT>
+__device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, const PwGeom& g, int m0) {
+  constexpr int ROWS = 16 * MT;
+  const int tid = threadIdx.x;
+  const int kp = g.ks * 32;
+  const uint16_t* __restrict__ wr = reinterpret_cast<const uint16_t*>(w);
+  if (!g.wt) {  // w is [M][K]
+    const bool vec = g.K % 8 == 0;
+    const int per_row = kp / 8;
+    for (int p = tid; p < ROWS * per_row; p += kPwThreads) {
+      const int r = p / per_row, k8 = (p % per_row) * 8;
+      const int m = m0 + r;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (m < g.M && k8 < g.K) {
+        const int64_t base = static_cast<int64_t>(m) * g.K + k8;
+        if (vec) {
+          v = *reinterpret_cast<const uint4*>(wr + base);
+        } else {
+          uint32_t wd[4] = {0u, 0u, 0u, 0u};
+          for (int e = 0; e < 8 && k8 + e < g.K; ++e) wd[e / 2] |= static_cast<uint32_t>(wr[base + e]) << (16 * (e & 1));
+          v = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        }
+      }
+      const int ks = k8 / 32, q = (k8 % 32) / 8, mt = r / 16, c = r % 16;
+      *reinterpret_cast<uint4*>(lds + (((ks * MT + mt) * 64) + q * 16 + c) * 8) = v;
+    }
+  } else {  // w is [K][M]: A[m][k] = w[k][m]
+    for (int p = tid; p < kp * ROWS; p += kPwThreads) {
+      const int k = p / ROWS, r = p % ROWS;
+      const int m = m0 + r;
+      const uint16_t v = (k < g.K && m < g.M) ? wr[static_cast<int64_t>(k) * g.M + m] : uint16_t{0};
+      const int ks = k / 32, q = (k % 32) / 8, i = k % 8, mt = r / 16, c = r % 16;
+      lds[(((ks * MT + mt) * 64) + q * 16 + c) * 8 + i] = v;
+    }
+  }
+}
+
+// Forward / transposed product. Workgroup = one group of 16 MT output rows
+// (its weight block in LDS) and a grid-stride run of 128-voxel chunks per
+// wave. Per chunk a lane (q, n) loads X[32 ks + 8 q + i][v0 + 8 n + j]
+// (i, j < 8: eight 16-byte loads per 32-channel slice), transposes the 8x8
+// block in registers into the eight B operands, and multiplies every m-tile:
+// C[16 mt + 4 q + r][n] of MFMA j is Y[m0 + 16 mt + 4 q + r][v0 + 8 n + j], so
+// the epilogue stores 8 consecutive voxels (16 bytes) per row and lane.
+//
+// KS > 0: ceil(K / 32) = KS (1 to 4), the slice loop is unrolled and the first slice of the
+// next chunk is loaded before this chunk's epilogue stores; with everything
+// static the compiler's vmcnt waits then never wait for those stores (on CDNA
+// the counter covers stores too). X slices rotate through two register
+// buffers (KS odd alternates their roles per chunk). KS == 0: any K % 32 == 0
+// with a runtime slice loop, prefetching one slice ahead inside a chunk.
+// Channels at or past K read as zero (X rows and weight columns), rows at or
+// past M are not stored, and a row's last partial 8-voxel group (V % 8 != 0)
+// goes through element accesses, so any K <= 2048, M and V are accepted.
+template <int KS, int MT, int PRO, int EPI>
+__global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __restrict__ x,
+                                                               const bf16_t* __restrict__ w,
+                                                               const bf16_t* __restrict__ bias,
+                                                               const bf16_t* __restrict__ aux,
+                                                               bf16_t* __restrict__ y, PwGeom g) {
+  constexpr bool kAux = EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD;
   extern __shared__ __align__(16) uint16_t pw_lds[];
-  const int m0 = blockIdx.y * kPwRows;
-  load_weight_block(w, pw_lds, g, m0);
+  const int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int mg = static_cast<int>(lin % g.mgroups);
+  const int64_t rest = lin / g.mgroups;
+  const int bx = static_cast<int>(rest % g.wgs);
+  const int64_t n = rest / g.wgs;
+  const int m0 = mg * 16 * MT;
+  load_weight_block<MT>(w, pw_lds, g, m0);
+  // Bias of this row group as fp32 after the weight block (zero past M).
+  float* const bias_lds = reinterpret_cast<float*>(pw_lds + static_cast<size_t>(16 * MT) * g.ks * 32);
+  if (threadIdx.x < 16 * MT) {
+    const int m = m0 + threadIdx.x;
+    bias_lds[threadIdx.x] =
+        (EPI != MEDNEXT_PW_EPILOGUE_GELU_GRAD && bias != nullptr && m < g.M) ? bf16_to_f32(bias[m].bits) : 0.f;
+  }
   __syncthreads();
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_col = lane & 15, q = lane >> 4;
-  const int64_t n = blockIdx.z;
   const uint32_t V = g.V;
   const __amdgpu_buffer_rsrc_t xr = slab_rsrc(x + n * g.K * static_cast<int64_t>(V), g.K * V * 2u);
   const __amdgpu_buffer_rsrc_t yr = slab_rsrc(y + n * g.M * static_cast<int64_t>(V), g.M * V * 2u);
   const bf16_t* auxn = aux != nullptr ? aux + n * g.M * static_cast<int64_t>(V) : nullptr;
   const __amdgpu_buffer_rsrc_t ar = slab_rsrc(auxn != nullptr ? auxn : y, auxn != nullptr ? g.M * V * 2u : 0u);
-  const int ksteps = g.K / 32;
-  const int mtiles = min(kPwMT, (g.M - m0) / 16);
+  const int mtiles = min(MT, (g.M - m0 + 15) / 16);
   const uint4* frag = reinterpret_cast<const uint4*>(pw_lds) + lane;
-
-  for (int chunk = blockIdx.x * 4 + wave; chunk < g.chunks; chunk += gridDim.x * 4) {
+  const int cstride = g.wgs * 4;
+  auto valid = [&](int chunk) -> uint32_t {  // voxels of this lane's group that exist
     const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
-    const bool vok = vl < V;
-    f32x4_t acc[kPwMT][8];
+    return (chunk < g.chunks && vl < V) ? min(8u, V - vl) : 0u;
+  };
+  auto load_slice = [&](int chunk, int ks, uint4 (&r)[8]) {
+    const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
+    const uint32_t nv = valid(chunk);
+    const uint32_t row0 = 32u * ks + 8u * q;
+    if (nv == 8u || nv == 0u) {
 #pragma unroll
-    for (int mt = 0; mt < kPwMT; ++mt)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-    uint4 raw[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) raw[i] = buf_load16(xr, vok ? ((8u * q + i) * V + vl) * 2u : kOob);
-    for (int ks = 0; ks < ksteps; ++ks) {
-      uint4 cur[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) cur[i] = raw[i];
-      if (ks + 1 < ksteps) {  // prefetch the next 32 channels
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const uint32_t row = 32u * (ks + 1) + 8u * q + i;
-          raw[i] = buf_load16(xr, vok ? (row * V + vl) * 2u : kOob);
-        }
+      for (int i = 0; i < 8; ++i) {
+        const bool ok = nv != 0u && row0 + i < static_cast<uint32_t>(g.K);
+        r[i] = buf_load16(xr, ok ? ((row0 + i) * V + vl) * 2u : kOob);
       }
-      if (PRO == MEDNEXT_PW_PROLOGUE_GELU) {
+    } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) cur[i] = gelu_vec(cur[i]);
-      }
-      uint4 bv[8];
-      transpose8x8(cur, bv);
-#pragma unroll
-      for (int mt = 0; mt < kPwMT; ++mt) {
-        if (mt < mtiles) {
-          const uint4 a = frag[(ks * kPwMT + mt) * 64];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[mt][j] = mfma16x16x32(a, bv[j], acc[mt][j]);
-        }
+      for (int i = 0; i < 8; ++i) {
+        const bool ok = row0 + i < static_cast<uint32_t>(g.K);
+        r[i] = load_group(xr, ((row0 + i) * V + vl) * 2u, ok ? nv : 0u);
       }
     }
-
-    // Epilogue: row m = m0 + 16 mt + 4 q + r, voxels vl .. vl + 7.
+  };
+  auto mma_slice = [&](const uint4 (&r)[8], int ks, f32x4_t (&acc)[MT][8]) {
+    uint4 cur[8];
 #pragma unroll
-    for (int mt = 0; mt < kPwMT; ++mt) {
+    for (int i = 0; i < 8; ++i) cur[i] = PRO == MEDNEXT_PW_PROLOGUE_GELU ? gelu_vec(r[i]) : r[i];
+    uint4 bv[8];
+    transpose8x8(cur, bv);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt < mtiles) {
+        const uint4 a = frag[(ks * MT + mt) * 64];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[mt][j] = mfma16x16x32(a, bv[j], acc[mt][j]);
+      }
+    }
+  };
+  auto load_aux = [&](int chunk, uint4 (&av)[MT][4]) {
+    if constexpr (kAux) {
+      const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
+      const uint32_t nv = valid(chunk);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = m0 + 16 * mt + 4 * q + r;
+          av[mt][r] = load_group(ar, (static_cast<uint32_t>(min(m, g.M - 1)) * V + vl) * 2u, m < g.M ? nv : 0u);
+        }
+    }
+  };
+  auto epilogue = [&](int chunk, const f32x4_t (&acc)[MT][8], const uint4 (&av)[MT][4]) {
+    const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
+    const uint32_t nv = valid(chunk);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
       if (mt >= mtiles) continue;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = m0 + 16 * mt + 4 * q + r;
-        const uint32_t off = vok ? (static_cast<uint32_t>(m) * V + vl) * 2u : kOob;
+        const int mrow = m0 + 16 * mt + 4 * q + r;
+        const uint32_t m = static_cast<uint32_t>(min(mrow, g.M - 1));
+        const float bv = bias_lds[16 * mt + 4 * q + r];
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = acc[mt][j][r];
-        if (EPI != MEDNEXT_PW_EPILOGUE_GELU_GRAD && bias != nullptr) {
-          const float b = bf16_to_f32(bias[m].bits);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] += b;
-        }
-        if (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU) {
+        for (int j = 0; j < 8; ++j) v[j] = acc[mt][j][r] + bv;
+        if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) v[j] = gelu_f(v[j]);
-        } else if (EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD) {
-          const uint4 a = buf_load16(ar, off);
+        } else if constexpr (kAux) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) {
-            const uint32_t wd = word(a, j / 2);
+            const uint32_t wd = word(av[mt][r], j / 2);
             const float e = (j & 1) ? bf16_hi(wd) : bf16_lo(wd);
             v[j] = EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD ? v[j] * gelu_grad_f(e) : v[j] + e;
           }
         }
-        buf_store16(yr, off,
+        store_group(yr, (m * V + vl) * 2u, mrow < g.M ? nv : 0u,
                     make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
                                pack_bf16x2(v[6], v[7])));
       }
     }
+  };
+
+  int chunk = bx * 4 + wave;
+  if (chunk >= g.chunks) return;  // no barrier follows
+  if constexpr (KS > 0) {
+    uint4 xb[2][8];
+    load_slice(chunk, 0, xb[0]);
+    // One chunk whose slice 0 sits in xb[P]; loads the next chunk's slice 0
+    // into xb[(P + KS) % 2] before storing this chunk's outputs.
+    auto process = [&](auto parity) {
+      constexpr int P = decltype(parity)::value;
+      constexpr int kAuxSlice = KS > 2 ? KS - 2 : 0;  // aux arrives during the last two slices
+      uint4 av[MT][4];
+      f32x4_t acc[MT][8];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks == kAuxSlice) load_aux(chunk, av);
+        if (ks + 1 < KS) {
+          load_slice(chunk, ks + 1, xb[(P + ks + 1) % 2]);
+        } else {
+          load_slice(chunk + cstride, 0, xb[(P + KS) % 2]);
+        }
+        mma_slice(xb[(P + ks) % 2], ks, acc);
+      }
+      epilogue(chunk, acc, av);
+      chunk += cstride;
+    };
+    for (;;) {
+      process(std::integral_constant<int, 0>{});
+      if (chunk >= g.chunks) break;
+      if constexpr (KS % 2 == 1) {
+        process(std::integral_constant<int, 1>{});
+        if (chunk >= g.chunks) break;
+      }
+    }
+  } else {
+    const int ksteps = g.ks;
+    for (; chunk < g.chunks; chunk += cstride) {
+      uint4 av[MT][4];
+      load_aux(chunk, av);
+      f32x4_t acc[MT][8];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      uint4 xa[8], xn[8];
+      load_slice(chunk, 0, xa);
+      int ks = 0;
+      for (; ks + 2 <= ksteps; ks += 2) {
+        load_slice(chunk, ks + 1, xn);
+        mma_slice(xa, ks, acc);
+        if (ks + 2 < ksteps) load_slice(chunk, ks + 2, xa);
+        mma_slice(xn, ks + 1, acc);
+      }
+      if (ks < ksteps) mma_slice(xa, ks, acc);
+      epilogue(chunk, acc, av);
+    }
+  }
+}
+
+// Large-K forward (K >= 256: the stage 3-4 expansions and their input
+// gradients, where V is small and a one-wave-per-chunk K loop would be a long
+// serial chain). The workgroup takes one 128-voxel chunk at a time and its
+// four waves split the 32-channel slices (wave w: slices w, w + 4, ...). The
+// partial accumulators are summed through LDS in wave order (fixed, so the
+// result is reproducible) and wave w then finishes rows 4 q + w of every
+// m-tile.
+template <int MT, int PRO, int EPI>
+__global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16_t* __restrict__ x,
+                                                                      const bf16_t* __restrict__ w,
+                                                                      const bf16_t* __restrict__ bias,
+                                                                      const bf16_t* __restrict__ aux,
+                                                                      bf16_t* __restrict__ y, PwGeom g) {
+  constexpr bool kAux = EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD;
+  extern __shared__ __align__(16) uint16_t pw_lds[];
+  const int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int mg = static_cast<int>(lin % g.mgroups);
+  const int64_t rest = lin / g.mgroups;
+  const int bx = static_cast<int>(rest % g.wgs);
+  const int64_t n = rest / g.wgs;
+  const int m0 = mg * 16 * MT;
+  load_weight_block<MT>(w, pw_lds, g, m0);
+  float* const bias_lds = reinterpret_cast<float*>(pw_lds + static_cast<size_t>(16 * MT) * g.ks * 32);
+  float* const red = bias_lds + 16 * MT;  // [MT][8][4][64] partial sums
+  if (threadIdx.x < 16 * MT) {
+    const int m = m0 + threadIdx.x;
+    bias_lds[threadIdx.x] =
+        (EPI != MEDNEXT_PW_EPILOGUE_GELU_GRAD && bias != nullptr && m < g.M) ? bf16_to_f32(bias[m].bits) : 0.f;
+  }
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_col = lane & 15, q = lane >> 4;
+  const uint32_t V = g.V;
+  const __amdgpu_buffer_rsrc_t xr = slab_rsrc(x + n * g.K * static_cast<int64_t>(V), g.K * V * 2u);
+  const __amdgpu_buffer_rsrc_t yr = slab_rsrc(y + n * g.M * static_cast<int64_t>(V), g.M * V * 2u);
+  const bf16_t* auxn = aux != nullptr ? aux + n * g.M * static_cast<int64_t>(V) : nullptr;
+  const __amdgpu_buffer_rsrc_t ar = slab_rsrc(auxn != nullptr ? auxn : y, auxn != nullptr ? g.M * V * 2u : 0u);
+  const int mtiles = min(MT, (g.M - m0 + 15) / 16);
+  const uint4* frag = reinterpret_cast<const uint4*>(pw_lds) + lane;
+
+  for (int chunk = bx; chunk < g.chunks; chunk += g.wgs) {
+    const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
+    const uint32_t nv = vl < V ? min(8u, V - vl) : 0u;
+    auto load_slice = [&](int ks, uint4 (&r)[8]) {
+      const uint32_t row0 = 32u * ks + 8u * q;
+      const bool in = ks < g.ks;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool ok = in && row0 + i < static_cast<uint32_t>(g.K);
+        if (nv == 8u || nv == 0u) {
+          r[i] = buf_load16(xr, ok && nv != 0u ? ((row0 + i) * V + vl) * 2u : kOob);
+        } else {
+          r[i] = load_group(xr, ((row0 + i) * V + vl) * 2u, ok ? nv : 0u);
+        }
+      }
+    };
+    uint4 av[MT];
+    if constexpr (kAux) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int m = m0 + 16 * mt + 4 * q + wave;
+        av[mt] = load_group(ar, (static_cast<uint32_t>(min(m, g.M - 1)) * V + vl) * 2u, m < g.M ? nv : 0u);
+      }
+    }
+    f32x4_t acc[MT][8];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto mma_slice = [&](const uint4 (&r)[8], int ks) {
+      uint4 cur[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) cur[i] = PRO == MEDNEXT_PW_PROLOGUE_GELU ? gelu_vec(r[i]) : r[i];
+      uint4 bv[8];
+      transpose8x8(cur, bv);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (mt < mtiles) {
+          const uint4 a = frag[(ks * MT + mt) * 64];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[mt][j] = mfma16x16x32(a, bv[j], acc[mt][j]);
+        }
+      }
+    };
+    uint4 xa[8], xn[8];
+    int ks = wave;
+    load_slice(ks, xa);
+    for (; ks + 4 < g.ks; ks += 8) {
+      load_slice(ks + 4, xn);
+      mma_slice(xa, ks);
+      load_slice(ks + 8, xa);
+      mma_slice(xn, ks + 4);
+    }
+    if (ks < g.ks) mma_slice(xa, ks);
+
+#pragma unroll
+    for (int turn = 0; turn < 4; ++turn) {
+      if (wave == turn) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float& e = red[((mt * 8 + j) * 4 + r) * 64 + lane];
+              e = turn == 0 ? acc[mt][j][r] : e + acc[mt][j][r];
+            }
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt >= mtiles) continue;
+      const int mrow = m0 + 16 * mt + 4 * q + wave;
+      const uint32_t m = static_cast<uint32_t>(min(mrow, g.M - 1));
+      const float b = bias_lds[16 * mt + 4 * q + wave];
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = red[((mt * 8 + j) * 4 + wave) * 64 + lane] + b;
+      if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = gelu_f(v[j]);
+      } else if constexpr (kAux) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t wd = word(av[mt], j / 2);
+          const float e = (j & 1) ? bf16_hi(wd) : bf16_lo(wd);
+          v[j] = EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD ? v[j] * gelu_grad_f(e) : v[j] + e;
+        }
+      }
+      store_group(yr, (m * V + vl) * 2u, mrow < g.M ? nv : 0u,
+                  make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                             pack_bf16x2(v[6], v[7])));
+    }
+    __syncthreads();  // the next chunk's turn 0 overwrites the sums read above
   }
 }
 
 // ---------------------------------------------------------------- weight grad
 
-constexpr int kWgTile = 64;  // output tile: 64 rows (M) x 64 columns (K) per workgroup
-constexpr int kWgStep = 32;  // voxels per MFMA step
+constexpr int kWgStage = 128;   // voxels per LDS stage (4 waves x one 32-voxel MFMA step)
+constexpr int kWgPitch = kWgStage + 8;  // LDS row pitch (elements): 272 bytes
 
 struct PwWGeom {
   int K, M;
   uint32_t V;
   int splits;      // workgroups per sample along V
-  uint32_t span;   // voxels per split (multiple of kWgStep)
-  int kblocks;     // ceil(K / 64)
+  uint32_t span;   // voxels per split (multiple of kWgStage)
+  int mblocks, kblocks;
   int64_t stride;  // floats per partial slot: M * K + M
 };
 
-template <int PRO>
-__global__ __launch_bounds__(kPwThreads) void pw_wgrad_kernel(const bf16_t* __restrict__ dy,
-                                                              const bf16_t* __restrict__ x,
-                                                              float* __restrict__ partial, PwWGeom g) {
-  __shared__ float red[kWgTile * kWgTile + kWgTile];
+// dW[M][K] = sum_v dY[M][v] X[K][v] over one split's voxel range, for an output
+// tile of 16 TM rows x 16 TK columns. Per 128-voxel stage the workgroup copies
+// the tile's dY rows and X rows into LDS with row-contiguous 16-byte loads (16
+// lanes cover 256 bytes of one row; GELU applied to X on the way when the
+// prologue asks for it), and wave w multiplies voxels 32 w .. 32 w + 31 of the
+// stage: A = 8 consecutive voxels of a dY row, B = the same voxels of an X row
+// per lane. The next stage's loads are in flight during the MFMAs. dB[m] =
+// sum_v dY[m][v] comes from the same loads: every thread owns fixed rows.
+template <int TM, int TK, int PRO>
+__global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_kernel(const bf16_t* __restrict__ dy,
+                                                                 const bf16_t* __restrict__ x,
+                                                                 float* __restrict__ partial, PwWGeom g) {
+  constexpr int RM = 16 * TM, RK = 16 * TK, ROWS = RM + RK;
+  constexpr int NLD = ROWS * (kWgStage / 8) / kPwThreads;  // 16-byte loads per thread per stage
+  static_assert(NLD * kPwThreads == ROWS * (kWgStage / 8), "rows must fill the workgroup");
+  constexpr int TILE = ROWS * kWgPitch;                     // elements
+  constexpr int RED = RM * RK + RM;                          // floats for the final reduction
+  constexpr int SMEM = (TILE * 2 > RED * 4 ? TILE * 2 : RED * 4);
+  __shared__ __align__(16) unsigned char smem[SMEM];
+  uint16_t* const tile = reinterpret_cast<uint16_t*>(smem);
+  float* const red = reinterpret_cast<float*>(smem);
+
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
-  const int m0 = (blockIdx.y / g.kblocks) * kWgTile;
-  const int k0 = (blockIdx.y % g.kblocks) * kWgTile;
-  const int64_t n = blockIdx.z;
+  const int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int tl = static_cast<int>(lin % (g.mblocks * g.kblocks));
+  const int64_t rest = lin / (g.mblocks * g.kblocks);
+  const int split = static_cast<int>(rest % g.splits);
+  const int64_t n = rest / g.splits;
+  const int m0 = (tl / g.kblocks) * RM;
+  const int k0 = (tl % g.kblocks) * RK;
   const uint32_t V = g.V;
   const __amdgpu_buffer_rsrc_t dr = slab_rsrc(dy + n * g.M * static_cast<int64_t>(V), g.M * V * 2u);
   const __amdgpu_buffer_rsrc_t xr = slab_rsrc(x + n * g.K * static_cast<int64_t>(V), g.K * V * 2u);
-  const uint32_t vbeg = blockIdx.x * g.span;
+  const uint32_t vbeg = static_cast<uint32_t>(split) * g.span;
   const uint32_t vend = min(V, vbeg + g.span);
-
-  bool mrow[4], krow[4];
-  uint32_t mbase[4], kbase[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int m = m0 + 16 * t + c, k = k0 + 16 * t + c;
-    mrow[t] = m < g.M;
-    krow[t] = k < g.K;
-    mbase[t] = static_cast<uint32_t>(m) * V * 2u;
-    kbase[t] = static_cast<uint32_t>(k) * V * 2u;
-  }
   const bool do_bias = k0 == 0;
-  f32x4_t acc[4][4];
-  float dbs[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int a = 0; a < 4; ++a)
-#pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  auto load = [&](uint32_t v0, uint4 (&av)[4], uint4 (&bv)[4]) {
-    const uint32_t vv = v0 + 8u * q;
-    const bool ok = vv < vend;
+  // Load slot u of this thread: tile row r = tid / 16 + 16 u (dY rows first,
+  // then X rows), voxels 8 (tid % 16) .. + 7 of the stage.
+  const int grp = threadIdx.x & 15;
+  uint32_t rbase[NLD];
+  bool rok[NLD];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      av[t] = buf_load16(dr, ok && mrow[t] ? mbase[t] + vv * 2u : kOob);
-      bv[t] = buf_load16(xr, ok && krow[t] ? kbase[t] + vv * 2u : kOob);
+  for (int u = 0; u < NLD; ++u) {
+    const int r = (threadIdx.x >> 4) + 16 * u;
+    const int row = r < RM ? m0 + r : k0 + (r - RM);
+    rok[u] = r < RM ? row < g.M : row < g.K;
+    rbase[u] = static_cast<uint32_t>(rok[u] ? row : 0) * V * 2u;
+  }
+  auto load = [&](uint32_t v, uint4 (&regs)[NLD]) {
+    const uint32_t vv = v + 8u * grp;
+    const uint32_t nv = vv < vend ? min(8u, vend - vv) : 0u;
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+      const int r = (threadIdx.x >> 4) + 16 * u;
+      const __amdgpu_buffer_rsrc_t rs = r < RM ? dr : xr;
+      if (nv == 8u || nv == 0u) {
+        regs[u] = buf_load16(rs, nv != 0u && rok[u] ? rbase[u] + vv * 2u : kOob);
+      } else {
+        regs[u] = load_group(rs, rbase[u] + vv * 2u, rok[u] ? nv : 0u);
+      }
+    }
+  };
+  float dbs[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) dbs[u] = 0.f;
+  auto stash = [&](const uint4 (&regs)[NLD]) {
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+      const int r = (threadIdx.x >> 4) + 16 * u;
+      uint4 v = regs[u];
+      if (r < RM) {
+        if (do_bias) {
+          dbs[u] += (bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y)) +
+                    (bf16_lo(v.z) + bf16_hi(v.z)) + (bf16_lo(v.w) + bf16_hi(v.w));
+        }
+      } else if (PRO == MEDNEXT_PW_PROLOGUE_GELU) {
+        v = gelu_vec(v);  // gelu(0) = 0: missing voxels stay zero
+      }
+      *reinterpret_cast<uint4*>(tile + r * kWgPitch + 8 * grp) = v;
     }
   };
 
-  uint32_t v0 = vbeg + wave * kWgStep;
-  uint4 an[4], bn[4];
-  load(v0, an, bn);
-  for (; v0 < vend; v0 += 4 * kWgStep) {
-    uint4 av[4], bv[4];
+  f32x4_t acc[TM][TK];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      av[t] = an[t];
-      bv[t] = bn[t];
+  for (int a = 0; a < TM; ++a)
+#pragma unroll
+    for (int b = 0; b < TK; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint4 regs[NLD];
+  uint32_t v = vbeg;
+  load(v, regs);
+  while (v < vend) {
+    stash(regs);
+    __syncthreads();
+    load(v + kWgStage, regs);  // next stage in flight during the MFMAs
+    uint4 bf[TK];
+#pragma unroll
+    for (int b = 0; b < TK; ++b)
+      bf[b] = *reinterpret_cast<const uint4*>(tile + (RM + 16 * b + c) * kWgPitch + 32 * wave + 8 * q);
+#pragma unroll
+    for (int a = 0; a < TM; ++a) {
+      const uint4 af = *reinterpret_cast<const uint4*>(tile + (16 * a + c) * kWgPitch + 32 * wave + 8 * q);
+#pragma unroll
+      for (int b = 0; b < TK; ++b) acc[a][b] = mfma16x16x32(af, bf[b], acc[a][b]);
     }
-    if (v0 + 4 * kWgStep < vend) load(v0 + 4 * kWgStep, an, bn);
-    if (PRO == MEDNEXT_PW_PROLOGUE_GELU) {
-      // gelu(0) = 0, so out-of-range (zero) voxels stay zero.
-#pragma unroll
-      for (int t = 0; t < 4; ++t) bv[t] = gelu_vec(bv[t]);
-    }
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int b = 0; b < 4; ++b) acc[a][b] = mfma16x16x32(av[a], bv[b], acc[a][b]);
-    if (do_bias) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint4 v = av[t];
-        dbs[t] += (bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y)) + (bf16_lo(v.z) + bf16_hi(v.z)) +
-                  (bf16_lo(v.w) + bf16_hi(v.w));
-      }
-    }
+    __syncthreads();
+    v += kWgStage;
   }
 
   // The four waves' tiles are summed into one LDS tile in wave order (every
   // lane owns the same elements in each wave, so turns only need barriers).
-  float dbw[4];
-  if (do_bias) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      float s = dbs[t];
-      s += __shfl_xor(s, 16);
-      s += __shfl_xor(s, 32);
-      dbw[t] = s;
-    }
-  }
   for (int turn = 0; turn < 4; ++turn) {
     if (wave == turn) {
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+      for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int b = 0; b < TK; ++b)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            float& e = red[(16 * a + 4 * q + r) * kWgTile + 16 * b + c];
+            float& e = red[(16 * a + 4 * q + r) * RK + 16 * b + c];
             e = turn == 0 ? acc[a][b][r] : e + acc[a][b][r];
           }
-      if (do_bias && q == 0) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          float& e = red[kWgTile * kWgTile + 16 * t + c];
-          e = turn == 0 ? dbw[t] : e + dbw[t];
-        }
-      }
     }
     __syncthreads();
   }
-  float* out = partial + (n * gridDim.x + blockIdx.x) * g.stride;
-  for (int e = threadIdx.x; e < kWgTile * kWgTile; e += kPwThreads) {
-    const int m = m0 + e / kWgTile, k = k0 + e % kWgTile;
+  if (do_bias) {
+    // Row sums: the 16 threads of a row are 16 consecutive lanes of one wave.
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+      float sum = dbs[u];
+      sum += __shfl_xor(sum, 1);
+      sum += __shfl_xor(sum, 2);
+      sum += __shfl_xor(sum, 4);
+      sum += __shfl_xor(sum, 8);
+      const int r = (threadIdx.x >> 4) + 16 * u;
+      if (grp == 0 && r < RM) red[RM * RK + r] = sum;
+    }
+    __syncthreads();
+  }
+  float* out = partial + (n * g.splits + split) * g.stride;
+  for (int e = threadIdx.x; e < RM * RK; e += kPwThreads) {
+    const int m = m0 + e / RK, k = k0 + e % RK;
     if (m < g.M && k < g.K) out[static_cast<int64_t>(m) * g.K + k] = red[e];
   }
-  if (do_bias && threadIdx.x < kWgTile) {
+  if (do_bias && threadIdx.x < RM) {
     const int m = m0 + threadIdx.x;
-    if (m < g.M) out[static_cast<int64_t>(g.M) * g.K + m] = red[kWgTile * kWgTile + threadIdx.x];
+    if (m < g.M) out[static_cast<int64_t>(g.M) * g.K + m] = red[RM * RK + threadIdx.x];
   }
 }
 
-// dW / dB = fixed-order fp64 sum of the per-split partials. A block reduces
-// kFinOut outputs; its kFinGroups thread groups each sum every kFinGroups-th
-// slot, and the group sums are added in group order.
-constexpr int kFinOut = 32;
-constexpr int kFinGroups = 8;
+// dW / dB = fixed-order fp64 sum of the per-split partials, in two passes so
+// the reduction spreads over the whole GPU. Pass 1: block (eb, r) sums slot
+// range r (slots r, r + kFinRanges, ...) for 64 consecutive outputs; its four
+// thread groups take every fourth slot of the range and are added in group
+// order. Pass 2 adds the kFinRanges range sums of each output in order and
+// rounds to bf16. Partials are [slot][M * K + M] (row-contiguous, so a wave
+// reads 256 bytes per slot).
+constexpr int kFinOut = 64;
+constexpr int kFinGroups = 4;
+constexpr int kFinRanges = 32;
 
-__global__ __launch_bounds__(kFinOut* kFinGroups) void pw_wgrad_finish_kernel(
-    const float* __restrict__ partial, bf16_t* __restrict__ dw, bf16_t* __restrict__ db, int64_t mk, int64_t m,
-    int64_t slots, int64_t stride) {
+__global__ __launch_bounds__(kFinOut* kFinGroups) void pw_wgrad_sum_kernel(const float* __restrict__ partial,
+                                                                           double* __restrict__ sums, int64_t total,
+                                                                           int64_t slots, int64_t stride) {
   __shared__ double part[kFinGroups][kFinOut];
   const int lo = threadIdx.x % kFinOut, grp = threadIdx.x / kFinOut;
   const int64_t e = blockIdx.x * static_cast<int64_t>(kFinOut) + lo;
-  const bool live = e < mk + m && (e < mk || db != nullptr);
+  const int64_t r = blockIdx.y;
   double s = 0.0;
-  if (live) {
-    for (int64_t t = grp; t < slots; t += kFinGroups) s += partial[t * stride + e];
+  if (e < total) {
+    for (int64_t t = r + kFinRanges * grp; t < slots; t += kFinRanges * kFinGroups) s += partial[t * stride + e];
   }
   part[grp][lo] = s;
   __syncthreads();
-  if (grp == 0 && live) {
-    double total = 0.0;
+  if (grp == 0 && e < total) {
+    double acc = 0.0;
 #pragma unroll
-    for (int g = 0; g < kFinGroups; ++g) total += part[g][lo];
-    const uint16_t v = f32_to_bf16(static_cast<float>(total));
-    if (e < mk) {
-      dw[e].bits = v;
-    } else {
-      db[e - mk].bits = v;
-    }
+    for (int gi = 0; gi < kFinGroups; ++gi) acc += part[gi][lo];
+    sums[r * total + e] = acc;
   }
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+__global__ __launch_bounds__(256) void pw_wgrad_finish_kernel(const double* __restrict__ sums,
+                                                              bf16_t* __restrict__ dw, bf16_t* __restrict__ db,
+                                                              int64_t mk, int64_t m) {
+  const int64_t e = blockIdx.x * static_cast<int64_t>(256) + threadIdx.x;
+  const int64_t total = mk + m;
+  if (e >= total || (e >= mk && db == nullptr)) return;
+  double acc = 0.0;
+#pragma unroll 4
+  for (int r = 0; r < kFinRanges; ++r) acc += sums[r * total + e];
+  const uint16_t v = f32_to_bf16(static_cast<float>(acc));
+  if (e < mk) {
+    dw[e].bits = v;
+  } else {
+    db[e - mk].bits = v;
+  }
+}
+
+bool aligned(const void* p, uintptr_t bytes) { return (reinterpret_cast<uintptr_t>(p) & (bytes - 1)) == 0; }
 
 int check_pw_shape(int64_t n, int64_t k, int64_t m, int64_t v, int32_t dtype) {
   MEDNEXT_CHECK_ARG(dtype == MEDNEXT_DTYPE_BF16, "pointwise kernels take bfloat16 tensors");
   MEDNEXT_CHECK_ARG(n >= 1 && k >= 1 && m >= 1 && v >= 1, "empty pointwise problem");
-  MEDNEXT_CHECK_ARG(k % 32 == 0, "input channels must be a multiple of 32");
-  MEDNEXT_CHECK_ARG(m % 16 == 0, "output channels must be a multiple of 16");
-  MEDNEXT_CHECK_ARG(v % 8 == 0, "voxels per sample must be a multiple of 8");
   MEDNEXT_CHECK_ARG(k * v * 2 < (int64_t{1} << 31) && m * v * 2 < (int64_t{1} << 31),
                     "one sample's tensor must be < 2 GiB");
-  MEDNEXT_CHECK_ARG(n <= 65535, "batch too large");
+  MEDNEXT_CHECK_ARG(n <= (int64_t{1} << 20), "batch too large");
   return MEDNEXT_STATUS_OK;
 }
 
-template <int PRO, int EPI>
-void launch_fwd(dim3 grid, size_t lds, hipStream_t s, const bf16_t* x, const bf16_t* w, const bf16_t* b,
-                const bf16_t* aux, bf16_t* y, const PwGeom& g) {
-  hipLaunchKernelGGL((pw_fwd_kernel<PRO, EPI>), grid, dim3(kPwThreads), lds, s, x, w, b, aux, y, g);
+using FwdKernel = void (*)(const bf16_t*, const bf16_t*, const bf16_t*, const bf16_t*, bf16_t*, PwGeom);
+
+constexpr int kSplitKSlices = 8;  // K >= 256: the four waves of a workgroup split K
+
+template <int MT>
+FwdKernel splitk_instance(int pro, int epi) {
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
+    switch (epi) {
+      case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_splitk_kernel<MT, 1, 0>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_splitk_kernel<MT, 1, 1>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_splitk_kernel<MT, 1, 2>;
+      default: return pw_fwd_splitk_kernel<MT, 1, 3>;
+    }
+  }
+  switch (epi) {
+    case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_splitk_kernel<MT, 0, 0>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_splitk_kernel<MT, 0, 1>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_splitk_kernel<MT, 0, 2>;
+    default: return pw_fwd_splitk_kernel<MT, 0, 3>;
+  }
+}
+
+// Four-tile row groups are only used by epilogues without an aux tensor.
+template <int KS, int MT>
+FwdKernel fwd_instance_noaux(int pro, int epi) {
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
+    return epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU ? pw_fwd_kernel<KS, MT, 1, 1> : pw_fwd_kernel<KS, MT, 1, 0>;
+  }
+  return epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU ? pw_fwd_kernel<KS, MT, 0, 1> : pw_fwd_kernel<KS, MT, 0, 0>;
+}
+
+template <int KS, int MT>
+FwdKernel fwd_instance(int pro, int epi) {
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
+    switch (epi) {
+      case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_kernel<KS, MT, 1, 0>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_kernel<KS, MT, 1, 1>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_kernel<KS, MT, 1, 2>;
+      default: return pw_fwd_kernel<KS, MT, 1, 3>;
+    }
+  }
+  switch (epi) {
+    case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_kernel<KS, MT, 0, 0>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_kernel<KS, MT, 0, 1>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_kernel<KS, MT, 0, 2>;
+    default: return pw_fwd_kernel<KS, MT, 0, 3>;
+  }
+}
+
+// Row-group height: four m-tiles (the whole 64-row output of the K = 32
+// expansions, so X is read once) when the epilogue reads no aux tensor;
+// otherwise two (accumulators + aux registers stay within two waves
+// per SIMD), one when the weight block would not fit the LDS budget.
+int pick_mt(int64_t k, int64_t m, int epi) {
+  const int64_t ks = cdiv(k, 32);
+  const bool aux = epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epi == MEDNEXT_PW_EPILOGUE_GELU_GRAD;
+  auto fits = [&](int mt) { return static_cast<size_t>(16 * mt) * ks * 32 * 2 <= kMaxWeightLds; };
+  if (ks >= kSplitKSlices) return m > 16 && fits(2) ? 2 : 1;
+  if (!aux && ks == 1 && m > 32 && fits(4)) return 4;
+  if (m > 16 && fits(2)) return 2;
+  return 1;
+}
+
+FwdKernel pick_fwd(int64_t k, int mt, int pro, int epi) {
+  const int64_t ks = cdiv(k, 32);
+  if (ks >= kSplitKSlices) return mt == 1 ? splitk_instance<1>(pro, epi) : splitk_instance<2>(pro, epi);
+  if (mt == 4) return fwd_instance_noaux<1, 4>(pro, epi);
+  if (mt == 1) return fwd_instance<0, 1>(pro, epi);
+  switch (ks) {
+    case 1: return fwd_instance<1, 2>(pro, epi);
+    case 2: return fwd_instance<2, 2>(pro, epi);
+    case 3: return fwd_instance<3, 2>(pro, epi);
+    case 4: return fwd_instance<4, 2>(pro, epi);
+    default: return fwd_instance<0, 2>(pro, epi);
+  }
+}
+
+using WgradKernel = void (*)(const bf16_t*, const bf16_t*, float*, PwWGeom);
+
+template <int TM, int TK>
+WgradKernel wgrad_instance(int pro) {
+  return pro == MEDNEXT_PW_PROLOGUE_GELU ? pw_wgrad_kernel<TM, TK, 1> : pw_wgrad_kernel<TM, TK, 0>;
+}
+
+// 16-row/column tiles per workgroup side: up to four, fewer when the matrix is
+// narrower (so no MFMA works on rows that do not exist).
+int tiles_for(int64_t rows) { return rows <= 16 ? 1 : rows <= 32 ? 2 : 4; }
+
+WgradKernel pick_wgrad(int tm, int tk, int pro) {
+  switch (tm * 8 + tk) {
+    case 1 * 8 + 1: return wgrad_instance<1, 1>(pro);
+    case 1 * 8 + 2: return wgrad_instance<1, 2>(pro);
+    case 1 * 8 + 4: return wgrad_instance<1, 4>(pro);
+    case 2 * 8 + 1: return wgrad_instance<2, 1>(pro);
+    case 2 * 8 + 2: return wgrad_instance<2, 2>(pro);
+    case 2 * 8 + 4: return wgrad_instance<2, 4>(pro);
+    case 4 * 8 + 1: return wgrad_instance<4, 1>(pro);
+    case 4 * 8 + 2: return wgrad_instance<4, 2>(pro);
+    default: return wgrad_instance<4, 4>(pro);
+  }
 }
 
 }  // namespace
@@ -423,53 +872,64 @@ extern "C" int32_t mednext_pointwise_fwd(const void* x, const void* weight, cons
                                          int32_t dtype, int32_t blocks_per_sample, void* stream) {
   if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
   MEDNEXT_CHECK_ARG(x != nullptr && weight != nullptr && y != nullptr, "null tensor pointer");
-  MEDNEXT_CHECK_ARG(k <= kMaxK, "input channels above 512 are not supported by the matrix-core GEMM");
+  MEDNEXT_CHECK_ARG(k <= kMaxK, "input channels above 2048 are not supported by the matrix-core GEMM");
   MEDNEXT_CHECK_ARG(weight_layout == 0 || weight_layout == 1, "weight_layout must be 0 ([M][K]) or 1 ([K][M])");
   MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU, "bad prologue");
   MEDNEXT_CHECK_ARG(epilogue >= MEDNEXT_PW_EPILOGUE_BIAS && epilogue <= MEDNEXT_PW_EPILOGUE_GELU_GRAD, "bad epilogue");
   const bool needs_aux = epilogue == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epilogue == MEDNEXT_PW_EPILOGUE_GELU_GRAD;
   MEDNEXT_CHECK_ARG(!needs_aux || aux != nullptr, "this epilogue needs the aux tensor");
-  MEDNEXT_CHECK_ARG(aligned16(x) && aligned16(weight) && aligned16(y) && (aux == nullptr || aligned16(aux)),
-                    "pointwise tensors must be 16-byte aligned");
-  MEDNEXT_CHECK_ARG(blocks_per_sample >= 1, "blocks_per_sample must be >= 1");
+  MEDNEXT_CHECK_ARG(aligned(x, 2) && aligned(y, 2) && (aux == nullptr || aligned(aux, 2)) && aligned(weight, 16) &&
+                        (bias == nullptr || aligned(bias, 2)),
+                    "pointwise tensors must be bf16-aligned and the weight 16-byte aligned");
+  MEDNEXT_CHECK_ARG(blocks_per_sample >= 0, "blocks_per_sample must be >= 0 (0 = automatic)");
+  const int mt = pick_mt(k, m, epilogue);
   PwGeom g;
   g.K = static_cast<int>(k);
   g.M = static_cast<int>(m);
+  g.ks = static_cast<int>(cdiv(k, 32));
   g.V = static_cast<uint32_t>(v);
   g.chunks = static_cast<int>(cdiv(v, kChunk));
+  g.mgroups = static_cast<int>(cdiv(m, 16 * mt));
   g.wt = weight_layout;
-  const int bx = static_cast<int>(std::min<int64_t>(blocks_per_sample, cdiv(g.chunks, 4)));
-  const dim3 grid(bx, static_cast<unsigned>(cdiv(m, kPwRows)), static_cast<unsigned>(n));
-  const size_t lds = static_cast<size_t>(kPwRows) * k * 2;
-  const auto s = static_cast<hipStream_t>(stream);
-  const auto* xb = static_cast<const bf16_t*>(x);
-  const auto* wb = static_cast<const bf16_t*>(weight);
-  const auto* bb = static_cast<const bf16_t*>(bias);
-  const auto* ab = static_cast<const bf16_t*>(aux);
-  auto* yb = static_cast<bf16_t*>(y);
-  if (prologue == MEDNEXT_PW_PROLOGUE_GELU) {
-    switch (epilogue) {
-      case MEDNEXT_PW_EPILOGUE_BIAS: launch_fwd<1, 0>(grid, lds, s, xb, wb, bb, ab, yb, g); break;
-      case MEDNEXT_PW_EPILOGUE_BIAS_GELU: launch_fwd<1, 1>(grid, lds, s, xb, wb, bb, ab, yb, g); break;
-      case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: launch_fwd<1, 2>(grid, lds, s, xb, wb, bb, ab, yb, g); break;
-      default: launch_fwd<1, 3>(grid, lds, s, xb, wb, bb, ab, yb, g); break;
-    }
-  } else {
-    switch (epilogue) {
-      case MEDNEXT_PW_EPILOGUE_BIAS: launch_fwd<0, 0>(grid, lds, s, xb, wb, bb, ab, yb, g); break;
-      case MEDNEXT_PW_EPILOGUE_BIAS_GELU: launch_fwd<0, 1>(grid, lds, s, xb, wb, bb, ab, yb, g); break;
-      case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: launch_fwd<0, 2>(grid, lds, s, xb, wb, bb, ab, yb, g); break;
-      default: launch_fwd<0, 3>(grid, lds, s, xb, wb, bb, ab, yb, g); break;
-    }
-  }
+  const bool splitk = g.ks >= kSplitKSlices;
+  const int64_t groups = n * g.mgroups;
+  // Every wave (split-K: every workgroup) gets at least one chunk.
+  const int64_t most = splitk ? g.chunks : cdiv(g.chunks, 4);
+  const int64_t wanted = blocks_per_sample > 0 ? blocks_per_sample : cdiv(kResidentWgs, groups);
+  g.wgs = static_cast<int>(std::max<int64_t>(1, std::min(wanted, most)));
+  const int64_t blocks = groups * g.wgs;
+  MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
+  const size_t lds = static_cast<size_t>(16 * mt) * g.ks * 32 * 2 + 16 * mt * sizeof(float) +
+                     (splitk ? static_cast<size_t>(mt) * 8 * 4 * 64 * sizeof(float) : 0);
+  hipLaunchKernelGGL(pick_fwd(k, mt, prologue, epilogue), dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds,
+                     static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(x),
+                     static_cast<const bf16_t*>(weight), static_cast<const bf16_t*>(bias),
+                     static_cast<const bf16_t*>(aux), static_cast<bf16_t*>(y), g);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }
 
+namespace {
+
+// Voxels per split for `splits` splits: whole 128-voxel LDS stages.
+int64_t wgrad_span(int64_t v, int32_t splits) { return cdiv(cdiv(v, kWgStage), splits) * kWgStage; }
+
+}  // namespace
+
+namespace {
+
+// Bytes of per-split fp32 partials; the fp64 range sums follow, 8-byte aligned.
+size_t wgrad_partial_bytes(int64_t n, int64_t k, int64_t m, int64_t v, int32_t splits) {
+  const int64_t used = cdiv(v, wgrad_span(v, splits));
+  return static_cast<size_t>(cdiv(static_cast<int64_t>(n) * used * (m * k + m), 2) * 2) * sizeof(float);
+}
+
+}  // namespace
+
 extern "C" size_t mednext_pointwise_wgrad_workspace_bytes(int64_t n, int64_t k, int64_t m, int64_t v,
                                                           int32_t splits) {
   if (n < 1 || k < 1 || m < 1 || v < 1 || splits < 1) return 0;
-  return static_cast<size_t>(n) * splits * static_cast<size_t>(m * k + m) * sizeof(float);
+  return wgrad_partial_bytes(n, k, m, v, splits) + static_cast<size_t>(kFinRanges) * (m * k + m) * sizeof(double);
 }
 
 extern "C" int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* grad_weight,
@@ -480,36 +940,37 @@ extern "C" int32_t mednext_pointwise_wgrad(const void* grad_output, const void* 
   MEDNEXT_CHECK_ARG(grad_output != nullptr && x != nullptr && grad_weight != nullptr, "null tensor pointer");
   MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU, "bad prologue");
   MEDNEXT_CHECK_ARG(splits >= 1 && splits <= 65535, "splits must be in [1, 65535]");
-  MEDNEXT_CHECK_ARG(aligned16(grad_output) && aligned16(x), "pointwise tensors must be 16-byte aligned");
+  MEDNEXT_CHECK_ARG(aligned(grad_output, 2) && aligned(x, 2) && aligned(grad_weight, 2) &&
+                        (grad_bias == nullptr || aligned(grad_bias, 2)),
+                    "pointwise tensors must be bf16-aligned");
   const size_t need = mednext_pointwise_wgrad_workspace_bytes(n, k, m, v, splits);
   MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+  MEDNEXT_CHECK_ARG(aligned(workspace, 8), "workspace must be 8-byte aligned");
   PwWGeom g;
   g.K = static_cast<int>(k);
   g.M = static_cast<int>(m);
   g.V = static_cast<uint32_t>(v);
-  const int64_t steps = cdiv(v, kWgStep);
-  const int64_t per_split = cdiv(steps, splits);
-  g.span = static_cast<uint32_t>(per_split * kWgStep);
+  g.span = static_cast<uint32_t>(wgrad_span(v, splits));
   g.splits = static_cast<int>(cdiv(v, static_cast<int64_t>(g.span)));
-  g.kblocks = static_cast<int>(cdiv(k, kWgTile));
+  const int tm = tiles_for(m), tk = tiles_for(k);
+  g.mblocks = static_cast<int>(cdiv(m, 16 * tm));
+  g.kblocks = static_cast<int>(cdiv(k, 16 * tk));
   g.stride = m * k + m;
-  const dim3 grid(static_cast<unsigned>(g.splits), static_cast<unsigned>(cdiv(m, kWgTile) * g.kblocks),
-                  static_cast<unsigned>(n));
+  const int64_t blocks = n * g.splits * g.mblocks * static_cast<int64_t>(g.kblocks);
+  MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
   const auto s = static_cast<hipStream_t>(stream);
   auto* part = static_cast<float*>(workspace);
-  if (prologue == MEDNEXT_PW_PROLOGUE_GELU) {
-    hipLaunchKernelGGL((pw_wgrad_kernel<1>), grid, dim3(kPwThreads), 0, s, static_cast<const bf16_t*>(grad_output),
-                       static_cast<const bf16_t*>(x), part, g);
-  } else {
-    hipLaunchKernelGGL((pw_wgrad_kernel<0>), grid, dim3(kPwThreads), 0, s, static_cast<const bf16_t*>(grad_output),
-                       static_cast<const bf16_t*>(x), part, g);
-  }
+  hipLaunchKernelGGL(pick_wgrad(tm, tk, prologue), dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), 0, s,
+                     static_cast<const bf16_t*>(grad_output), static_cast<const bf16_t*>(x), part, g);
   MEDNEXT_CHECK_LAUNCH();
   const int64_t total = m * k + m;
-  hipLaunchKernelGGL(pw_wgrad_finish_kernel, dim3(static_cast<unsigned>(cdiv(total, kFinOut))),
-                     dim3(kFinOut * kFinGroups), 0, s,
-                     part, static_cast<bf16_t*>(grad_weight), static_cast<bf16_t*>(grad_bias), m * k, m,
-                     n * g.splits, g.stride);
+  auto* sums = reinterpret_cast<double*>(static_cast<unsigned char*>(workspace) +
+                                         wgrad_partial_bytes(n, k, m, v, splits));
+  hipLaunchKernelGGL(pw_wgrad_sum_kernel, dim3(static_cast<unsigned>(cdiv(total, kFinOut)), kFinRanges),
+                     dim3(kFinOut * kFinGroups), 0, s, part, sums, total, n * g.splits, g.stride);
+  MEDNEXT_CHECK_LAUNCH();
+  hipLaunchKernelGGL(pw_wgrad_finish_kernel, dim3(static_cast<unsigned>(cdiv(total, 256))), dim3(256), 0, s, sums,
+                     static_cast<bf16_t*>(grad_weight), static_cast<bf16_t*>(grad_bias), m * k, m);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }

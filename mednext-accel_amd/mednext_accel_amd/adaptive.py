@@ -237,11 +237,17 @@ class _AdaptiveModule(nn.Module):
 
 
 class AdaptivePointwise3d(_AdaptiveModule):
+    """1x1x1 stride-1 convolution wrapper (reference ops/adaptive.py:125-200).
+
+    Besides the reference's ``nn.Conv3d`` it also takes a 1x1x1 stride-1
+    ``nn.ConvTranspose3d`` (the MedNeXt output heads, whose weight is stored
+    [Cin, Cout, 1, 1, 1]); ``transposed`` records which one it holds."""
+
     _mednext_accel_backend_kind = "pointwise_gemm"
 
     def __init__(
         self,
-        conv: nn.Conv3d,
+        conv: nn.Conv3d | nn.ConvTranspose3d,
         resolver: PolicyResolver,
         model_context: ModelOptimizationContext,
         *,
@@ -252,6 +258,9 @@ class AdaptivePointwise3d(_AdaptiveModule):
         self.bias = conv.bias
         for name in ("in_channels", "out_channels", "kernel_size", "stride", "padding", "dilation", "groups"):
             setattr(self, name, getattr(conv, name))
+        self.transposed = isinstance(conv, nn.ConvTranspose3d)
+        if self.transposed:
+            self.output_padding = conv.output_padding
         self.descriptor = _conv_descriptor(conv, role=role)
         self.resolver = resolver
         self.model_context = model_context
@@ -277,7 +286,10 @@ class AdaptivePointwise3d(_AdaptiveModule):
         if decision.implementation == "hip_pointwise_gemm" and _gemm_guards(x, self.in_channels, self.out_channels):
             dt = torch.bfloat16
             bias = self.bias.to(dt) if self.bias is not None else None
-            return _hip_ops().pointwise_conv3d(x.to(dt), self.weight.to(dt), bias)
+            op = _hip_ops().pointwise_conv_transpose3d if self.transposed else _hip_ops().pointwise_conv3d
+            return op(x.to(dt), self.weight.to(dt), bias)
+        if self.transposed:
+            return F.conv_transpose3d(x, self.weight, self.bias)
         if (
             decision.implementation == "pointwise_gemm_per_sample"
             and torch.is_grad_enabled()
@@ -488,8 +500,12 @@ class AdaptiveExpansion:
 
 
 def _pointwise_eligible(module: nn.Module) -> bool:
+    """1x1x1 stride-1 Conv3d (reference ops/adaptive.py:323-332) or the same
+    geometry as a ConvTranspose3d without output padding (the output heads)."""
+    if type(module) is nn.ConvTranspose3d and module.output_padding != (0, 0, 0):
+        return False
     return (
-        type(module) is nn.Conv3d
+        type(module) in (nn.Conv3d, nn.ConvTranspose3d)
         and module.kernel_size == (1, 1, 1)
         and module.stride == (1, 1, 1)
         and module.padding == (0, 0, 0)

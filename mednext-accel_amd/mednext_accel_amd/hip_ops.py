@@ -585,6 +585,19 @@ def _(x, weight, bias):
     return x.new_empty((x.shape[0], weight.shape[0], *x.shape[2:]))
 
 
+@torch.library.custom_op("mednext_accel_amd::pointwise_conv_transpose3d", mutates_args=())
+def pointwise_conv_transpose3d(x: Tensor, weight: Tensor, bias: Tensor | None) -> Tensor:
+    """1x1x1 stride-1 ConvTranspose3d (bf16): ``Y = W^T . X + b`` with the
+    transposed conv's [Cin, Cout, 1, 1, 1] weight (the MedNeXt output heads,
+    reference models/blocks.py:185-194)."""
+    return pointwise_conv(x.contiguous(), weight, bias, transpose=True)
+
+
+@pointwise_conv_transpose3d.register_fake
+def _(x, weight, bias):
+    return x.new_empty((x.shape[0], weight.shape[1], *x.shape[2:]))
+
+
 def _setup_pointwise(ctx, inputs, output):
     x, weight, bias = inputs
     ctx.save_for_backward(x, weight)
@@ -603,6 +616,33 @@ def _pointwise_backward(ctx, grad_output):
 
 
 pointwise_conv3d.register_autograd(_pointwise_backward, setup_context=_setup_pointwise)
+
+
+def _pointwise_transpose_backward(ctx, grad_output):
+    # Y = W^T X + b with W [Cin, Cout]: dX = W dY, dW = X dY^T, dB = sum dY.
+    x, weight = ctx.saved_tensors
+    need_x, need_w, need_b = ctx.needs_input_grad
+    grad_output = grad_output.contiguous()
+    dx = pointwise_forward_grad_op(grad_output, weight) if need_x else None
+    dw = db = None
+    if need_w or (need_b and ctx.has_bias):
+        dwt, db = pointwise_weight_grad_op(grad_output, x, False)  # [Cout, Cin]
+        dw = dwt.reshape(dwt.shape[0], dwt.shape[1]).t().reshape(weight.shape)
+    return dx, dw if need_w else None, db if (need_b and ctx.has_bias) else None
+
+
+@torch.library.custom_op("mednext_accel_amd::pointwise_forward_grad", mutates_args=())
+def pointwise_forward_grad_op(grad_output: Tensor, weight: Tensor) -> Tensor:
+    """dX = W . dY of a 1x1x1 transposed conv with weight [Cin, Cout] (bf16)."""
+    return pointwise_conv(grad_output.contiguous(), weight)
+
+
+@pointwise_forward_grad_op.register_fake
+def _(grad_output, weight):
+    return grad_output.new_empty((grad_output.shape[0], weight.shape[0], *grad_output.shape[2:]))
+
+
+pointwise_conv_transpose3d.register_autograd(_pointwise_transpose_backward, setup_context=_setup_pointwise)
 
 
 @torch.library.custom_op("mednext_accel_amd::mlp_expansion", mutates_args=())

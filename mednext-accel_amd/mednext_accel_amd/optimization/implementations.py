@@ -155,8 +155,10 @@ def _hip_group_norm(descriptor, context, phase: str) -> str | None:
 
 
 def _pointwise_geometry(descriptor) -> bool:
+    """1x1x1 stride-1 convolution; ``transpose`` covers a 1x1x1 ConvTranspose3d,
+    which is the same product with the weight read transposed."""
     return (
-        descriptor.direction == "regular"
+        descriptor.direction in ("regular", "transpose")
         and descriptor.kernel_size == (1, 1, 1)
         and descriptor.stride == (1, 1, 1)
         and descriptor.padding == (0, 0, 0)
@@ -224,7 +226,7 @@ def default_implementation_registry(*, triton_available: bool | None = None) -> 
         ("hip_depthwise_stride2", ("depthwise_conv3d",), ("forward", "backward_input", "backward_weight"), "numerical", False, partial(_hip_depthwise_stride2, direction="downsample"), _DW_GUARDS),
         ("hip_depthwise_transpose2", ("depthwise_conv_transpose3d",), ("forward", "backward_input", "backward_weight"), "numerical", False, partial(_hip_depthwise_stride2, direction="transpose"), _DW_GUARDS),
         ("hip_group_norm", ("group_norm3d",), ("training",), "numerical", False, _hip_group_norm, _TENSOR_GUARDS),
-        ("hip_pointwise_gemm", ("pointwise_conv3d",), ("training",), "numerical", False, _hip_pointwise, (*_TENSOR_GUARDS, "channels_supported")),
+        ("hip_pointwise_gemm", ("pointwise_conv3d", "conv_transpose3d"), ("training",), "numerical", False, _hip_pointwise, (*_TENSOR_GUARDS, "channels_supported")),
         ("hip_fused_expansion", ("mlp_expansion3d",), ("training",), "numerical", False, _hip_expansion, (*_TENSOR_GUARDS, "channels_supported")),
         ("pointwise_gemm_per_sample", ("pointwise_conv3d",), ("training",), "numerical", False, _pointwise_gemm, _TENSOR_GUARDS),
         ("triton_depthwise_dx", ("depthwise_conv3d",), ("backward_input",), "numerical", False, _no_triton, _DW_GUARDS),

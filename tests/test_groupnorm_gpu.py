@@ -38,7 +38,8 @@ def test_golden_fp64():
 
 @pytest.mark.parametrize(
     "shape,splits",
-    [((2, 3, 5, 6, 7), None), ((1, 4, 9, 9, 9), 3), ((3, 2, 1, 1, 5), 2), ((1, 8, 16, 16, 16), 7)],
+    [((2, 3, 5, 6, 7), None), ((1, 4, 9, 9, 9), 3), ((3, 2, 1, 1, 5), 2), ((1, 8, 16, 16, 16), 7),
+     ((1, 3, 13, 15, 17), 5), ((2, 5, 7, 9, 11), 9)],
 )
 def test_fp32_against_oracle(shape, splits):
     print(f"[groupnorm fp32] shape={shape} splits={splits}", flush=True)
@@ -83,6 +84,27 @@ def test_autocast_bf16_in_fp32_out_stage0():
     assert max_rel(dx, rdx) <= BF16
     assert max_rel(dg, rdg) <= FP32_WGRAD
     assert max_rel(db, rdb) <= FP32_WGRAD
+
+
+@pytest.mark.parametrize("size,splits", [(63, None), (31, 7), (15, 2)])
+def test_autocast_bf16_odd_volumes(size, splits):
+    """Up-block volumes (2s - 1)^3: every row starts at a different alignment,
+    so the scalar head / 16-byte body / scalar tail split is exercised."""
+    print(f"[groupnorm odd] 1x6x{size}^3 splits={splits}", flush=True)
+    gen = torch.Generator().manual_seed(size)
+    x = torch.randn(1, 6, size, size, size, generator=gen).bfloat16()
+    gam, bet = torch.randn(6, generator=gen), torch.randn(6, generator=gen)
+    dy = torch.randn(1, 6, size, size, size, generator=gen)
+    y, mean, rstd = hip_ops.group_norm_forward(x.to(DEV), gam.to(DEV), bet.to(DEV), out_dtype=torch.float32,
+                                               splits=splits)
+    dx, dg, db = hip_ops.group_norm_backward(dy.to(DEV), x.to(DEV), mean, rstd, gam.to(DEV), splits=splits)
+    xn, gn, bn, dyn = (t.double().numpy() for t in (x, gam, bet, dy))
+    y_ref, _, _ = ogn.forward(xn, gn, bn)
+    dx_ref, dg_ref, db_ref = ogn.backward(dyn, xn, gn)
+    assert max_rel(y, y_ref) <= FP32_OUT
+    assert max_rel(dx, dx_ref) <= BF16
+    assert max_rel(dg, dg_ref) <= FP32_WGRAD
+    assert max_rel(db, db_ref) <= FP32_WGRAD
 
 
 def test_large_mean_is_stable():

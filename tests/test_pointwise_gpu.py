@@ -186,17 +186,101 @@ def test_opcheck_pointwise_ops():
     torch.library.opcheck(hip_ops.mlp_expansion, (x, w, b, w2, None, res))
 
 
-def test_channels_above_512_are_rejected_and_not_selected():
-    """Stages 3-4 (1024 / 2048 hidden channels) exceed the 64 x 512 LDS weight
-    block: the tile policy does not select the kernel and the C ABI refuses it."""
+def test_channels_above_2048_are_rejected_and_not_selected():
+    """The LDS weight block holds K <= 2048 reduction channels: the tile policy
+    does not select the kernel beyond that and the C ABI refuses it."""
     from mednext_accel_amd.tiles import pointwise_supported
 
-    assert not pointwise_supported(256, 1024, 16**3)
-    assert pointwise_supported(128, 512, 32**3)
-    x = torch.randn(1, 1024, 2, 2, 8, device=DEV).bfloat16()
-    w = torch.randn(256, 1024, 1, 1, 1, device=DEV).bfloat16()
-    with pytest.raises(hip_ops._hip.HipLibraryError, match="above 512"):
+    assert not pointwise_supported(4096, 512, 8**3)
+    assert pointwise_supported(2048, 512, 8**3) and pointwise_supported(1, 32, 127**3)
+    x = torch.randn(1, 4096, 1, 1, 8, device=DEV).bfloat16()
+    w = torch.randn(256, 4096, 1, 1, 1, device=DEV).bfloat16()
+    with pytest.raises(hip_ops._hip.HipLibraryError, match="above 2048"):
         hip_ops.pointwise_conv(x, w)
+
+
+# Ragged and odd shapes: K not a multiple of 32 (stem K = 1, head dgrad K = 3),
+# M not a multiple of 16 (head M = 3), V not a multiple of 8 (the up blocks'
+# (2s-1)^3 volumes), large K (stage 3-4 and the bottleneck), and single-
+# workgroup launches whose waves loop over many chunks (odd chunk counts, so
+# the next-chunk prefetch and the odd-KS buffer alternation both run).
+ODD = [
+    # (n, cin, cout, spatial, blocks)
+    (1, 1, 32, (5, 7, 9), None),
+    (1, 32, 3, (5, 7, 9), None),
+    (2, 3, 32, (3, 3, 3), None),
+    (1, 40, 24, (2, 3, 41), None),
+    (1, 32, 64, (3, 5, 347), 1),  # KS = 1, MT = 4, 41 chunks over 4 waves
+    (1, 64, 32, (3, 5, 347), 1),  # KS = 2
+    (1, 96, 64, (7, 9, 83), 1),  # KS = 3
+    (2, 128, 48, (2, 9, 131), 1),  # KS = 4, partial row group
+    (1, 160, 32, (1, 11, 107), 1),  # KS = 5: runtime slice loop, odd count
+    (1, 1024, 256, (4, 4, 4), None),  # split-K: the four waves share each chunk
+    (1, 2048, 64, (3, 3, 3), None),  # K = 2048: 16-row groups
+    (1, 288, 32, (3, 5, 43), 1),  # split-K, 9 slices over 4 waves, 6 chunks in one workgroup
+    (2, 256, 48, (2, 3, 130), 1),  # split-K, partial row group, ragged V
+]
+
+
+@pytest.mark.parametrize("n,cin,cout,spatial,blocks", ODD)
+@pytest.mark.parametrize("epilogue", ["bias", "bias_residual", "gelu_grad"])
+def test_odd_shapes_forward_against_oracle(n, cin, cout, spatial, blocks, epilogue):
+    print(f"[pw odd] n={n} cin={cin} cout={cout} spatial={spatial} blocks={blocks} epi={epilogue}", flush=True)
+    gen = torch.Generator().manual_seed(cin * 13 + cout + 7 * spatial[-1])
+    x = bf((n, cin, *spatial), gen)
+    w = bf((cout, cin, 1, 1, 1), gen, cin**-0.5)
+    b = bf((cout,), gen)
+    aux = bf((n, cout, *spatial), gen, 1.5)
+    code = {"bias": PW_EPILOGUE_BIAS, "bias_residual": PW_EPILOGUE_BIAS_RESIDUAL, "gelu_grad": PW_EPILOGUE_GELU_GRAD}
+    pro = PW_PROLOGUE_GELU if epilogue == "bias_residual" else PW_PROLOGUE_NONE
+    y = hip_ops.pointwise_conv(
+        x.to(DEV), w.to(DEV), None if epilogue == "gelu_grad" else b.to(DEV),
+        aux=None if epilogue == "bias" else aux.to(DEV), prologue=pro, epilogue=code[epilogue], blocks=blocks,
+    )
+    xin = opw.gelu(f64(x)) if pro == PW_PROLOGUE_GELU else f64(x)
+    if epilogue == "gelu_grad":
+        expect = opw.conv1x1(xin, f64(w)) * opw.gelu_grad(f64(aux))
+    else:
+        expect = opw.conv1x1(xin, f64(w), f64(b))
+        if epilogue == "bias_residual":
+            expect = expect + f64(aux)
+    assert y.shape == (n, cout, *spatial)
+    assert max_rel(y, expect) <= BF16
+
+
+@pytest.mark.parametrize("n,cin,cout,spatial,blocks", ODD)
+def test_odd_shapes_transposed_and_weight_grad(n, cin, cout, spatial, blocks):
+    gen = torch.Generator().manual_seed(cin + 17 * cout)
+    x = bf((n, cin, *spatial), gen)
+    dy = bf((n, cout, *spatial), gen)
+    w = bf((cout, cin, 1, 1, 1), gen, cin**-0.5)
+    want_dx, want_dw, want_db = opw.conv1x1_backward(f64(dy), f64(x), f64(w))
+    if cout <= 2048:
+        dx = hip_ops.pointwise_conv(dy.to(DEV), w.to(DEV), transpose=True, blocks=blocks)
+        assert max_rel(dx, want_dx) <= BF16
+    splits = 1 if blocks == 1 else None
+    dw, db = hip_ops.pointwise_weight_grad(dy.to(DEV), x.to(DEV), splits=splits)
+    assert max_rel(dw, want_dw) <= BF16 and max_rel(db, want_db) <= BF16
+
+
+def test_transposed_conv_op_matches_native_fp32():
+    """The output-head route: 1x1x1 ConvTranspose3d (weight [Cin, Cout]) against
+    PyTorch in fp32, forward and all three gradients, V = 9^3 (odd)."""
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    x = torch.randn(1, 32, 9, 9, 9, device=DEV, generator=gen).bfloat16().requires_grad_()
+    w = (torch.randn(32, 3, 1, 1, 1, device=DEV, generator=gen) / 6).bfloat16().requires_grad_()
+    b = torch.randn(3, device=DEV, generator=gen).bfloat16().requires_grad_()
+    y = hip_ops.pointwise_conv_transpose3d(x, w, b)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    xr, wr, br = (t.detach().float().requires_grad_() for t in (x, w, b))
+    yr = F.conv_transpose3d(xr, wr, br)
+    yr.backward(dy.float())
+    assert max_rel(y, yr.detach().double().cpu().numpy()) <= BF16
+    for got, want in ((x.grad, xr.grad), (w.grad, wr.grad), (b.grad, br.grad)):
+        assert got.shape == want.shape
+        assert max_rel(got, want.double().cpu().numpy()) <= BF16
+    torch.library.opcheck(hip_ops.pointwise_conv_transpose3d, (x.detach().requires_grad_(), w, b))
 
 
 def test_pointwise_argument_errors():
@@ -208,10 +292,5 @@ def test_pointwise_argument_errors():
         hip_ops.pointwise_conv(x, torch.randn(64, 16, 1, 1, 1, device=DEV).bfloat16())  # channel mismatch
     with pytest.raises(ValueError):
         hip_ops.pointwise_conv(x.transpose(3, 4), w)  # non-contiguous
-    with pytest.raises(hip_ops._hip.HipLibraryError):
-        hip_ops.pointwise_conv(torch.randn(1, 16, 2, 2, 8, device=DEV).bfloat16(),
-                               torch.randn(64, 16, 1, 1, 1, device=DEV).bfloat16())  # K % 32
-    with pytest.raises(hip_ops._hip.HipLibraryError):
-        hip_ops.pointwise_conv(torch.randn(1, 32, 1, 1, 7, device=DEV).bfloat16(), w)  # V % 8
     with pytest.raises(hip_ops._hip.HipLibraryError):
         hip_ops.pointwise_conv(x, w, aux=None, epilogue=PW_EPILOGUE_BIAS_RESIDUAL)  # missing aux
