@@ -5,9 +5,10 @@ Headline (BASELINE.json metric "depthwise Conv3d fwd+bwd GB/s (% of HBM
 peak)"): one step = depthwise Conv3d forward + input-grad + weight-grad (with
 the fused bias grad) at the configs[1] headline shape, N=1 C=32 D=H=W=128, k=3,
 bf16 in / fp32 accumulate. ``value`` = algorithmic bytes of the three phases
-(12 * E bytes: two bf16 streams per phase) / their summed HIP-event time, with
-inputs resident in HBM and rotated over three input sets (>256 MiB Infinity
-Cache) so repeated timing cannot hit in MALL.
+(12 * E bytes: two bf16 streams per phase) / the sum of their per-launch
+times. Each phase is timed on its own (as configs[1] asks) over K back-to-back
+launches between two HIP events, inputs resident in HBM and rotated over three
+input sets (>256 MiB Infinity Cache) so repeated timing cannot hit in MALL.
 
 Also reported: per-phase microseconds, the roofline of the dominant kernel
 (with HBM traffic from the committed rocprofv3 --pmc summary when present),
@@ -115,48 +116,38 @@ def time_depthwise(args, torch, hip_ops, lead: GpuLead):
         del src, dst
     torch.cuda.synchronize()
 
-    def step(i: int, events=None):
-        x, dy = sets[i % len(sets)]
-        if events:
-            events[0].record()
-        y = hip_ops.depthwise_forward(x, w, b)
-        if events:
-            events[1].record()
-        dx = hip_ops.depthwise_input_grad(dy, w)
-        if events:
-            events[2].record()
-        dw, db = hip_ops.depthwise_weight_grad(x, dy, k)
-        if events:
-            events[3].record()
-        return y, dx, dw, db
-
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    all_events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    # The GPU spins ~30 ms first, so the host has enqueued the timed steps
-    # before the first of them starts and the phase events bracket kernel time.
-    lead(30.0)
-    wall0 = time.perf_counter()
-    for i, ev in enumerate(all_events):
-        step(i, ev)
-    enqueue = time.perf_counter() - wall0
-    torch.cuda.synchronize()
-    phase_ms = {
-        "forward": [ev[0].elapsed_time(ev[1]) for ev in all_events],
-        "input_grad": [ev[1].elapsed_time(ev[2]) for ev in all_events],
-        "weight_grad": [ev[2].elapsed_time(ev[3]) for ev in all_events],
+    phases = {
+        "forward": lambda i: hip_ops.depthwise_forward(sets[i % 3][0], w, b),
+        "input_grad": lambda i: hip_ops.depthwise_input_grad(sets[i % 3][1], w),
+        "weight_grad": lambda i: hip_ops.depthwise_weight_grad(sets[i % 3][0], sets[i % 3][1], k),
     }
-    mean_ms = {name: statistics.fmean(v) for name, v in phase_ms.items()}
-    median_us = {name: 1000.0 * statistics.median(v) for name, v in phase_ms.items()}
+    for i in range(args.warmup):
+        for fn in phases.values():
+            fn(i)
+    torch.cuda.synchronize()
+    # Each phase: `steps` back-to-back launches (inputs rotated over the three
+    # sets) between two events, after a ~20 ms GPU spin so the host has
+    # enqueued them all before the first starts: the mean per launch is the
+    # kernels' own time (plus the inter-launch gap).
+    mean_ms = {}
+    enqueue = 0.0
+    for name, fn in phases.items():
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        lead(20.0)
+        t0 = time.perf_counter()
+        start.record()
+        for i in range(args.steps):
+            fn(i)
+        end.record()
+        enqueue += time.perf_counter() - t0
+        torch.cuda.synchronize()
+        mean_ms[name] = start.elapsed_time(end) / args.steps
     step_ms = sum(mean_ms.values())
     bytes_per_phase = 2 * elements * 2  # two bf16 streams of E elements
     return {
         "elements": elements,
         "bytes_per_phase": bytes_per_phase,
         "mean_ms": mean_ms,
-        "median_us": median_us,
         "step_ms": step_ms,
         "host_enqueue_ms_per_step": 1000.0 * enqueue / max(1, args.steps),
         "gbs": 3 * bytes_per_phase / (step_ms * 1e-3) / 1e9,
@@ -486,7 +477,6 @@ def main() -> int:
             ),
             "hbm_frac_of_peak": round(dw["gbs"] / HBM_PEAK_GBS, 4),
             "phase_us": phase_us,
-            "phase_median_us": {k: round(v, 2) for k, v in dw["median_us"].items()},
             "host_enqueue_ms_per_step": round(dw["host_enqueue_ms_per_step"], 4),
             "copy_ceiling": ceiling,
         },

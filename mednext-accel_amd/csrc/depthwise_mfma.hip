@@ -560,7 +560,7 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
 template <int K, bool FLIP>
 int launch_stencil_ct(const void* x, const void* wt, const void* bias, void* y, const MGeom& g,
                       int tile_cols, int64_t blocks, hipStream_t st) {
-  constexpr int PD = K == 3 ? 3 : 2;
+  constexpr int PD = K == 3 ? 4 : 2;
   switch (tile_cols) {
     case 32: return launch_stencil<K, FLIP, 2, PD>(x, wt, bias, y, g, blocks, st);
     case 64: return launch_stencil<K, FLIP, 4, PD>(x, wt, bias, y, g, blocks, st);

@@ -701,10 +701,11 @@ __global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_ke
 
 // dW / dB = fixed-order fp64 sum of the per-split partials, in two passes so
 // the reduction spreads over the whole GPU. Pass 1: block (eb, r) sums slot
-// range r (slots r, r + kFinRanges, ...) for 64 consecutive outputs; its four
+// range r of R (slots r, r + R, ...) for 64 consecutive outputs; its four
 // thread groups take every fourth slot of the range and are added in group
-// order. Pass 2 adds the kFinRanges range sums of each output in order and
-// rounds to bf16. Partials are [slot][M * K + M] (row-contiguous, so a wave
+// order. Pass 2 adds the R range sums of each output in order and rounds to
+// bf16. R (at most kFinRanges) gives each range about 16 slots, so small slot
+// counts do not launch empty ranges. Partials are [slot][M * K + M] (row-contiguous, so a wave
 // reads 256 bytes per slot).
 constexpr int kFinOut = 64;
 constexpr int kFinGroups = 4;
@@ -716,10 +717,10 @@ __global__ __launch_bounds__(kFinOut* kFinGroups) void pw_wgrad_sum_kernel(const
   __shared__ double part[kFinGroups][kFinOut];
   const int lo = threadIdx.x % kFinOut, grp = threadIdx.x / kFinOut;
   const int64_t e = blockIdx.x * static_cast<int64_t>(kFinOut) + lo;
-  const int64_t r = blockIdx.y;
+  const int64_t r = blockIdx.y, nr = gridDim.y;
   double s = 0.0;
   if (e < total) {
-    for (int64_t t = r + kFinRanges * grp; t < slots; t += kFinRanges * kFinGroups) s += partial[t * stride + e];
+    for (int64_t t = r + nr * grp; t < slots; t += nr * kFinGroups) s += partial[t * stride + e];
   }
   part[grp][lo] = s;
   __syncthreads();
@@ -733,13 +734,12 @@ __global__ __launch_bounds__(kFinOut* kFinGroups) void pw_wgrad_sum_kernel(const
 
 __global__ __launch_bounds__(256) void pw_wgrad_finish_kernel(const double* __restrict__ sums,
                                                               bf16_t* __restrict__ dw, bf16_t* __restrict__ db,
-                                                              int64_t mk, int64_t m) {
+                                                              int64_t mk, int64_t m, int ranges) {
   const int64_t e = blockIdx.x * static_cast<int64_t>(256) + threadIdx.x;
   const int64_t total = mk + m;
   if (e >= total || (e >= mk && db == nullptr)) return;
   double acc = 0.0;
-#pragma unroll 4
-  for (int r = 0; r < kFinRanges; ++r) acc += sums[r * total + e];
+  for (int r = 0; r < ranges; ++r) acc += sums[r * total + e];
   const uint16_t v = f32_to_bf16(static_cast<float>(acc));
   if (e < mk) {
     dw[e].bits = v;
@@ -966,11 +966,13 @@ extern "C" int32_t mednext_pointwise_wgrad(const void* grad_output, const void* 
   const int64_t total = m * k + m;
   auto* sums = reinterpret_cast<double*>(static_cast<unsigned char*>(workspace) +
                                          wgrad_partial_bytes(n, k, m, v, splits));
-  hipLaunchKernelGGL(pw_wgrad_sum_kernel, dim3(static_cast<unsigned>(cdiv(total, kFinOut)), kFinRanges),
-                     dim3(kFinOut * kFinGroups), 0, s, part, sums, total, n * g.splits, g.stride);
+  const int64_t slots = n * g.splits;
+  const int ranges = static_cast<int>(std::min<int64_t>(kFinRanges, cdiv(slots, 16)));
+  hipLaunchKernelGGL(pw_wgrad_sum_kernel, dim3(static_cast<unsigned>(cdiv(total, kFinOut)), ranges),
+                     dim3(kFinOut * kFinGroups), 0, s, part, sums, total, slots, g.stride);
   MEDNEXT_CHECK_LAUNCH();
   hipLaunchKernelGGL(pw_wgrad_finish_kernel, dim3(static_cast<unsigned>(cdiv(total, 256))), dim3(256), 0, s, sums,
-                     static_cast<bf16_t*>(grad_weight), static_cast<bf16_t*>(grad_bias), m * k, m);
+                     static_cast<bf16_t*>(grad_weight), static_cast<bf16_t*>(grad_bias), m * k, m, ranges);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }
