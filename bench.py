@@ -52,6 +52,10 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--train-warmup", type=int, default=20)
     ap.add_argument("--train-size", type=int, default=128)
     ap.add_argument("--no-eager-step", action="store_true", help="time only the HIP-backed training step")
+    ap.add_argument("--no-large-step", action="store_true",
+                    help="skip the MedNeXt-Large k5 checkpointed training step (configs[4])")
+    ap.add_argument("--large-steps", type=int, default=10)
+    ap.add_argument("--large-warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
     ap.add_argument("--train-only", action="store_true", help="time only the MedNeXt-Base training step(s)")
     ap.add_argument(
@@ -186,24 +190,34 @@ def time_copy_ceiling(torch) -> dict:
             "gbs": round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)}
 
 
-def time_train_step(args, torch, optimization: str) -> dict:
-    """MedNeXt-Base (1 in, 3 classes, k3, deep supervision) training step at
-    1x1xS^3 in bf16 autocast with AdamW, the reference's step protocol
-    (benchmarks/implementations.py:133-190): event median over the timed steps."""
-    from mednext_accel_amd import mednext_base
+def time_train_step(args, torch, optimization: str, variant: str = "base", steps: int | None = None,
+                    warmup: int | None = None) -> dict:
+    """MedNeXt training step at 1x1xS^3 in bf16 autocast with AdamW, the
+    reference's step protocol (benchmarks/implementations.py:133-190): event
+    median over the timed steps. ``base``: MedNeXt-Base k3, no checkpointing
+    (configs[3]); ``large``: MedNeXt-Large k5 with expansion-branch
+    checkpointing on all stages."""
+    from mednext_accel_amd import CheckpointConfig, mednext_base, mednext_large
     from mednext_accel_amd.step import make_training_step
 
+    steps = args.train_steps if steps is None else steps
+    warmup = args.train_warmup if warmup is None else warmup
     torch.manual_seed(1234)
-    model = mednext_base(in_channels=1, out_channels=3, kernel_size=3, deep_supervision=True, optimization=optimization)
+    if variant == "large":
+        model = mednext_large(in_channels=1, out_channels=3, kernel_size=5, deep_supervision=True,
+                              checkpointing=CheckpointConfig(style="expansion", stages=None), optimization=optimization)
+    else:
+        model = mednext_base(in_channels=1, out_channels=3, kernel_size=3, deep_supervision=True,
+                             optimization=optimization)
     model = model.cuda().train()
     step = make_training_step(model, size=args.train_size, device="cuda")
-    for _ in range(args.train_warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     events = []
     wall0 = time.perf_counter()
-    for _ in range(args.train_steps):
+    for _ in range(steps):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         step()
@@ -214,7 +228,7 @@ def time_train_step(args, torch, optimization: str) -> dict:
     times = [a.elapsed_time(b) for a, b in events]
     result = {
         "median_step_ms": round(statistics.median(times), 3),
-        "mean_wall_step_ms": round(1000.0 * wall / max(1, args.train_steps), 3),
+        "mean_wall_step_ms": round(1000.0 * wall / max(1, steps), 3),
         "peak_allocated_mib": round(torch.cuda.max_memory_allocated() / 2**20, 1),
         "final_loss": round(float(step.last_loss.detach()), 5),
     }
@@ -432,7 +446,11 @@ def main() -> int:
         sweep(args, torch, hip_ops, lead)
         return 0
     if args.train_only:
-        print(json.dumps({"train_step_hip": time_train_step(args, torch, "auto")}))
+        out = {"train_step_hip": time_train_step(args, torch, "auto")}
+        if not args.no_large_step:
+            out["train_step_large_hip"] = time_train_step(args, torch, "auto", "large", args.large_steps,
+                                                          args.large_warmup)
+        print(json.dumps(out))
         return 0
     dw = time_depthwise(args, torch, hip_ops, lead)
     ceiling = time_copy_ceiling(torch)
@@ -496,6 +514,20 @@ def main() -> int:
             "reference_eager": eager,
             "speedup_vs_reference_eager": round(eager["median_step_ms"] / ours["median_step_ms"], 3) if eager else None,
         }
+        if not args.no_large_step:
+            big = time_train_step(args, torch, "auto", "large", args.large_steps, args.large_warmup)
+            big_eager = None if args.no_eager_step else time_train_step(
+                args, torch, "reference", "large", max(3, args.large_steps // 2), 2)
+            result["train_step_large"] = {
+                "model": (
+                    f"MedNeXt-Large k5, 1x1x{args.train_size}^3, 5-head deep supervision, expansion-branch "
+                    "checkpointing on all stages, bf16 autocast, AdamW lr 1e-3 (BASELINE configs[4])"
+                ),
+                "hip": big,
+                "reference_eager": big_eager,
+                "speedup_vs_reference_eager": round(big_eager["median_step_ms"] / big["median_step_ms"], 3)
+                if big_eager else None,
+            }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, torch)
     print(json.dumps(result))

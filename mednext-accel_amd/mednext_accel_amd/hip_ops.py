@@ -522,6 +522,8 @@ def _setup_group_norm(ctx, inputs, output):
     x, weight, bias, _eps, _out_dtype = inputs
     _y, mean, rstd = output
     ctx.mark_non_differentiable(mean, rstd)
+    # mean / rstd never receive gradients: do not let autograd build zero tensors for them.
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(x, mean, rstd, weight)
     ctx.param_dtype = (weight if weight is not None else bias).dtype if (weight is not None or bias is not None) else torch.float32
     ctx.has_weight = weight is not None
@@ -529,6 +531,8 @@ def _setup_group_norm(ctx, inputs, output):
 
 
 def _group_norm_backward(ctx, grad_y, _grad_mean, _grad_rstd):
+    if grad_y is None:
+        return None, None, None, None, None
     x, mean, rstd, weight = ctx.saved_tensors
     dx, dgamma, dbeta = group_norm_channels_backward(
         grad_y, x, mean, rstd, weight if ctx.has_weight else None, ctx.param_dtype
@@ -701,11 +705,16 @@ def _setup_mlp(ctx, inputs, output):
     x, w1, b1, w2, b2, residual = inputs
     _out, h = output
     ctx.mark_non_differentiable(h)
+    # h (kept for the backward) never receives a gradient: without this autograd
+    # would fill a zero tensor the size of the expanded activation every step.
+    ctx.set_materialize_grads(False)
     ctx.save_for_backward(x, h, w1, w2)
     ctx.has_b1, ctx.has_b2, ctx.has_residual = b1 is not None, b2 is not None, residual is not None
 
 
 def _mlp_backward(ctx, grad_out, _grad_h):
+    if grad_out is None:
+        return None, None, None, None, None, None
     x, h, w1, w2 = ctx.saved_tensors
     dx, dw1, db1, dw2, db2 = mlp_expansion_backward(grad_out, x, h, w1, w2)
     return (

@@ -245,6 +245,37 @@ def test_base_training_step_128_bf16_matches_reference():
     torch.cuda.empty_cache()
 
 
+def test_large_k5_checkpointed_step_matches_reference():
+    """MedNeXt-Large k5 with expansion checkpointing on all stages (BASELINE
+    configs[4]) at 64^3: one bf16 AdamW step through the HIP ops (k5 depthwise,
+    fused expansions recomputed in backward) gives the reference model's loss
+    within the bf16 tolerance and the same gradient norms."""
+    print("[model step] large k5 ckpt 64^3 bf16", flush=True)
+    from mednext_accel_amd import mednext_large
+
+    torch.manual_seed(4321)
+    ckpt = CheckpointConfig(style="expansion", stages=None)
+    ref = mednext_large(in_channels=1, out_channels=3, kernel_size=5, deep_supervision=True, checkpointing=ckpt,
+                        optimization="reference").to(DEV).train()
+    cand = mednext_large(in_channels=1, out_channels=3, kernel_size=5, deep_supervision=True,
+                         checkpointing=ckpt).to(DEV).train()
+    cand.load_state_dict(ref.state_dict())
+    losses, norms = [], []
+    for model in (cand, ref):
+        step = make_training_step(model, size=64, device=DEV)
+        with Observe() as seen:
+            loss = step()
+        losses.append(float(loss.detach()))
+        norms.append(torch.stack([p.grad.float().norm() for p in model.parameters()]))
+        if model is cand:
+            assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops and MLP_OP in seen.ops
+        del step
+    assert abs(losses[0] - losses[1]) / abs(losses[1]) < BF16
+    assert torch.isfinite(norms[0]).all()
+    assert float(((norms[0] - norms[1]).norm() / norms[1].norm())) < 5e-2
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("style", ["expansion", "block"])
 def test_checkpointed_model_runs_hip_ops(style):
     """Activation checkpointing recomputes through the HIP ops: bf16 autocast
