@@ -14,7 +14,10 @@ from .policy_io import PolicySource, load_policy
 from .policy_resolver import PolicyResolver
 
 POLICY_DIR = Path(__file__).resolve().parent.parent / "policies"
-BUNDLED = ("gfx950",)
+# Layer order: the measured exact-context gfx950 policy (MedNeXt-Base 128^3,
+# written by mednext_accel_amd.profiling) before the formula-driven gfx950
+# policy, which covers every other context.
+BUNDLED = ("gfx950_base128", "gfx950")
 
 
 @cache

@@ -103,7 +103,12 @@ def test_per_sample_gemm_matches_convolution(batch, bias):
 @pytest.mark.parametrize("k", [3, 5])
 @pytest.mark.parametrize("channels,size", STAGES)
 def test_gfx950_policy_selects_hip_depthwise_with_tile_recipes(channels, size, k):
-    resolver = PolicyRegistry().resolver()
+    """The formula-driven gfx950 layer on its own: HIP everywhere at the stage
+    shapes, with the tile recipe of ``tiles.depthwise_recipe``."""
+    from mednext_accel_amd.optimization.policies import load_bundled_policy
+    from mednext_accel_amd.optimization.policy_resolver import PolicyResolver
+
+    resolver = PolicyResolver((load_bundled_policy("gfx950"),))
     conv = nn.Conv3d(channels, channels, k, padding=k // 2, groups=channels)
     desc = _conv_descriptor(conv, role="encoder_stages.0.0.depthwise")
     c = ctx((size,) * 3)
@@ -116,6 +121,34 @@ def test_gfx950_policy_selects_hip_depthwise_with_tile_recipes(channels, size, k
         assert d.implementation == impl and d.policy == "gfx950" and d.disposition == "custom"
         want = tiles.depthwise_recipe(1, channels, (size,) * 3, k, "bfloat16", tile_phase)
         assert [d.parameters["engine"], d.parameters["tile_w"], d.parameters["depth_chunk"]] == want
+
+
+@pytest.mark.parametrize("k", [3, 5])
+@pytest.mark.parametrize("channels,size", STAGES)
+def test_measured_policy_layer_matches_its_evidence(channels, size, k):
+    """The bundled registry resolves the MedNeXt-Base 128^3 depthwise contexts
+    through the measured exact-context layer, and each selected recipe is the
+    fastest valid candidate recorded in that layer's evidence file."""
+    import json
+
+    from mednext_accel_amd.optimization.policies import POLICY_DIR
+
+    evidence = json.loads((POLICY_DIR / "gfx950_base128_evidence.json").read_text())["measurements"]
+    resolver = PolicyRegistry().resolver()
+    conv = nn.Conv3d(channels, channels, k, padding=k // 2, groups=channels)
+    desc = _conv_descriptor(conv, role="encoder_stages.0.0.depthwise")
+    for phase in ("forward", "backward_input", "backward_weight"):
+        d = resolver.resolve(desc, ctx((size,) * 3), phase)
+        rows = [m for m in evidence if m["family"] == "depthwise_conv3d" and m["phase"] == phase
+                and m["in_channels"] == channels and m["kernel_size"] == k and m["spatial_shape"] == [size] * 3
+                and m["valid"]]
+        best = min(rows, key=lambda m: m["candidate_ms"])
+        assert d.policy == "gfx950-base-128-measured"
+        assert d.implementation == best["implementation"]
+        if best["parameters"]:
+            assert d.parameters == best["parameters"]
+        # Every HIP candidate beat native PyTorch at these shapes on MI355X.
+        assert d.disposition == "custom"
 
 
 def test_gfx950_policy_group_norm_and_pointwise():

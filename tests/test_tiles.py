@@ -31,8 +31,7 @@ def test_depthwise_recipe_invariants(channels, size, k, dtype, phase):
         wgs = plan.workgroups
         target = tiles.TARGET_WORKGROUPS
     # Fill the chip unless the minimum D-run (halo bound) forbids it.
-    floor = min(size, max(4, 2 * (k - 1)))
-    assert wgs >= target or depth_chunk == floor
+    assert wgs >= target or depth_chunk == tiles.depth_chunk_floor(size, k)
 
 
 def test_bf16_stage0_uses_matrix_cores():
