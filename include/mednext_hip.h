@@ -165,8 +165,9 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
  * accumulate): x [N][K][V], y [N][M][V] (V = D*H*W voxels), weight [M][K]
  * (weight_layout 0) or [K][M] (weight_layout 1, i.e. the transposed product
  * for the input gradient: grad_x = W^T . grad_y with W the conv's [M][K]).
- * Requirements: bf16, K % 32 == 0, K <= 512, M % 16 == 0, V % 8 == 0, one
- * sample's x and y each < 2 GiB, 16-byte aligned pointers.
+ * Requirements: bf16, 1 <= K <= 2048, any M >= 1 and V >= 1 (a row's last
+ * partial 8-voxel group uses element accesses), one sample's x and y each
+ * < 2 GiB, bf16-aligned tensors and a 16-byte aligned weight.
  * Prologue, applied to every x element as loaded:
  *   MEDNEXT_PW_PROLOGUE_GELU: x -> GELU(x) (exact erf form).
  * Epilogue, applied to each accumulator y[n][m][v] (bias may be NULL):
@@ -184,7 +185,8 @@ enum mednext_pw_epilogue {
 };
 
 /* y = epilogue(op(W) . prologue(x)); blocks_per_sample = workgroups along V
- * per (sample, 64-row output block), from the gfx950 tile policy.
+ * per (sample, output row group), 0 = the library's choice (two resident
+ * workgroups per CU over the whole grid).
  * Replaces the forward of AdaptivePointwise3d (reference
  * src/mednext_accel/ops/adaptive.py:174-200: per-sample addmm / F.conv3d) and,
  * with the epilogues, the GELU (models/blocks.py:39-41) and residual add
@@ -195,14 +197,15 @@ int32_t mednext_pointwise_fwd(const void* x, const void* weight, const void* bia
                               int32_t weight_layout, int32_t prologue, int32_t epilogue,
                               int32_t dtype, int32_t blocks_per_sample, void* stream);
 
-/* fp32 bytes of per-split partials the weight-gradient launch needs. */
+/* Bytes of workspace the weight-gradient launch needs: fp32 per-split
+ * partials followed by fp64 range sums (8-byte aligned). */
 size_t mednext_pointwise_wgrad_workspace_bytes(int64_t n, int64_t k, int64_t m, int64_t v,
                                                int32_t splits);
 
 /* grad_weight[M][K] = sum_{n,v} grad_output[n][m][v] * prologue(x[n][k][v]);
  * grad_bias[m] = sum_{n,v} grad_output[n][m][v] (skipped when NULL). Both bf16;
  * fixed-order reduction (bit-reproducible). splits = workgroups per sample
- * along V. Replaces the weight/bias gradient of the reference's pointwise
+ * along V. Any K, M >= 1; the workspace must be 8-byte aligned. Replaces the weight/bias gradient of the reference's pointwise
  * conv (adaptive.py:174-200, autograd of addmm / conv3d). */
 int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* grad_weight,
                                 void* grad_bias, void* workspace, size_t workspace_bytes,
