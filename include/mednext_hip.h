@@ -212,6 +212,34 @@ int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* gr
                                 int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
                                 int32_t dtype, int32_t splits, void* stream);
 
+/* ------------------------------------------------------------------ GRN
+ * Global Response Normalization of MedNeXt v2 on [N, C, V]:
+ *   n_c = ||x[n, c, :]||_2, S = sum_c n_c, r_c = n_c / (S + eps),
+ *   y = x + gamma_c * x * r_c + beta_c
+ * computed in fp32 from f16/bf16/f32 input (fp64 for fp64), y in x's dtype.
+ * Replaces the reference's fused Triton GRN (reference
+ * src/mednext_accel/ops/_triton/grn.py:177-229 forward, :242-317 backward)
+ * behind the formula of ops/grn.py:16-30. gamma/beta ([C], param_dtype,
+ * nullable = 0) are the (1, C, 1, 1, 1) parameters read flat. `coef` receives
+ * [N*C][4] fp64 (1 + gamma r, beta, r, n_c) for the backward. `splits` chunks
+ * each (n, c) row across workgroups (1..4096); workspace is 8-byte aligned. */
+size_t mednext_grn_workspace_bytes(int64_t n, int64_t c, int64_t spatial, int32_t splits);
+
+int32_t mednext_grn_fwd(const void* x, int32_t x_dtype, const void* gamma, const void* beta,
+                        int32_t param_dtype, void* y, void* coef, int64_t n, int64_t c,
+                        int64_t spatial, double eps, int32_t splits, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* grad_input (x's dtype, nullable), grad_gamma / grad_beta ([C], param_dtype,
+ * nullable) from grad_output (pairs dy/x: same dtype, or f32 with bf16/f16 x),
+ * x and the forward's coef, including the cross-channel term through S and a
+ * zero subgradient where n_c == 0. Fixed-order reductions (bit-reproducible). */
+int32_t mednext_grn_bwd(const void* grad_output, int32_t dy_dtype, const void* x, int32_t x_dtype,
+                        const void* coef, const void* gamma, int32_t param_dtype,
+                        void* grad_input, void* grad_gamma, void* grad_beta, int64_t n, int64_t c,
+                        int64_t spatial, double eps, int32_t splits, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

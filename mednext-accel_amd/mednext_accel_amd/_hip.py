@@ -64,6 +64,15 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p),
     ),
+    "mednext_grn_workspace_bytes": (c_size_t, (_i64, _i64, _i64, _i32)),
+    "mednext_grn_fwd": (
+        _i32,
+        (_p, _i32, _p, _p, _i32, _p, _p, _i64, _i64, _i64, c_double, _i32, _p, c_size_t, _p),
+    ),
+    "mednext_grn_bwd": (
+        _i32,
+        (_p, _i32, _p, _i32, _p, _p, _i32, _p, _p, _p, _i64, _i64, _i64, c_double, _i32, _p, c_size_t, _p),
+    ),
     "mednext_depthwise3d_s2_gather": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
     "mednext_depthwise3d_s2_scatter": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
     "mednext_depthwise3d_s2_wgrad_workspace_bytes": (c_size_t, (*(_i64,) * 8, _i32, _i32)),

@@ -18,6 +18,7 @@ launch raises.
 from __future__ import annotations
 
 import functools
+import math
 
 import torch
 from torch import Tensor
@@ -910,3 +911,164 @@ def _t2_backward(ctx, grad_output):
 
 
 depthwise_conv_transpose3d_stride2.register_autograd(_t2_backward, setup_context=_setup_s2)
+
+
+# ------------------------------------------------------------------------ GRN
+
+
+def grn_forward(
+    x: Tensor, gamma: Tensor | None, beta: Tensor | None, eps: float = 1e-6, splits: int | None = None
+) -> tuple[Tensor, Tensor]:
+    """Global Response Normalization forward (reference ops/grn.py:16-30):
+    returns ``(y, coef)`` with ``coef`` [N, C, 4] fp64 = (1 + gamma r, beta, r, ||x_c||).
+    Accepts f16 / bf16 / f32 / f64 input; parameters are read flat ([C] values)."""
+    _check_device(x)
+    if x.ndim != 5 or not x.is_contiguous():
+        raise ValueError("a contiguous NCDHW input is required")
+    n, c = int(x.shape[0]), int(x.shape[1])
+    v = x.numel() // max(1, n * c)
+    params = [p for p in (gamma, beta) if p is not None]
+    pdtype = params[0].dtype if params else torch.float32
+    for p in params:
+        if p.numel() != c or p.dtype != pdtype or not p.is_cuda or not p.is_contiguous():
+            raise ValueError("gamma / beta must be contiguous CUDA tensors of C values and one dtype")
+    if x.numel() == 0:
+        raise ValueError("GRN requires nonempty input dimensions")
+    y = torch.empty_like(x)
+    coef = torch.empty((n, c, 4), device=x.device, dtype=torch.float64)
+    splits = group_norm_splits(n, c, v) if splits is None else int(splits)
+    lib = _hip.load()
+    nbytes = lib.mednext_grn_workspace_bytes(n, c, v, splits)
+    workspace = torch.empty((max(8, nbytes),), device=x.device, dtype=torch.uint8)
+    _hip.check(
+        lib.mednext_grn_fwd(
+            x.data_ptr(), _hip.dtype_code(x.dtype), _hip.ptr(gamma), _hip.ptr(beta), _hip.dtype_code(pdtype),
+            y.data_ptr(), coef.data_ptr(), n, c, v, float(eps), splits, workspace.data_ptr(), nbytes,
+            _hip.stream_of(x),
+        ),
+        "mednext_grn_fwd",
+    )
+    return y, coef
+
+
+def grn_backward(
+    grad_output: Tensor,
+    x: Tensor,
+    coef: Tensor,
+    gamma: Tensor | None,
+    eps: float = 1e-6,
+    need_input: bool = True,
+    need_params: bool = True,
+    param_dtype: torch.dtype = torch.float32,
+    param_shape: tuple[int, ...] | None = None,
+    splits: int | None = None,
+) -> tuple[Tensor | None, Tensor | None, Tensor | None]:
+    """GRN backward: (dx in x.dtype, dgamma, dbeta in ``param_dtype`` and ``param_shape``)."""
+    _check_device(grad_output, x, coef)
+    if grad_output.shape != x.shape or not (grad_output.is_contiguous() and x.is_contiguous()):
+        raise ValueError("grad_output and x must be contiguous with the same shape")
+    n, c = int(x.shape[0]), int(x.shape[1])
+    v = x.numel() // max(1, n * c)
+    if coef.dtype != torch.float64 or coef.numel() != n * c * 4 or not coef.is_contiguous():
+        raise ValueError("coef must be the forward's contiguous [N, C, 4] float64 tensor")
+    if gamma is not None:
+        param_dtype = gamma.dtype
+    if grad_output.dtype != x.dtype and not (
+        grad_output.dtype == torch.float32 and x.dtype in (torch.bfloat16, torch.float16)
+    ):
+        grad_output = grad_output.to(x.dtype)
+    shape = (c,) if param_shape is None else tuple(param_shape)
+    dx = torch.empty_like(x) if need_input else None
+    dgamma = torch.empty(shape, device=x.device, dtype=param_dtype) if need_params else None
+    dbeta = torch.empty(shape, device=x.device, dtype=param_dtype) if need_params else None
+    splits = group_norm_splits(n, c, v) if splits is None else int(splits)
+    lib = _hip.load()
+    nbytes = lib.mednext_grn_workspace_bytes(n, c, v, splits)
+    workspace = torch.empty((max(8, nbytes),), device=x.device, dtype=torch.uint8)
+    _hip.check(
+        lib.mednext_grn_bwd(
+            grad_output.data_ptr(), _hip.dtype_code(grad_output.dtype), x.data_ptr(), _hip.dtype_code(x.dtype),
+            coef.data_ptr(), _hip.ptr(gamma), _hip.dtype_code(param_dtype), _hip.ptr(dx), _hip.ptr(dgamma),
+            _hip.ptr(dbeta), n, c, v, float(eps), splits, workspace.data_ptr(), nbytes, _hip.stream_of(x),
+        ),
+        "mednext_grn_bwd",
+    )
+    return dx, dgamma, dbeta
+
+
+@torch.library.custom_op("mednext_accel_amd::grn_forward", mutates_args=())
+def grn_forward_op(x: Tensor, gamma: Tensor, beta: Tensor, eps: float) -> tuple[Tensor, Tensor]:
+    """Fused GRN forward (reference ops/_triton/grn.py:177-229): (y, coef)."""
+    return grn_forward(x, gamma, beta, eps)
+
+
+@grn_forward_op.register_fake
+def _(x, gamma, beta, eps):
+    return torch.empty_like(x), x.new_empty((x.shape[0], x.shape[1], 4), dtype=torch.float64)
+
+
+@torch.library.custom_op("mednext_accel_amd::grn_backward", mutates_args=())
+def grn_backward_op(
+    grad_output: Tensor, x: Tensor, gamma: Tensor, coef: Tensor, eps: float
+) -> tuple[Tensor, Tensor, Tensor]:
+    """Fused GRN backward (reference ops/_triton/grn.py:242-317): (dx, dgamma, dbeta)."""
+    dx, dgamma, dbeta = grn_backward(
+        grad_output.contiguous(), x, coef, gamma, eps, param_shape=tuple(gamma.shape)
+    )
+    return dx, dgamma, dbeta
+
+
+@grn_backward_op.register_fake
+def _(grad_output, x, gamma, coef, eps):
+    return torch.empty_like(x), torch.empty_like(gamma), torch.empty_like(gamma)
+
+
+def _setup_grn(ctx, inputs, output):
+    x, gamma, _beta, eps = inputs
+    _y, coef = output
+    ctx.mark_non_differentiable(coef)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(x, gamma, coef)
+    ctx.eps = eps
+
+
+def _grn_backward(ctx, grad_output, _grad_coef):
+    if grad_output is None:
+        return None, None, None, None
+    x, gamma, coef = ctx.saved_tensors
+    dx, dgamma, dbeta = grn_backward_op(grad_output, x, gamma, coef, ctx.eps)
+    need = ctx.needs_input_grad
+    return (dx if need[0] else None, dgamma if need[1] else None, dbeta if need[2] else None, None)
+
+
+grn_forward_op.register_autograd(_grn_backward, setup_context=_setup_grn)
+
+
+def fused_global_response_norm3d(x: Tensor, gamma: Tensor, beta: Tensor, eps: float = 1e-6) -> Tensor:
+    """Fused GRN with the reference's direct-call contract (reference
+    ops/_triton/grn.py:404-438): nonempty contiguous NCDHW f16/bf16 GPU input,
+    contiguous float32 gamma and beta of shape (1, C, 1, 1, 1) on the same
+    device, finite positive eps; anything else raises ``ValueError`` with the
+    reference's message instead of silently falling back."""
+    if x.ndim != 5:
+        raise ValueError("fused GRN expects a rank-5 NCDHW input")
+    if not (x.is_cuda and gamma.is_cuda and beta.is_cuda):
+        raise ValueError("fused GRN requires CUDA tensors")
+    if gamma.device != x.device or beta.device != x.device:
+        raise ValueError("fused GRN requires all tensors on the same CUDA device")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("fused GRN requires a float16 or bfloat16 input")
+    if not x.is_contiguous():
+        raise ValueError("fused GRN requires a contiguous NCDHW input")
+    if any(size == 0 for size in x.shape):
+        raise ValueError("fused GRN requires nonempty input dimensions")
+    if gamma.dtype != torch.float32 or beta.dtype != torch.float32:
+        raise ValueError("fused GRN requires float32 gamma and beta")
+    expected = (1, x.shape[1], 1, 1, 1)
+    if tuple(gamma.shape) != expected or tuple(beta.shape) != expected:
+        raise ValueError("fused GRN requires gamma and beta with shape (1, C, 1, 1, 1)")
+    if not gamma.is_contiguous() or not beta.is_contiguous():
+        raise ValueError("fused GRN requires contiguous gamma and beta")
+    if not math.isfinite(eps) or eps <= 0:
+        raise ValueError("fused GRN requires eps to be finite and positive")
+    return grn_forward_op(x, gamma, beta, float(eps))[0]

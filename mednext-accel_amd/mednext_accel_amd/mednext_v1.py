@@ -226,9 +226,15 @@ def checkpoint_name(config: CheckpointConfig | None) -> str:
     return f"{config.style}:{','.join(map(str, config.stages))}"
 
 
+# Resampling-block convs that read the block's input (the rest of the block
+# runs at the resampled resolution).
+_BLOCK_INPUT_CONVS = ("depthwise", "residual")
+
+
 def spatial_shape_for_role(role: str | None, input_spatial: tuple[int, ...]) -> tuple[int, ...]:
     """Spatial shape the module named ``role`` sees for a given model input
-    (halving per stride-2 step, rounding up; up-block convs see 2s-1 before padding)."""
+    (halving per stride-2 step, rounding up; up-block modules after the
+    transposed depthwise conv see 2s-1 before padding)."""
     if role is None or role == "stem" or role.startswith("head"):
         return tuple(input_spatial)
     parts = role.split(".")
@@ -236,7 +242,7 @@ def spatial_shape_for_role(role: str | None, input_spatial: tuple[int, ...]) -> 
     if top == "encoder_stages":
         halvings = int(parts[1])
     elif top == "downsamples":
-        halvings = int(parts[1]) + (0 if parts[-1] == "depthwise" else 1)
+        halvings = int(parts[1]) + (0 if parts[-1] in _BLOCK_INPUT_CONVS else 1)
     elif top == "bottleneck":
         halvings = 4
     elif top == "upsamples":
@@ -250,7 +256,7 @@ def spatial_shape_for_role(role: str | None, input_spatial: tuple[int, ...]) -> 
     shape = tuple(input_spatial)
     for _ in range(halvings):
         shape = tuple((s + 1) // 2 for s in shape)
-    if top == "upsamples" and parts[-1] != "depthwise":
+    if top == "upsamples" and parts[-1] not in _BLOCK_INPUT_CONVS:
         shape = tuple(2 * s - 1 for s in shape)
     return shape
 

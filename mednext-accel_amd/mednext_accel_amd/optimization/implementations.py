@@ -187,6 +187,19 @@ def _hip_expansion(descriptor, context, phase: str) -> str | None:
     return None
 
 
+def _hip_grn(descriptor, context, phase: str) -> str | None:
+    """Training GRN on an AMD GPU over half-precision activations, the input
+    contract of the reference's fused GRN (optimization/implementations.py:18-33)."""
+    reason = _training_gpu(context, amd=True)
+    if reason is not None:
+        return reason
+    if phase != "training":
+        return "implementation requires training"
+    if context.dtype not in ("float16", "bfloat16"):
+        return "implementation does not support this dtype"
+    return None
+
+
 def _pointwise_gemm(descriptor, context, phase: str) -> str | None:
     if context.phase != "training":
         return "implementation requires training"
@@ -228,6 +241,7 @@ def default_implementation_registry(*, triton_available: bool | None = None) -> 
         ("hip_group_norm", ("group_norm3d",), ("training",), "numerical", False, _hip_group_norm, _TENSOR_GUARDS),
         ("hip_pointwise_gemm", ("pointwise_conv3d", "conv_transpose3d"), ("training",), "numerical", False, _hip_pointwise, (*_TENSOR_GUARDS, "channels_supported")),
         ("hip_fused_expansion", ("mlp_expansion3d",), ("training",), "numerical", False, _hip_expansion, (*_TENSOR_GUARDS, "channels_supported")),
+        ("hip_fused_grn", ("global_response_norm3d",), ("training",), "numerical", False, _hip_grn, _TENSOR_GUARDS),
         ("pointwise_gemm_per_sample", ("pointwise_conv3d",), ("training",), "numerical", False, _pointwise_gemm, _TENSOR_GUARDS),
         ("triton_depthwise_dx", ("depthwise_conv3d",), ("backward_input",), "numerical", False, _no_triton, _DW_GUARDS),
         ("triton_split_dw", ("depthwise_conv3d",), ("backward_weight",), "numerical", False, _no_triton, _DW_GUARDS),

@@ -19,6 +19,12 @@ Pinning (how each oracle function is itself checked, see tests/test_oracle.py):
   pointwise.*      torch float64 F.conv3d(1x1x1) / addmm, the golden fixtures, an
                    asymmetric shape that fails a transposed weight, and GELU
                    special values (gelu(0)=0, odd part, large-|x| limits).
+  grn.*            torch float64 autograd of the reference's GRN formula (a
+                   check of the hand-derived backward), central finite
+                   differences, the reference tests' closed-form coupling case
+                   (x = (1, 2, 4), gamma = (2, 3, -4), dy only in channel 0 ->
+                   -2 / (7 + eps)^2 in the others) and the all-zero input
+                   (dx = dy exactly, dgamma = 0).
   reference_cpu.*  not a restatement: the reference's own CPU path (PyTorch's
                    F.conv3d + aten.convolution_backward), timed by bench.py as
                    the CPU baseline.
