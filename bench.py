@@ -56,8 +56,13 @@ def parse_args() -> argparse.Namespace:
                     help="skip the MedNeXt-Large k5 checkpointed training step (configs[4])")
     ap.add_argument("--large-steps", type=int, default=10)
     ap.add_argument("--large-warmup", type=int, default=5)
+    ap.add_argument("--no-v2-step", action="store_true", help="skip the MedNeXt v2 Base training step")
+    ap.add_argument("--v2-steps", type=int, default=10)
+    ap.add_argument("--v2-warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
-    ap.add_argument("--train-only", action="store_true", help="time only the MedNeXt-Base training step(s)")
+    ap.add_argument("--train-only", action="store_true", help="time only the training step(s) of --train-variants")
+    ap.add_argument("--train-variants", default="base,large,v2",
+                    help="comma list of base / large / v2 for --train-only (--no-large-step / --no-v2-step drop one)")
     ap.add_argument(
         "--sweep",
         action="store_true",
@@ -196,14 +201,17 @@ def time_train_step(args, torch, optimization: str, variant: str = "base", steps
     reference's step protocol (benchmarks/implementations.py:133-190): event
     median over the timed steps. ``base``: MedNeXt-Base k3, no checkpointing
     (configs[3]); ``large``: MedNeXt-Large k5 with expansion-branch
-    checkpointing on all stages."""
-    from mednext_accel_amd import CheckpointConfig, mednext_base, mednext_large
+    checkpointing on all stages; ``v2``: MedNeXt v2 Base (GRN in
+    every expansion), no checkpointing."""
+    from mednext_accel_amd import CheckpointConfig, mednext_base, mednext_large, mednext_v2_base
     from mednext_accel_amd.step import make_training_step
 
     steps = args.train_steps if steps is None else steps
     warmup = args.train_warmup if warmup is None else warmup
     torch.manual_seed(1234)
-    if variant == "large":
+    if variant == "v2":
+        model = mednext_v2_base(in_channels=1, out_channels=3, deep_supervision=True, optimization=optimization)
+    elif variant == "large":
         model = mednext_large(in_channels=1, out_channels=3, kernel_size=5, deep_supervision=True,
                               checkpointing=CheckpointConfig(style="expansion", stages=None), optimization=optimization)
     else:
@@ -294,6 +302,7 @@ def cpu_baseline(args, torch):
 STAGE_SHAPES = ((32, 128), (64, 64), (128, 32), (256, 16), (512, 8))
 # MedNeXt-Base expansion ratios of the encoder stages 0-4 (stage 4 = bottleneck).
 BASE_RATIOS = (2, 3, 4, 4, 4)
+V2_RATIOS = (3, 4, 8, 8, 8)  # MedNeXt v2 encoder expansion ratios
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 ROTATE_BYTES = 768 << 20  # rotate inputs over > 3x the 256 MiB Infinity Cache
 
@@ -341,6 +350,28 @@ def sweep(args, torch, hip_ops, lead: GpuLead) -> None:
             rec.update(tflops=round(tf, 2), mfma_frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4))
         rec.update(extra)
         _emit(rec)
+
+    for (c, s), ratio in zip(STAGE_SHAPES, V2_RATIOS):
+        # GRN of a MedNeXt v2 expansion (C * ratio channels) at this stage, bf16
+        # in / out, float32 affine, autocast form (bf16 upstream gradient).
+        # Algorithmic bytes: forward reads x, writes y; backward reads dy and x,
+        # writes dx (the kernels read x a second time to apply the norms).
+        m = c * ratio
+        e = m * s**3
+        nsets = max(1, min(12, -(-ROTATE_BYTES // (4 * e))))
+        gx = [randn(1, m, s, s, s) for _ in range(nsets)]
+        gdy = [randn(1, m, s, s, s) for _ in range(nsets)]
+        gam = torch.randn(1, m, 1, 1, 1, generator=gen, device=dev)
+        bet = torch.randn(1, m, 1, 1, 1, generator=gen, device=dev)
+        us = _timed_launches(torch, lead, lambda i: hip_ops.grn_forward(gx[i], gam, bet), nsets, reps)
+        record("grn_forward", f"1x{m}x{s}^3", us, 4 * e)
+        coefs = [hip_ops.grn_forward(gx[i], gam, bet)[1] for i in range(nsets)]
+        us = _timed_launches(
+            torch, lead, lambda i: hip_ops.grn_backward(gdy[i], gx[i], coefs[i], gam, param_shape=(1, m, 1, 1, 1)),
+            nsets, reps)
+        record("grn_backward", f"1x{m}x{s}^3", us, 6 * e)
+        del gx, gdy, coefs
+        torch.cuda.empty_cache()
 
     for (c, s), ratio in zip(STAGE_SHAPES, BASE_RATIOS):
         e = c * s**3
@@ -446,10 +477,15 @@ def main() -> int:
         sweep(args, torch, hip_ops, lead)
         return 0
     if args.train_only:
-        out = {"train_step_hip": time_train_step(args, torch, "auto")}
-        if not args.no_large_step:
+        variants = {v.strip() for v in args.train_variants.split(",") if v.strip()}
+        out = {}
+        if "base" in variants:
+            out["train_step_hip"] = time_train_step(args, torch, "auto")
+        if "large" in variants and not args.no_large_step:
             out["train_step_large_hip"] = time_train_step(args, torch, "auto", "large", args.large_steps,
                                                           args.large_warmup)
+        if "v2" in variants and not args.no_v2_step:
+            out["train_step_v2_hip"] = time_train_step(args, torch, "auto", "v2", args.v2_steps, args.v2_warmup)
         print(json.dumps(out))
         return 0
     dw = time_depthwise(args, torch, hip_ops, lead)
@@ -528,6 +564,20 @@ def main() -> int:
                 "speedup_vs_reference_eager": round(big_eager["median_step_ms"] / big["median_step_ms"], 3)
                 if big_eager else None,
             }
+    if not args.no_train_step and not args.no_v2_step:
+        v2 = time_train_step(args, torch, "auto", "v2", args.v2_steps, args.v2_warmup)
+        v2_eager = None if args.no_eager_step else time_train_step(
+            args, torch, "reference", "v2", max(3, args.v2_steps // 2), 2)
+        result["train_step_v2"] = {
+            "model": (
+                f"MedNeXt v2 Base (GRN), 1x1x{args.train_size}^3, 5-head deep supervision, no checkpointing, "
+                "bf16 autocast, AdamW lr 1e-3, random init, synthetic N(0,1) input and uniform labels"
+            ),
+            "hip": v2,
+            "reference_eager": v2_eager,
+            "speedup_vs_reference_eager": round(v2_eager["median_step_ms"] / v2["median_step_ms"], 3)
+            if v2_eager else None,
+        }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, torch)
     print(json.dumps(result))

@@ -170,18 +170,38 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
  * < 2 GiB, bf16-aligned tensors and a 16-byte aligned weight.
  * Prologue, applied to every x element as loaded:
  *   MEDNEXT_PW_PROLOGUE_GELU: x -> GELU(x) (exact erf form).
+ *   MEDNEXT_PW_PROLOGUE_GELU_AFFINE: x -> a * s[n][k] + t[n][k], a = bf16(GELU(x)),
+ *     (s, t) = entries 0 and 1 of the fp64 record prologue_coef[(n * K + k) * 4]
+ *     (the layout mednext_grn_stats writes: GRN of the GELU output, folded in).
+ *     The weight gradient rounds a * s + t to bf16 per element; the forward
+ *     product computes the same W . (a s + t) as (W diag(s)) . a + W . t, with
+ *     W diag(s) rounded to bf16 and W . t added to the bias in fp32
+ *     (weight_layout 0 only).
  * Epilogue, applied to each accumulator y[n][m][v] (bias may be NULL):
  *   BIAS:          y = acc + bias[m]
  *   BIAS_GELU:     y = GELU(acc + bias[m])
  *   BIAS_RESIDUAL: y = acc + bias[m] + aux[n][m][v]
  *   GELU_GRAD:     y = acc * GELU'(aux[n][m][v])   (bias unused)
+ *   ROW_REDUCE:    y is not written; per row, row_partial receives the fp64
+ *                  pair (sum_v acc * a, sum_v acc), a = bf16(GELU(aux)), one
+ *                  pair per slot: row_partial[((n * M + m) * slots + slot) * 2]
+ *                  (slots from mednext_pointwise_row_slots; bias unused)
+ *   AFFINE_GELU_GRAD: y = (acc * c0 + a * c1) * GELU'(aux[n][m][v]) with
+ *                  (c0, c1) = epilogue_coef[(n * M + m) * 2 + {0, 1}] (fp64)
+ *                  and a = bf16(GELU(aux)) (bias unused)
  */
-enum mednext_pw_prologue { MEDNEXT_PW_PROLOGUE_NONE = 0, MEDNEXT_PW_PROLOGUE_GELU = 1 };
+enum mednext_pw_prologue {
+  MEDNEXT_PW_PROLOGUE_NONE = 0,
+  MEDNEXT_PW_PROLOGUE_GELU = 1,
+  MEDNEXT_PW_PROLOGUE_GELU_AFFINE = 2
+};
 enum mednext_pw_epilogue {
   MEDNEXT_PW_EPILOGUE_BIAS = 0,
   MEDNEXT_PW_EPILOGUE_BIAS_GELU = 1,
   MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL = 2,
-  MEDNEXT_PW_EPILOGUE_GELU_GRAD = 3
+  MEDNEXT_PW_EPILOGUE_GELU_GRAD = 3,
+  MEDNEXT_PW_EPILOGUE_ROW_REDUCE = 4,
+  MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD = 5
 };
 
 /* y = epilogue(op(W) . prologue(x)); blocks_per_sample = workgroups along V
@@ -197,6 +217,26 @@ int32_t mednext_pointwise_fwd(const void* x, const void* weight, const void* bia
                               int32_t weight_layout, int32_t prologue, int32_t epilogue,
                               int32_t dtype, int32_t blocks_per_sample, void* stream);
 
+/* mednext_pointwise_fwd with the coefficient tensors of the GELU_AFFINE
+ * prologue and the ROW_REDUCE / AFFINE_GELU_GRAD epilogues (NULL where the
+ * chosen mode does not use them). Together they run the MedNeXt v2 block
+ * expansion project(GRN(GELU(expand(x)))) without materialising GELU or GRN
+ * outputs: the forward of the project GEMM (reference models/blocks_v2.py:44-45
+ * with ops/grn.py:16-30 between the GEMMs), and in the backward the GRN row sums
+ * and the gradient through GRN and GELU (reference ops/_triton/grn.py:242-317
+ * plus the GELU backward). */
+int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* bias, const void* aux,
+                                 void* y, int64_t n, int64_t k, int64_t m, int64_t v,
+                                 int32_t weight_layout, int32_t prologue, int32_t epilogue,
+                                 const void* prologue_coef, const void* epilogue_coef,
+                                 void* row_partial, int32_t dtype, int32_t blocks_per_sample,
+                                 void* stream);
+
+/* Slots per (sample, row) the ROW_REDUCE epilogue writes for this launch
+ * shape (0 on invalid arguments). */
+int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, int64_t v,
+                                    int32_t blocks_per_sample);
+
 /* Bytes of workspace the weight-gradient launch needs: fp32 per-split
  * partials followed by fp64 range sums (8-byte aligned). */
 size_t mednext_pointwise_wgrad_workspace_bytes(int64_t n, int64_t k, int64_t m, int64_t v,
@@ -211,6 +251,14 @@ int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* gr
                                 void* grad_bias, void* workspace, size_t workspace_bytes,
                                 int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
                                 int32_t dtype, int32_t splits, void* stream);
+
+/* mednext_pointwise_wgrad with the prologue's coefficient records (for
+ * GELU_AFFINE: the GRN-normalised GELU output as the x operand). */
+int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const void* x, void* grad_weight,
+                                   void* grad_bias, void* workspace, size_t workspace_bytes,
+                                   int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
+                                   const void* prologue_coef, int32_t dtype, int32_t splits,
+                                   void* stream);
 
 /* ------------------------------------------------------------------ GRN
  * Global Response Normalization of MedNeXt v2 on [N, C, V]:
@@ -229,6 +277,26 @@ int32_t mednext_grn_fwd(const void* x, int32_t x_dtype, const void* gamma, const
                         int32_t param_dtype, void* y, void* coef, int64_t n, int64_t c,
                         int64_t spatial, double eps, int32_t splits, void* workspace,
                         size_t workspace_bytes, void* stream);
+
+/* Statistics only (no output tensor): coef as mednext_grn_fwd writes it, of
+ * x itself (gelu_input 0) or of bf16(GELU(x)) (gelu_input 1, bf16 x only: the
+ * MedNeXt v2 expansion, whose GELU is fused into the next GEMM). Same
+ * workspace as mednext_grn_fwd. */
+int32_t mednext_grn_stats(const void* x, int32_t x_dtype, int32_t gelu_input, const void* gamma,
+                          const void* beta, int32_t param_dtype, void* coef, int64_t n, int64_t c,
+                          int64_t spatial, double eps, int32_t splits, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* The GRN backward's per-(n, c) coefficients from row sums a GEMM epilogue
+ * produced (row_partial [N][C][slots][2] fp64 = partial (sum dy * y_in,
+ * sum dy), see MEDNEXT_PW_EPILOGUE_ROW_REDUCE): coef_out [N][C][2] fp64 =
+ * (1 + gamma r, (gamma g / (S + eps) - T / (S + eps)^2) / n_c), and the
+ * parameter gradients grad_gamma / grad_beta ([C], param_dtype, nullable).
+ * workspace: N * C * 4 doubles. */
+int32_t mednext_grn_bwd_rows(const void* row_partial, int64_t slots, const void* coef,
+                             const void* gamma, int32_t param_dtype, void* coef_out,
+                             void* grad_gamma, void* grad_beta, int64_t n, int64_t c, double eps,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* grad_input (x's dtype, nullable), grad_gamma / grad_beta ([C], param_dtype,
  * nullable) from grad_output (pairs dy/x: same dtype, or f32 with bf16/f16 x),

@@ -15,6 +15,7 @@
 // and derives the per-(n, c) coefficients; (3) an elementwise pass applies
 // them. Rows stream as a scalar head, 16-byte vectors and a scalar tail, so any
 // volume is handled. All reductions are fixed-order (bit-reproducible).
+#include "activation.h"
 #include "common.h"
 
 namespace mednext {
@@ -76,8 +77,9 @@ __device__ inline void store_param(void* p, int dtype, int64_t i, double v) {
   }
 }
 
-// Pass 1 (forward): partial sum of squares per (row, split).
-template <typename T>
+// Pass 1 (forward): partial sum of squares per (row, split), of x or (GELU)
+// of bf16(GELU(x)) as the bf16 tensor torch's GELU would produce holds it.
+template <typename T, bool GELU = false>
 __global__ __launch_bounds__(kThreads) void grn_sumsq_kernel(const T* __restrict__ x, int64_t v, int splits,
                                                             int64_t chunk, bool vec_ok, double* __restrict__ part) {
   using Acc = typename AccOf<T>::type;
@@ -86,7 +88,8 @@ __global__ __launch_bounds__(kThreads) void grn_sumsq_kernel(const T* __restrict
   const RowSpan rs = row_span(ck.row * v + ck.begin, ck.end - ck.begin, vec_ok);
   Acc s = Acc(0);
   for (int64_t i = threadIdx.x; i < rs.scalar_count(); i += blockDim.x) {
-    const Acc e = Cvt<T, Acc>::load(cp[rs.scalar_index(i)]);
+    Acc e = Cvt<T, Acc>::load(cp[rs.scalar_index(i)]);
+    if constexpr (GELU) e = gelu_bf16(e);
     s += e * e;
   }
   for (int64_t j0 = threadIdx.x; j0 < rs.nvec; j0 += kUnroll * blockDim.x) {
@@ -104,7 +107,11 @@ __global__ __launch_bounds__(kThreads) void grn_sumsq_kernel(const T* __restrict
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) s += e[u][t] * e[u][t];
+      for (int t = 0; t < 8; ++t) {
+        Acc f = e[u][t];
+        if constexpr (GELU) f = gelu_bf16(f);  // gelu(0) = 0: padding stays zero
+        s += f * f;
+      }
   }
   double a = s, b = 0.0;
   block_sum2(a, b);
@@ -310,6 +317,25 @@ __global__ __launch_bounds__(kThreads) void grn_bwd_apply_kernel(const Tdy* __re
   }
 }
 
+// Row sums of GEMM-epilogue partials: one wave per (n, c) row; lane l sums
+// slots l, l + 64, ... in order, then a fixed wave reduction.
+__global__ __launch_bounds__(64) void grn_row_sum_kernel(const double* __restrict__ rpart, int64_t slots,
+                                                       double* __restrict__ out) {
+  const int64_t row = blockIdx.x;
+  const double* p = rpart + row * slots * 2;
+  double a = 0.0, b = 0.0;
+  for (int64_t s = threadIdx.x; s < slots; s += 64) {
+    a += p[2 * s];
+    b += p[2 * s + 1];
+  }
+  a = wave_sum(a);
+  b = wave_sum(b);
+  if (threadIdx.x == 0) {
+    out[row * 2] = a;
+    out[row * 2 + 1] = b;
+  }
+}
+
 __global__ void grn_param_grad_kernel(const double* __restrict__ rows, int64_t n, int64_t c,
                                       void* __restrict__ dgamma, void* __restrict__ dbeta, int pdtype) {
   const int64_t ch = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -341,6 +367,21 @@ size_t fwd_workspace(int64_t n, int64_t c, int splits) { return static_cast<size
 // Backward workspace: partials [N*C*splits*2] + coefficients [N*C*2] + rows [N*C*2].
 size_t bwd_workspace(int64_t n, int64_t c, int splits) {
   return static_cast<size_t>(n * c * (static_cast<int64_t>(splits) * 2 + 4)) * sizeof(double);
+}
+
+// Pass 1 + pass 2 only: coef without an output tensor.
+template <typename T, bool GELU>
+int grn_stats_typed(const void* x, const void* gamma, const void* beta, int pdtype, double* coef, int64_t n,
+                    int64_t c, int64_t v, double eps, int splits, double* part, hipStream_t st) {
+  const int64_t chunk = chunk_len(v, splits);
+  const int64_t blocks = n * c * splits;
+  hipLaunchKernelGGL((grn_sumsq_kernel<T, GELU>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st,
+                     static_cast<const T*>(x), v, splits, chunk, aligned64(x), part);
+  MEDNEXT_CHECK_LAUNCH();
+  hipLaunchKernelGGL(grn_fwd_coef_kernel, dim3(static_cast<unsigned>(n)), dim3(kThreads), 0, st, part, c, splits,
+                     gamma, beta, pdtype, eps, coef);
+  MEDNEXT_CHECK_LAUNCH();
+  return MEDNEXT_STATUS_OK;
 }
 
 template <typename T>
@@ -451,4 +492,58 @@ extern "C" int32_t mednext_grn_bwd(const void* grad_output, int32_t dy_dtype, co
 #undef GRN_BWD
   set_error("mednext_grn_bwd: unsupported (grad_output, x) dtype pair");
   return MEDNEXT_STATUS_UNSUPPORTED;
+}
+
+extern "C" int32_t mednext_grn_stats(const void* x, int32_t x_dtype, int32_t gelu_input, const void* gamma,
+                                     const void* beta, int32_t param_dtype, void* coef, int64_t n, int64_t c,
+                                     int64_t spatial, double eps, int32_t splits, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  if (int st = check_shape(n, c, spatial, splits)) return st;
+  MEDNEXT_CHECK_ARG(x && coef, "null tensor pointer");
+  MEDNEXT_CHECK_ARG(dtype_ok(x_dtype) && dtype_ok(param_dtype), "unsupported dtype");
+  MEDNEXT_CHECK_ARG(gelu_input == 0 || (gelu_input == 1 && x_dtype == MEDNEXT_DTYPE_BF16),
+                    "gelu_input must be 0, or 1 with a bf16 input");
+  MEDNEXT_CHECK_ARG(eps > 0.0, "eps must be positive");
+  MEDNEXT_CHECK_ARG(workspace && workspace_bytes >= fwd_workspace(n, c, splits), "workspace too small");
+  auto* part = static_cast<double*>(workspace);
+  auto* cf = static_cast<double*>(coef);
+  auto s = static_cast<hipStream_t>(stream);
+  if (gelu_input) return grn_stats_typed<bf16_t, true>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+  switch (x_dtype) {
+    case MEDNEXT_DTYPE_F32: return grn_stats_typed<float, false>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+    case MEDNEXT_DTYPE_F64: return grn_stats_typed<double, false>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+    case MEDNEXT_DTYPE_F16: return grn_stats_typed<f16_t, false>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+    default: return grn_stats_typed<bf16_t, false>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+  }
+}
+
+extern "C" int32_t mednext_grn_bwd_rows(const void* row_partial, int64_t slots, const void* coef,
+                                        const void* gamma, int32_t param_dtype, void* coef_out, void* grad_gamma,
+                                        void* grad_beta, int64_t n, int64_t c, double eps, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  MEDNEXT_CHECK_ARG(n >= 1 && c >= 1, "shape must be positive");
+  MEDNEXT_CHECK_ARG(slots >= 1 && slots < (int64_t(1) << 24), "slots must be in [1, 2^24)");
+  MEDNEXT_CHECK_ARG(n < (int64_t(1) << 31) && n * c * slots < (int64_t(1) << 40), "problem too large");
+  MEDNEXT_CHECK_ARG(row_partial && coef && coef_out, "null tensor pointer");
+  MEDNEXT_CHECK_ARG(dtype_ok(param_dtype), "unsupported dtype");
+  MEDNEXT_CHECK_ARG(eps > 0.0, "eps must be positive");
+  MEDNEXT_CHECK_ARG(workspace && workspace_bytes >= static_cast<size_t>(n * c * 4) * sizeof(double),
+                    "workspace too small");
+  MEDNEXT_CHECK_ARG(n * c < (int64_t(1) << 31), "grid too large");
+  auto s = static_cast<hipStream_t>(stream);
+  auto* sums = static_cast<double*>(workspace);
+  double* rows = sums + n * c * 2;
+  hipLaunchKernelGGL(grn_row_sum_kernel, dim3(static_cast<unsigned>(n * c)), dim3(64), 0, s,
+                     static_cast<const double*>(row_partial), slots, sums);
+  MEDNEXT_CHECK_LAUNCH();
+  hipLaunchKernelGGL(grn_bwd_coef_kernel, dim3(static_cast<unsigned>(n)), dim3(kThreads), 0, s, sums,
+                     static_cast<const double*>(coef), c, 1, gamma, param_dtype, eps, static_cast<double*>(coef_out),
+                     rows);
+  MEDNEXT_CHECK_LAUNCH();
+  if (grad_gamma || grad_beta) {
+    hipLaunchKernelGGL(grn_param_grad_kernel, dim3(static_cast<unsigned>(cdiv(c, 256))), dim3(256), 0, s, rows, n,
+                       c, grad_gamma, grad_beta, param_dtype);
+    MEDNEXT_CHECK_LAUNCH();
+  }
+  return MEDNEXT_STATUS_OK;
 }

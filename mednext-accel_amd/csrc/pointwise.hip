@@ -29,12 +29,11 @@
 // Each workgroup writes a deterministic fp32 partial of its V range; a finish
 // kernel sums the partials in a fixed order in fp64.
 //
-// GELU is the exact (erf) form. erf uses Abramowitz & Stegun, Handbook of
-// Mathematical Functions, eq. 7.1.26 (|error| <= 1.5e-7), far below the bf16
-// rounding the results get.
+// GELU is the exact (erf) form (activation.h).
 #include <algorithm>
 #include <type_traits>
 
+#include "activation.h"
 #include "cdna4.h"
 #include "common.h"
 
@@ -57,41 +56,119 @@ struct PwGeom {
   int wt;       // 1: weight stored [K][M] (A = W^T), 0: [M][K]
 };
 
-__device__ inline float erf_as(float x) {
-  const float ax = fabsf(x);
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, ax, 1.0f));
-  float p = fmaf(1.061405429f, t, -1.453152027f);
-  p = fmaf(p, t, 1.421413741f);
-  p = fmaf(p, t, -0.284496736f);
-  p = fmaf(p, t, 0.254829592f);
-  p *= t;
-  const float r = 1.0f - p * __expf(-ax * ax);
-  return copysignf(r, x);
-}
-
-__device__ inline float gelu_f(float h) { return 0.5f * h * (1.0f + erf_as(h * 0.7071067811865476f)); }
-
-// d/dh of h * Phi(h) = Phi(h) + h * phi(h); phi(h) = exp(-h^2 / 2) / sqrt(2 pi)
-// shares its exponential with the erf approximation.
-__device__ inline float gelu_grad_f(float h) {
-  const float ax = fabsf(h) * 0.7071067811865476f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, ax, 1.0f));
-  float p = fmaf(1.061405429f, t, -1.453152027f);
-  p = fmaf(p, t, 1.421413741f);
-  p = fmaf(p, t, -0.284496736f);
-  p = fmaf(p, t, 0.254829592f);
-  p *= t;
-  const float e = __expf(-ax * ax);
-  const float erf_abs = 1.0f - p * e;
-  const float cdf = 0.5f + 0.5f * copysignf(erf_abs, h);
-  return fmaf(h * 0.3989422804014327f, e, cdf);
-}
-
 __device__ inline uint32_t gelu_word(uint32_t w) {
   return pack_bf16x2(gelu_f(bf16_lo(w)), gelu_f(bf16_hi(w)));
 }
 __device__ inline uint4 gelu_vec(uint4 v) {
   return make_uint4(gelu_word(v.x), gelu_word(v.y), gelu_word(v.z), gelu_word(v.w));
+}
+
+// bf16(bf16(GELU(x)) * s + t) for the 8 values of one 16-byte group.
+__device__ inline uint32_t gelu_affine_word(uint32_t w, float s, float t) {
+  return pack_bf16x2(fmaf(gelu_bf16(bf16_lo(w)), s, t), fmaf(gelu_bf16(bf16_hi(w)), s, t));
+}
+__device__ inline uint4 gelu_affine_vec(uint4 v, float s, float t) {
+  return make_uint4(gelu_affine_word(v.x, s, t), gelu_affine_word(v.y, s, t), gelu_affine_word(v.z, s, t),
+                    gelu_affine_word(v.w, s, t));
+}
+
+// Coefficient tensors of the GELU_AFFINE prologue and the ROW_REDUCE /
+// AFFINE_GELU_GRAD epilogues (unused members are null).
+struct PwExtra {
+  const double* pcoef;  // [N][K][4]: (s, t, ., .) per (sample, input channel)
+  const double* ecoef;  // [N][M][2]: (c0, c1) per (sample, output row)
+  double* rpart;        // [N][M][slots][2] row sums
+  int slots;
+};
+
+constexpr bool epi_has_aux(int epi) {
+  return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epi == MEDNEXT_PW_EPILOGUE_GELU_GRAD ||
+         epi == MEDNEXT_PW_EPILOGUE_ROW_REDUCE || epi == MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD;
+}
+
+// Per-row LDS vectors after the weight block: bias, then the AFFINE_GELU_GRAD
+// coefficients c0 and c1 (16 MT floats each).
+constexpr int kRowVecs = 3;
+
+// The forward GEMMs take GELU_AFFINE as W . (a s + t) = (W diag(s)) . a + W . t
+// with a = bf16(GELU(x)): the column scale goes into the LDS weight block
+// (load_weight_block), W . t into the row bias, and X only needs GELU.
+// shift[r] = sum_k W[m0 + r][k] t[k] for the workgroup's 16 MT rows (weight
+// stored [M][K]); threads_per_row consecutive lanes share a row and combine
+// their strided partial sums with shuffles (fixed order).
+template <int MT>
+__device__ void affine_row_shift(const bf16_t* __restrict__ w, const double* __restrict__ coef_n, const PwGeom& g,
+                                 int m0, float* shift) {
+  constexpr int ROWS = 16 * MT;
+  constexpr int TPR = kPwThreads / ROWS;
+  const int r = threadIdx.x / TPR, j = threadIdx.x % TPR;
+  const int m = m0 + r;
+  float acc = 0.f;
+  if (m < g.M) {
+    const uint16_t* __restrict__ wr = reinterpret_cast<const uint16_t*>(w) + static_cast<int64_t>(m) * g.K;
+    for (int k = j; k < g.K; k += TPR) acc = fmaf(bf16_to_f32(wr[k]), static_cast<float>(coef_n[k * 4 + 1]), acc);
+  }
+#pragma unroll
+  for (int off = 1; off < TPR; off <<= 1) acc += __shfl_xor(acc, off);
+  if (j == 0) shift[r] = acc;
+}
+
+// X slice rows through the prologue (GELU for GELU and, with the affine
+// folded into W and the bias, GELU_AFFINE).
+template <int PRO>
+__device__ inline void apply_prologue(const uint4 (&r)[8], uint4 (&cur)[8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) cur[i] = PRO != MEDNEXT_PW_PROLOGUE_NONE ? gelu_vec(r[i]) : r[i];
+}
+
+// One output row's 8 accumulators through a value epilogue (not ROW_REDUCE).
+// `av` holds the row's 8 aux values (bf16), b the row bias, c0 / c1 the
+// AFFINE_GELU_GRAD coefficients.
+template <int EPI>
+__device__ inline void epilogue_values(float (&v)[8], const uint4& av, float b, float c0, float c1) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] += b;
+  if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = gelu_f(v[j]);
+  } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD ||
+                       EPI == MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t wd = j / 2 == 0 ? av.x : j / 2 == 1 ? av.y : j / 2 == 2 ? av.z : av.w;
+      const float e = (j & 1) ? bf16_hi(wd) : bf16_lo(wd);
+      if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL) {
+        v[j] += e;
+      } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD) {
+        v[j] *= gelu_grad_f(e);
+      } else {
+        float g, dg;
+        gelu_pair(e, g, dg);
+        const float a = bf16_to_f32(f32_to_bf16(g));
+        v[j] = fmaf(v[j], c0, a * c1) * dg;
+      }
+    }
+  }
+}
+
+// ROW_REDUCE: add sum_j acc_j * bf16(GELU(aux_j)) and sum_j acc_j to (ra, rb).
+__device__ inline void row_reduce_add(const float (&v)[8], const uint4& av, float& ra, float& rb) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t wd = j / 2 == 0 ? av.x : j / 2 == 1 ? av.y : j / 2 == 2 ? av.z : av.w;
+    const float a = gelu_bf16((j & 1) ? bf16_hi(wd) : bf16_lo(wd));
+    ra = fmaf(v[j], a, ra);
+    rb += v[j];
+  }
+}
+
+// Sum over the 16 lanes of a row group (lanes differing in bits 0-3), fixed order.
+__device__ inline float sum16(float x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
 }
 
 __device__ inline uint32_t word(const uint4& v, int d) {
@@ -163,7 +240,8 @@ __device__ inline void store_group(__amdgpu_buffer_rsrc_t r, uint32_t off, uint3
 // 16-byte global reads when whole 8-element groups exist, element reads
 // otherwise (only for small, odd-shaped weights).
 template <int MT>
-__device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, const PwGeom& g, int m0) {
+__device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, const PwGeom& g, int m0,
+                                  const double* __restrict__ col_scale = nullptr) {
   constexpr int ROWS = 16 * MT;
   const int tid = threadIdx.x;
   const int kp = g.ks * 32;
@@ -182,6 +260,16 @@ __device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, c
         } else {
           uint32_t wd[4] = {0u, 0u, 0u, 0u};
           for (int e = 0; e < 8 && k8 + e < g.K; ++e) wd[e / 2] |= static_cast<uint32_t>(wr[base + e]) << (16 * (e & 1));
+          v = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        }
+        if (col_scale != nullptr) {  // W[m][k] * s[k], rounded to bf16
+          uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) {
+            const float s0 = k8 + e < g.K ? static_cast<float>(col_scale[(k8 + e) * 4]) : 0.f;
+            const float s1 = k8 + e + 1 < g.K ? static_cast<float>(col_scale[(k8 + e + 1) * 4]) : 0.f;
+            wd[e / 2] = pack_bf16x2(bf16_lo(wd[e / 2]) * s0, bf16_hi(wd[e / 2]) * s1);
+          }
           v = make_uint4(wd[0], wd[1], wd[2], wd[3]);
         }
       }
@@ -221,8 +309,9 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
                                                                const bf16_t* __restrict__ w,
                                                                const bf16_t* __restrict__ bias,
                                                                const bf16_t* __restrict__ aux,
-                                                               bf16_t* __restrict__ y, PwGeom g) {
-  constexpr bool kAux = EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD;
+                                                               bf16_t* __restrict__ y, PwGeom g, PwExtra ex) {
+  constexpr bool kAux = epi_has_aux(EPI);
+  constexpr bool kReduce = EPI == MEDNEXT_PW_EPILOGUE_ROW_REDUCE;
   extern __shared__ __align__(16) uint16_t pw_lds[];
   const int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
   const int mg = static_cast<int>(lin % g.mgroups);
@@ -230,13 +319,29 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   const int bx = static_cast<int>(rest % g.wgs);
   const int64_t n = rest / g.wgs;
   const int m0 = mg * 16 * MT;
-  load_weight_block<MT>(w, pw_lds, g, m0);
-  // Bias of this row group as fp32 after the weight block (zero past M).
+  constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE;
+  const double* const coef_n = kAffine ? ex.pcoef + n * g.K * 4 : nullptr;
+  load_weight_block<MT>(w, pw_lds, g, m0, coef_n);
+  // Row vectors of this row group as fp32 after the weight block (zero past
+  // M): bias (plus W . t for GELU_AFFINE), then the AFFINE_GELU_GRAD
+  // coefficients c0, c1.
   float* const bias_lds = reinterpret_cast<float*>(pw_lds + static_cast<size_t>(16 * MT) * g.ks * 32);
+  float* const c0_lds = bias_lds + 16 * MT;
+  float* const c1_lds = c0_lds + 16 * MT;
+  if constexpr (kAffine) {
+    affine_row_shift<MT>(w, coef_n, g, m0, c0_lds);
+    __syncthreads();
+  }
   if (threadIdx.x < 16 * MT) {
     const int m = m0 + threadIdx.x;
-    bias_lds[threadIdx.x] =
-        (EPI != MEDNEXT_PW_EPILOGUE_GELU_GRAD && bias != nullptr && m < g.M) ? bf16_to_f32(bias[m].bits) : 0.f;
+    const bool in = m < g.M;
+    float b = (EPI <= MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
+    if constexpr (kAffine) b += c0_lds[threadIdx.x];
+    bias_lds[threadIdx.x] = b;
+    if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD) {
+      c0_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2]) : 0.f;
+      c1_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2 + 1]) : 0.f;
+    }
   }
   __syncthreads();
 
@@ -274,8 +379,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   };
   auto mma_slice = [&](const uint4 (&r)[8], int ks, f32x4_t (&acc)[MT][8]) {
     uint4 cur[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) cur[i] = PRO == MEDNEXT_PW_PROLOGUE_GELU ? gelu_vec(r[i]) : r[i];
+    apply_prologue<PRO>(r, cur);
     uint4 bv[8];
     transpose8x8(cur, bv);
 #pragma unroll
@@ -300,6 +404,12 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
         }
     }
   };
+  // ROW_REDUCE: this lane's running row sums (rows 16 mt + 4 q + r).
+  float rsa[MT][4], rsb[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) rsa[mt][r] = rsb[mt][r] = 0.f;
   auto epilogue = [&](int chunk, const f32x4_t (&acc)[MT][8], const uint4 (&av)[MT][4]) {
     const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
     const uint32_t nv = valid(chunk);
@@ -310,30 +420,49 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
       for (int r = 0; r < 4; ++r) {
         const int mrow = m0 + 16 * mt + 4 * q + r;
         const uint32_t m = static_cast<uint32_t>(min(mrow, g.M - 1));
-        const float bv = bias_lds[16 * mt + 4 * q + r];
+        const int lr = 16 * mt + 4 * q + r;
         float v[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = acc[mt][j][r] + bv;
-        if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU) {
+        for (int j = 0; j < 8; ++j) v[j] = acc[mt][j][r];
+        if constexpr (kReduce) {
+          // Voxels past V and rows past M have zero accumulators: no masking.
+          row_reduce_add(v, av[mt][r], rsa[mt][r], rsb[mt][r]);
+        } else {
+          uint4 a4 = make_uint4(0u, 0u, 0u, 0u);
+          if constexpr (kAux) a4 = av[mt][r];
+          epilogue_values<EPI>(v, a4, bias_lds[lr], c0_lds[lr], c1_lds[lr]);
+          store_group(yr, (m * V + vl) * 2u, mrow < g.M ? nv : 0u,
+                      make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                                 pack_bf16x2(v[6], v[7])));
+        }
+      }
+    }
+  };
+  // ROW_REDUCE: one slot per wave (bx * 4 + wave), written once at the end
+  // (zeros for a wave without chunks).
+  auto flush_rows = [&]() {
+    if constexpr (kReduce) {
+      const int slot = bx * 4 + wave;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v[j] = gelu_f(v[j]);
-        } else if constexpr (kAux) {
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint32_t wd = word(av[mt][r], j / 2);
-            const float e = (j & 1) ? bf16_hi(wd) : bf16_lo(wd);
-            v[j] = EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD ? v[j] * gelu_grad_f(e) : v[j] + e;
+        for (int r = 0; r < 4; ++r) {
+          const float a = sum16(rsa[mt][r]), b = sum16(rsb[mt][r]);
+          const int mrow = m0 + 16 * mt + 4 * q + r;
+          if (n_col == 0 && mrow < g.M) {
+            double* dst = ex.rpart + ((n * g.M + mrow) * static_cast<int64_t>(ex.slots) + slot) * 2;
+            dst[0] = a;
+            dst[1] = b;
           }
         }
-        store_group(yr, (m * V + vl) * 2u, mrow < g.M ? nv : 0u,
-                    make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                               pack_bf16x2(v[6], v[7])));
-      }
     }
   };
 
   int chunk = bx * 4 + wave;
-  if (chunk >= g.chunks) return;  // no barrier follows
+  if (chunk >= g.chunks) {  // no barrier follows
+    flush_rows();
+    return;
+  }
   if constexpr (KS > 0) {
     uint4 xb[2][8];
     load_slice(chunk, 0, xb[0]);
@@ -369,6 +498,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
         if (chunk >= g.chunks) break;
       }
     }
+    flush_rows();
   } else {
     const int ksteps = g.ks;
     for (; chunk < g.chunks; chunk += cstride) {
@@ -391,6 +521,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
       if (ks < ksteps) mma_slice(xa, ks, acc);
       epilogue(chunk, acc, av);
     }
+    flush_rows();
   }
 }
 
@@ -406,8 +537,9 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
                                                                       const bf16_t* __restrict__ w,
                                                                       const bf16_t* __restrict__ bias,
                                                                       const bf16_t* __restrict__ aux,
-                                                                      bf16_t* __restrict__ y, PwGeom g) {
-  constexpr bool kAux = EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD;
+                                                                      bf16_t* __restrict__ y, PwGeom g, PwExtra ex) {
+  constexpr bool kAux = epi_has_aux(EPI);
+  constexpr bool kReduce = EPI == MEDNEXT_PW_EPILOGUE_ROW_REDUCE;
   extern __shared__ __align__(16) uint16_t pw_lds[];
   const int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
   const int mg = static_cast<int>(lin % g.mgroups);
@@ -415,13 +547,27 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
   const int bx = static_cast<int>(rest % g.wgs);
   const int64_t n = rest / g.wgs;
   const int m0 = mg * 16 * MT;
-  load_weight_block<MT>(w, pw_lds, g, m0);
+  constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE;
+  const double* const coef_n = kAffine ? ex.pcoef + n * g.K * 4 : nullptr;
+  load_weight_block<MT>(w, pw_lds, g, m0, coef_n);
   float* const bias_lds = reinterpret_cast<float*>(pw_lds + static_cast<size_t>(16 * MT) * g.ks * 32);
-  float* const red = bias_lds + 16 * MT;  // [MT][8][4][64] partial sums
+  float* const c0_lds = bias_lds + 16 * MT;
+  float* const c1_lds = c0_lds + 16 * MT;
+  float* const red = bias_lds + kRowVecs * 16 * MT;  // [MT][8][4][64] partial sums
+  if constexpr (kAffine) {
+    affine_row_shift<MT>(w, coef_n, g, m0, c0_lds);
+    __syncthreads();
+  }
   if (threadIdx.x < 16 * MT) {
     const int m = m0 + threadIdx.x;
-    bias_lds[threadIdx.x] =
-        (EPI != MEDNEXT_PW_EPILOGUE_GELU_GRAD && bias != nullptr && m < g.M) ? bf16_to_f32(bias[m].bits) : 0.f;
+    const bool in = m < g.M;
+    float b = (EPI <= MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
+    if constexpr (kAffine) b += c0_lds[threadIdx.x];
+    bias_lds[threadIdx.x] = b;
+    if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD) {
+      c0_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2]) : 0.f;
+      c1_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2 + 1]) : 0.f;
+    }
   }
   __syncthreads();
 
@@ -434,6 +580,9 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
   const __amdgpu_buffer_rsrc_t ar = slab_rsrc(auxn != nullptr ? auxn : y, auxn != nullptr ? g.M * V * 2u : 0u);
   const int mtiles = min(MT, (g.M - m0 + 15) / 16);
   const uint4* frag = reinterpret_cast<const uint4*>(pw_lds) + lane;
+  float rsa[MT], rsb[MT];  // ROW_REDUCE running sums of rows 16 mt + 4 q + wave
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) rsa[mt] = rsb[mt] = 0.f;
 
   for (int chunk = bx; chunk < g.chunks; chunk += g.wgs) {
     const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
@@ -466,8 +615,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
       for (int j = 0; j < 8; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     auto mma_slice = [&](const uint4 (&r)[8], int ks) {
       uint4 cur[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) cur[i] = PRO == MEDNEXT_PW_PROLOGUE_GELU ? gelu_vec(r[i]) : r[i];
+      apply_prologue<PRO>(r, cur);
       uint4 bv[8];
       transpose8x8(cur, bv);
 #pragma unroll
@@ -510,26 +658,35 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
       if (mt >= mtiles) continue;
       const int mrow = m0 + 16 * mt + 4 * q + wave;
       const uint32_t m = static_cast<uint32_t>(min(mrow, g.M - 1));
-      const float b = bias_lds[16 * mt + 4 * q + wave];
+      const int lr = 16 * mt + 4 * q + wave;
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = red[((mt * 8 + j) * 4 + wave) * 64 + lane] + b;
-      if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = gelu_f(v[j]);
-      } else if constexpr (kAux) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint32_t wd = word(av[mt], j / 2);
-          const float e = (j & 1) ? bf16_hi(wd) : bf16_lo(wd);
-          v[j] = EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD ? v[j] * gelu_grad_f(e) : v[j] + e;
-        }
+      for (int j = 0; j < 8; ++j) v[j] = red[((mt * 8 + j) * 4 + wave) * 64 + lane];
+      if constexpr (kReduce) {
+        row_reduce_add(v, av[mt], rsa[mt], rsb[mt]);
+      } else {
+        uint4 a4 = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (kAux) a4 = av[mt];
+        epilogue_values<EPI>(v, a4, bias_lds[lr], c0_lds[lr], c1_lds[lr]);
+        store_group(yr, (m * V + vl) * 2u, mrow < g.M ? nv : 0u,
+                    make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                               pack_bf16x2(v[6], v[7])));
       }
-      store_group(yr, (m * V + vl) * 2u, mrow < g.M ? nv : 0u,
-                  make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                             pack_bf16x2(v[6], v[7])));
     }
     __syncthreads();  // the next chunk's turn 0 overwrites the sums read above
+  }
+  if constexpr (kReduce) {
+    // One slot per workgroup (bx); zeros when it had no chunk.
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float a = sum16(rsa[mt]), b = sum16(rsb[mt]);
+      const int mrow = m0 + 16 * mt + 4 * q + wave;
+      if (n_col == 0 && mrow < g.M) {
+        double* dst = ex.rpart + ((n * g.M + mrow) * static_cast<int64_t>(ex.slots) + bx) * 2;
+        dst[0] = a;
+        dst[1] = b;
+      }
+    }
   }
 }
 
@@ -545,6 +702,7 @@ struct PwWGeom {
   uint32_t span;   // voxels per split (multiple of kWgStage)
   int mblocks, kblocks;
   int64_t stride;  // floats per partial slot: M * K + M
+  const double* pcoef;  // GELU_AFFINE prologue records [N][K][4] (else null)
 };
 
 // dW[M][K] = sum_v dY[M][v] X[K][v] over one split's voxel range, for an output
@@ -584,6 +742,17 @@ __global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_ke
   const uint32_t vbeg = static_cast<uint32_t>(split) * g.span;
   const uint32_t vend = min(V, vbeg + g.span);
   const bool do_bias = k0 == 0;
+  // GELU_AFFINE: (s, t) of the tile's X rows in LDS (zero past K); voxels
+  // past the range load as zero and become t, which meets zero grad_output.
+  __shared__ float aff[PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE ? 2 * RK : 1];
+  if constexpr (PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) {
+    for (int i = threadIdx.x; i < RK; i += kPwThreads) {
+      const int k = k0 + i;
+      aff[i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4]) : 0.f;
+      aff[RK + i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4 + 1]) : 0.f;
+    }
+    __syncthreads();
+  }
 
   // Load slot u of this thread: tile row r = tid / 16 + 16 u (dY rows first,
   // then X rows), voxels 8 (tid % 16) .. + 7 of the stage.
@@ -626,6 +795,8 @@ __global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_ke
         }
       } else if (PRO == MEDNEXT_PW_PROLOGUE_GELU) {
         v = gelu_vec(v);  // gelu(0) = 0: missing voxels stay zero
+      } else if (PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) {
+        v = gelu_affine_vec(v, aff[r - RM], aff[RK + r - RM]);
       }
       *reinterpret_cast<uint4*>(tile + r * kWgPitch + 8 * grp) = v;
     }
@@ -759,12 +930,24 @@ int check_pw_shape(int64_t n, int64_t k, int64_t m, int64_t v, int32_t dtype) {
   return MEDNEXT_STATUS_OK;
 }
 
-using FwdKernel = void (*)(const bf16_t*, const bf16_t*, const bf16_t*, const bf16_t*, bf16_t*, PwGeom);
+using FwdKernel = void (*)(const bf16_t*, const bf16_t*, const bf16_t*, const bf16_t*, bf16_t*, PwGeom, PwExtra);
 
 constexpr int kSplitKSlices = 8;  // K >= 256: the four waves of a workgroup split K
 
+// Supported (prologue, epilogue) pairs: NONE with any epilogue, GELU with
+// BIAS .. GELU_GRAD, GELU_AFFINE with BIAS or BIAS_RESIDUAL.
+bool pro_epi_supported(int pro, int epi) {
+  if (pro == MEDNEXT_PW_PROLOGUE_NONE) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD;
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_GELU_GRAD;
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) return epi == MEDNEXT_PW_EPILOGUE_BIAS || epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL;
+  return false;
+}
+
 template <int MT>
 FwdKernel splitk_instance(int pro, int epi) {
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) {
+    return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL ? pw_fwd_splitk_kernel<MT, 2, 2> : pw_fwd_splitk_kernel<MT, 2, 0>;
+  }
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
     switch (epi) {
       case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_splitk_kernel<MT, 1, 0>;
@@ -777,13 +960,16 @@ FwdKernel splitk_instance(int pro, int epi) {
     case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_splitk_kernel<MT, 0, 0>;
     case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_splitk_kernel<MT, 0, 1>;
     case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_splitk_kernel<MT, 0, 2>;
-    default: return pw_fwd_splitk_kernel<MT, 0, 3>;
+    case MEDNEXT_PW_EPILOGUE_GELU_GRAD: return pw_fwd_splitk_kernel<MT, 0, 3>;
+    case MEDNEXT_PW_EPILOGUE_ROW_REDUCE: return pw_fwd_splitk_kernel<MT, 0, 4>;
+    default: return pw_fwd_splitk_kernel<MT, 0, 5>;
   }
 }
 
 // Four-tile row groups are only used by epilogues without an aux tensor.
 template <int KS, int MT>
 FwdKernel fwd_instance_noaux(int pro, int epi) {
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) return pw_fwd_kernel<KS, MT, 2, 0>;
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
     return epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU ? pw_fwd_kernel<KS, MT, 1, 1> : pw_fwd_kernel<KS, MT, 1, 0>;
   }
@@ -792,6 +978,9 @@ FwdKernel fwd_instance_noaux(int pro, int epi) {
 
 template <int KS, int MT>
 FwdKernel fwd_instance(int pro, int epi) {
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) {
+    return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL ? pw_fwd_kernel<KS, MT, 2, 2> : pw_fwd_kernel<KS, MT, 2, 0>;
+  }
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
     switch (epi) {
       case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_kernel<KS, MT, 1, 0>;
@@ -804,7 +993,9 @@ FwdKernel fwd_instance(int pro, int epi) {
     case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_kernel<KS, MT, 0, 0>;
     case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_kernel<KS, MT, 0, 1>;
     case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_kernel<KS, MT, 0, 2>;
-    default: return pw_fwd_kernel<KS, MT, 0, 3>;
+    case MEDNEXT_PW_EPILOGUE_GELU_GRAD: return pw_fwd_kernel<KS, MT, 0, 3>;
+    case MEDNEXT_PW_EPILOGUE_ROW_REDUCE: return pw_fwd_kernel<KS, MT, 0, 4>;
+    default: return pw_fwd_kernel<KS, MT, 0, 5>;
   }
 }
 
@@ -814,7 +1005,7 @@ FwdKernel fwd_instance(int pro, int epi) {
 // per SIMD), one when the weight block would not fit the LDS budget.
 int pick_mt(int64_t k, int64_t m, int epi) {
   const int64_t ks = cdiv(k, 32);
-  const bool aux = epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epi == MEDNEXT_PW_EPILOGUE_GELU_GRAD;
+  const bool aux = epi_has_aux(epi);
   auto fits = [&](int mt) { return static_cast<size_t>(16 * mt) * ks * 32 * 2 <= kMaxWeightLds; };
   if (ks >= kSplitKSlices) return m > 16 && fits(2) ? 2 : 1;
   if (!aux && ks == 1 && m > 32 && fits(4)) return 4;
@@ -840,6 +1031,7 @@ using WgradKernel = void (*)(const bf16_t*, const bf16_t*, float*, PwWGeom);
 
 template <int TM, int TK>
 WgradKernel wgrad_instance(int pro) {
+  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) return pw_wgrad_kernel<TM, TK, 2>;
   return pro == MEDNEXT_PW_PROLOGUE_GELU ? pw_wgrad_kernel<TM, TK, 1> : pw_wgrad_kernel<TM, TK, 0>;
 }
 
@@ -866,47 +1058,98 @@ WgradKernel pick_wgrad(int tm, int tk, int pro) {
 
 using namespace mednext;
 
-extern "C" int32_t mednext_pointwise_fwd(const void* x, const void* weight, const void* bias, const void* aux,
-                                         void* y, int64_t n, int64_t k, int64_t m, int64_t v,
-                                         int32_t weight_layout, int32_t prologue, int32_t epilogue,
-                                         int32_t dtype, int32_t blocks_per_sample, void* stream) {
-  if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
-  MEDNEXT_CHECK_ARG(x != nullptr && weight != nullptr && y != nullptr, "null tensor pointer");
-  MEDNEXT_CHECK_ARG(k <= kMaxK, "input channels above 2048 are not supported by the matrix-core GEMM");
-  MEDNEXT_CHECK_ARG(weight_layout == 0 || weight_layout == 1, "weight_layout must be 0 ([M][K]) or 1 ([K][M])");
-  MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU, "bad prologue");
-  MEDNEXT_CHECK_ARG(epilogue >= MEDNEXT_PW_EPILOGUE_BIAS && epilogue <= MEDNEXT_PW_EPILOGUE_GELU_GRAD, "bad epilogue");
-  const bool needs_aux = epilogue == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epilogue == MEDNEXT_PW_EPILOGUE_GELU_GRAD;
-  MEDNEXT_CHECK_ARG(!needs_aux || aux != nullptr, "this epilogue needs the aux tensor");
-  MEDNEXT_CHECK_ARG(aligned(x, 2) && aligned(y, 2) && (aux == nullptr || aligned(aux, 2)) && aligned(weight, 16) &&
-                        (bias == nullptr || aligned(bias, 2)),
-                    "pointwise tensors must be bf16-aligned and the weight 16-byte aligned");
-  MEDNEXT_CHECK_ARG(blocks_per_sample >= 0, "blocks_per_sample must be >= 0 (0 = automatic)");
-  const int mt = pick_mt(k, m, epilogue);
+namespace {
+
+// Launch shape of one forward / transposed product (shared by the launch and
+// the ROW_REDUCE slot query).
+struct FwdPlan {
   PwGeom g;
+  int mt;
+  bool splitk;
+  int64_t blocks;
+  int slots;  // ROW_REDUCE slots per (sample, row)
+};
+
+FwdPlan plan_fwd(int64_t n, int64_t k, int64_t m, int64_t v, int epi, int32_t blocks_per_sample) {
+  FwdPlan p;
+  p.mt = pick_mt(k, m, epi);
+  PwGeom& g = p.g;
   g.K = static_cast<int>(k);
   g.M = static_cast<int>(m);
   g.ks = static_cast<int>(cdiv(k, 32));
   g.V = static_cast<uint32_t>(v);
   g.chunks = static_cast<int>(cdiv(v, kChunk));
-  g.mgroups = static_cast<int>(cdiv(m, 16 * mt));
-  g.wt = weight_layout;
-  const bool splitk = g.ks >= kSplitKSlices;
+  g.mgroups = static_cast<int>(cdiv(m, 16 * p.mt));
+  g.wt = 0;
+  p.splitk = g.ks >= kSplitKSlices;
   const int64_t groups = n * g.mgroups;
   // Every wave (split-K: every workgroup) gets at least one chunk.
-  const int64_t most = splitk ? g.chunks : cdiv(g.chunks, 4);
+  const int64_t most = p.splitk ? g.chunks : cdiv(g.chunks, 4);
   const int64_t wanted = blocks_per_sample > 0 ? blocks_per_sample : cdiv(kResidentWgs, groups);
   g.wgs = static_cast<int>(std::max<int64_t>(1, std::min(wanted, most)));
-  const int64_t blocks = groups * g.wgs;
-  MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
-  const size_t lds = static_cast<size_t>(16 * mt) * g.ks * 32 * 2 + 16 * mt * sizeof(float) +
-                     (splitk ? static_cast<size_t>(mt) * 8 * 4 * 64 * sizeof(float) : 0);
-  hipLaunchKernelGGL(pick_fwd(k, mt, prologue, epilogue), dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds,
-                     static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(x),
+  p.blocks = groups * g.wgs;
+  p.slots = p.splitk ? g.wgs : 4 * g.wgs;
+  return p;
+}
+
+}  // namespace
+
+extern "C" int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, int64_t v,
+                                               int32_t blocks_per_sample) {
+  if (n < 1 || k < 1 || k > kMaxK || m < 1 || v < 1 || blocks_per_sample < 0) return 0;
+  return plan_fwd(n, k, m, v, MEDNEXT_PW_EPILOGUE_ROW_REDUCE, blocks_per_sample).slots;
+}
+
+extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* bias, const void* aux,
+                                            void* y, int64_t n, int64_t k, int64_t m, int64_t v,
+                                            int32_t weight_layout, int32_t prologue, int32_t epilogue,
+                                            const void* prologue_coef, const void* epilogue_coef,
+                                            void* row_partial, int32_t dtype, int32_t blocks_per_sample,
+                                            void* stream) {
+  if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
+  const bool reduce = epilogue == MEDNEXT_PW_EPILOGUE_ROW_REDUCE;
+  MEDNEXT_CHECK_ARG(x != nullptr && weight != nullptr && (y != nullptr || reduce), "null tensor pointer");
+  MEDNEXT_CHECK_ARG(k <= kMaxK, "input channels above 2048 are not supported by the matrix-core GEMM");
+  MEDNEXT_CHECK_ARG(weight_layout == 0 || weight_layout == 1, "weight_layout must be 0 ([M][K]) or 1 ([K][M])");
+  MEDNEXT_CHECK_ARG(pro_epi_supported(prologue, epilogue), "unsupported prologue / epilogue combination");
+  MEDNEXT_CHECK_ARG(!epi_has_aux(epilogue) || aux != nullptr, "this epilogue needs the aux tensor");
+  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_GELU_AFFINE || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
+                    "the GELU_AFFINE prologue needs 8-byte aligned coefficient records");
+  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_GELU_AFFINE || weight_layout == 0,
+                    "the GELU_AFFINE prologue takes a [M][K] weight");
+  MEDNEXT_CHECK_ARG(epilogue != MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD ||
+                        (epilogue_coef != nullptr && aligned(epilogue_coef, 8)),
+                    "the AFFINE_GELU_GRAD epilogue needs 8-byte aligned coefficients");
+  MEDNEXT_CHECK_ARG(!reduce || (row_partial != nullptr && aligned(row_partial, 8)),
+                    "the ROW_REDUCE epilogue needs an 8-byte aligned row_partial buffer");
+  MEDNEXT_CHECK_ARG(aligned(x, 2) && (y == nullptr || aligned(y, 2)) && (aux == nullptr || aligned(aux, 2)) &&
+                        aligned(weight, 16) && (bias == nullptr || aligned(bias, 2)),
+                    "pointwise tensors must be bf16-aligned and the weight 16-byte aligned");
+  MEDNEXT_CHECK_ARG(blocks_per_sample >= 0, "blocks_per_sample must be >= 0 (0 = automatic)");
+  FwdPlan p = plan_fwd(n, k, m, v, epilogue, blocks_per_sample);
+  p.g.wt = weight_layout;
+  MEDNEXT_CHECK_ARG(p.blocks < (int64_t{1} << 31), "grid too large");
+  const int mt = p.mt;
+  const size_t lds = static_cast<size_t>(16 * mt) * p.g.ks * 32 * 2 + kRowVecs * 16 * mt * sizeof(float) +
+                     (p.splitk ? static_cast<size_t>(mt) * 8 * 4 * 64 * sizeof(float) : 0);
+  PwExtra ex{static_cast<const double*>(prologue_coef), static_cast<const double*>(epilogue_coef),
+             static_cast<double*>(row_partial), p.slots};
+  hipLaunchKernelGGL(pick_fwd(k, mt, prologue, epilogue), dim3(static_cast<unsigned>(p.blocks)), dim3(kPwThreads),
+                     lds, static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(x),
                      static_cast<const bf16_t*>(weight), static_cast<const bf16_t*>(bias),
-                     static_cast<const bf16_t*>(aux), static_cast<bf16_t*>(y), g);
+                     static_cast<const bf16_t*>(aux), static_cast<bf16_t*>(y), p.g, ex);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
+}
+
+extern "C" int32_t mednext_pointwise_fwd(const void* x, const void* weight, const void* bias, const void* aux,
+                                         void* y, int64_t n, int64_t k, int64_t m, int64_t v,
+                                         int32_t weight_layout, int32_t prologue, int32_t epilogue,
+                                         int32_t dtype, int32_t blocks_per_sample, void* stream) {
+  MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU, "bad prologue");
+  MEDNEXT_CHECK_ARG(epilogue >= MEDNEXT_PW_EPILOGUE_BIAS && epilogue <= MEDNEXT_PW_EPILOGUE_GELU_GRAD, "bad epilogue");
+  return mednext_pointwise_fwd_ex(x, weight, bias, aux, y, n, k, m, v, weight_layout, prologue, epilogue, nullptr,
+                                  nullptr, nullptr, dtype, blocks_per_sample, stream);
 }
 
 namespace {
@@ -932,13 +1175,18 @@ extern "C" size_t mednext_pointwise_wgrad_workspace_bytes(int64_t n, int64_t k, 
   return wgrad_partial_bytes(n, k, m, v, splits) + static_cast<size_t>(kFinRanges) * (m * k + m) * sizeof(double);
 }
 
-extern "C" int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* grad_weight,
-                                           void* grad_bias, void* workspace, size_t workspace_bytes,
-                                           int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
-                                           int32_t dtype, int32_t splits, void* stream) {
+extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const void* x, void* grad_weight,
+                                              void* grad_bias, void* workspace, size_t workspace_bytes,
+                                              int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
+                                              const void* prologue_coef, int32_t dtype, int32_t splits,
+                                              void* stream) {
   if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
   MEDNEXT_CHECK_ARG(grad_output != nullptr && x != nullptr && grad_weight != nullptr, "null tensor pointer");
-  MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU, "bad prologue");
+  MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU ||
+                        prologue == MEDNEXT_PW_PROLOGUE_GELU_AFFINE,
+                    "bad prologue");
+  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_GELU_AFFINE || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
+                    "the GELU_AFFINE prologue needs 8-byte aligned coefficient records");
   MEDNEXT_CHECK_ARG(splits >= 1 && splits <= 65535, "splits must be in [1, 65535]");
   MEDNEXT_CHECK_ARG(aligned(grad_output, 2) && aligned(x, 2) && aligned(grad_weight, 2) &&
                         (grad_bias == nullptr || aligned(grad_bias, 2)),
@@ -956,6 +1204,7 @@ extern "C" int32_t mednext_pointwise_wgrad(const void* grad_output, const void* 
   g.mblocks = static_cast<int>(cdiv(m, 16 * tm));
   g.kblocks = static_cast<int>(cdiv(k, 16 * tk));
   g.stride = m * k + m;
+  g.pcoef = static_cast<const double*>(prologue_coef);
   const int64_t blocks = n * g.splits * g.mblocks * static_cast<int64_t>(g.kblocks);
   MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
   const auto s = static_cast<hipStream_t>(stream);
@@ -975,4 +1224,13 @@ extern "C" int32_t mednext_pointwise_wgrad(const void* grad_output, const void* 
                      static_cast<bf16_t*>(grad_weight), static_cast<bf16_t*>(grad_bias), m * k, m, ranges);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
+}
+
+extern "C" int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* grad_weight,
+                                           void* grad_bias, void* workspace, size_t workspace_bytes,
+                                           int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
+                                           int32_t dtype, int32_t splits, void* stream) {
+  MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU, "bad prologue");
+  return mednext_pointwise_wgrad_ex(grad_output, x, grad_weight, grad_bias, workspace, workspace_bytes, n, k, m, v,
+                                    prologue, nullptr, dtype, splits, stream);
 }

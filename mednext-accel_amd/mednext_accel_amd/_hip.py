@@ -59,7 +59,16 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
     ),
+    "mednext_pointwise_fwd_ex": (
+        _i32,
+        (_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p),
+    ),
+    "mednext_pointwise_row_slots": (_i64, (_i64, _i64, _i64, _i64, _i32)),
     "mednext_pointwise_wgrad_workspace_bytes": (c_size_t, (_i64, _i64, _i64, _i64, _i32)),
+    "mednext_pointwise_wgrad_ex": (
+        _i32,
+        (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i32, _p, _i32, _i32, _p),
+    ),
     "mednext_pointwise_wgrad": (
         _i32,
         (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p),
@@ -73,6 +82,14 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _i32, _p, _i32, _p, _p, _i32, _p, _p, _p, _i64, _i64, _i64, c_double, _i32, _p, c_size_t, _p),
     ),
+    "mednext_grn_stats": (
+        _i32,
+        (_p, _i32, _i32, _p, _p, _i32, _p, _i64, _i64, _i64, c_double, _i32, _p, c_size_t, _p),
+    ),
+    "mednext_grn_bwd_rows": (
+        _i32,
+        (_p, _i64, _p, _p, _i32, _p, _p, _p, _i64, _i64, c_double, _p, c_size_t, _p),
+    ),
     "mednext_depthwise3d_s2_gather": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
     "mednext_depthwise3d_s2_scatter": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
     "mednext_depthwise3d_s2_wgrad_workspace_bytes": (c_size_t, (*(_i64,) * 8, _i32, _i32)),
@@ -82,7 +99,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

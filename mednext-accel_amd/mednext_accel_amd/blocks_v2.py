@@ -49,7 +49,22 @@ class MedNeXtV2Block(nn.Module):
         return self.project(self.grn(self.activation(self.expand(h))))
 
     def forward(self, x: Tensor) -> Tensor:
-        h = self.norm(self.depthwise(x))
+        # A fused expansion (attached by the model's optimization setup; a plain
+        # attribute, not a submodule) replaces expand -> GELU -> GRN -> project
+        # and the residual add with matrix-core kernels when it applies.
+        fused = self.__dict__.get("fused_expansion")
+        if fused is not None and fused.applies(x):
+            d = self.depthwise(x)
+            if fused.supports(d):
+                h = self.norm(d, out_dtype=torch.bfloat16)
+                residual = x if self.use_residual else None
+                if self.checkpoint_expansion and self.training and torch.is_grad_enabled():
+                    return checkpoint(fused, h, residual, use_reentrant=False)
+                return fused(h, residual)
+            return self._finish(self.norm(d), x)
+        return self._finish(self.norm(self.depthwise(x)), x)
+
+    def _finish(self, h: Tensor, x: Tensor) -> Tensor:
         if self.checkpoint_expansion and self.training and torch.is_grad_enabled():
             h = checkpoint(self._expansion_forward, h, use_reentrant=False)
         else:

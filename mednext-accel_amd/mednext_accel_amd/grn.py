@@ -110,6 +110,95 @@ class AdaptiveGlobalResponseNorm3d(nn.Module):
         return f"{self.gamma.shape[1]}, eps={self.eps}"
 
 
+class AdaptiveGRNExpansion:
+    """Fused ``project(GRN(GELU(expand(h)))) [+ residual]`` of one MedNeXt v2
+    block (``hip_ops.grn_expansion``).
+
+    Like the v1 block's fused expansion it is a plain attribute of the block,
+    not a submodule: it reads the block's own ``expand`` / ``grn`` /
+    ``project`` Parameters at call time, so installing it changes neither
+    ``parameters()`` nor the state-dict keys. ``MedNeXtV2Block.forward``
+    consults it; when ``applies`` or ``supports`` is false the block runs its
+    modules as without it.
+    """
+
+    #: Widest hidden layer the fused path takes: the project GEMM recomputes
+    #: GELU and the GRN affine per 32-row output group, which pays while the
+    #: hidden tensor's HBM passes it saves dominate (MI355X, MedNeXt v2 Base).
+    max_hidden = 512
+
+    def __init__(self, block: nn.Module, resolver: PolicyResolver, model_context: ModelOptimizationContext,
+                 *, role: str | None = None) -> None:
+        self.block = block
+        self.resolver = resolver
+        self.model_context = model_context
+        self.descriptor = OperatorDescriptor(
+            "grn_expansion3d", "regular", block.expand.in_channels, block.project.out_channels, role=role
+        )
+
+    def applies(self, x: Tensor) -> bool:
+        """Training with grad, bf16 autocast on a GPU and the policy selecting
+        the fused kernels (decided from the block input)."""
+        b = self.block
+        if not (b.training and torch.is_grad_enabled() and x.is_cuda and x.ndim == 5):
+            return False
+        context = _context_from_tensor(x, self.model_context, training=True)
+        if context.dtype != "bfloat16":
+            return False
+        return self.resolver.resolve(self.descriptor, context, "training").implementation == "hip_fused_grn_expansion"
+
+    def supports(self, h: Tensor) -> bool:
+        """Shape check on the expansion's input (the depthwise output)."""
+        from .tiles import pointwise_supported
+
+        b = self.block
+        hidden = b.expand.out_channels
+        v = int(h.shape[2] * h.shape[3] * h.shape[4])
+        return (
+            h.is_contiguous()
+            and hidden <= self.max_hidden
+            and pointwise_supported(b.expand.in_channels, hidden, v)
+            and pointwise_supported(hidden, b.project.out_channels, v)
+        )
+
+    def __call__(self, h: Tensor, residual: Tensor | None) -> Tensor:
+        b = self.block
+        dt = torch.bfloat16
+        w1, w2 = b.expand.weight.to(dt), b.project.weight.to(dt)
+        b1 = b.expand.bias.to(dt) if b.expand.bias is not None else None
+        b2 = b.project.bias.to(dt) if b.project.bias is not None else None
+        fuse_residual = residual is not None and residual.dtype == dt and residual.is_contiguous()
+        out, _u, _coef = _hip_ops().grn_expansion(
+            h.to(dt), w1, b1, w2, b2, b.grn.gamma, b.grn.beta, residual if fuse_residual else None, float(b.grn.eps)
+        )
+        if residual is not None and not fuse_residual:
+            out = out + residual
+        return out
+
+
+def install_fused_grn_expansions(
+    model: nn.Module,
+    *,
+    resolver: PolicyResolver,
+    model_context: ModelOptimizationContext,
+) -> int:
+    """Attach an ``AdaptiveGRNExpansion`` to every MedNeXt v2 block whose
+    GroupNorm and GRN were wrapped; returns how many were attached."""
+    from .adaptive import AdaptiveGroupNorm3d
+    from .blocks_v2 import MedNeXtV2Block
+
+    count = 0
+    for role, module in model.named_modules():
+        if (
+            isinstance(module, MedNeXtV2Block)
+            and isinstance(module.norm, AdaptiveGroupNorm3d)
+            and isinstance(module.grn, AdaptiveGlobalResponseNorm3d)
+        ):
+            module.__dict__["fused_expansion"] = AdaptiveGRNExpansion(module, resolver, model_context, role=role or None)
+            count += 1
+    return count
+
+
 def install_adaptive_grn(
     model: nn.Module,
     *,

@@ -275,8 +275,9 @@ def group_norm_backward(
 
 # --------------------------------------------------------------------- pointwise
 
-PW_PROLOGUE_NONE, PW_PROLOGUE_GELU = 0, 1
+PW_PROLOGUE_NONE, PW_PROLOGUE_GELU, PW_PROLOGUE_GELU_AFFINE = 0, 1, 2
 PW_EPILOGUE_BIAS, PW_EPILOGUE_BIAS_GELU, PW_EPILOGUE_BIAS_RESIDUAL, PW_EPILOGUE_GELU_GRAD = 0, 1, 2, 3
+PW_EPILOGUE_ROW_REDUCE, PW_EPILOGUE_AFFINE_GELU_GRAD = 4, 5
 
 
 def _weight2d(weight: Tensor) -> Tensor:
@@ -304,12 +305,19 @@ def pointwise_conv(
     epilogue: int = PW_EPILOGUE_BIAS,
     transpose: bool = False,
     blocks: int | None = None,
-) -> Tensor:
+    prologue_coef: Tensor | None = None,
+    epilogue_coef: Tensor | None = None,
+    row_partial: Tensor | None = None,
+) -> Tensor | None:
     """``y = epilogue(W . prologue(x) [+ b])`` per sample on the matrix cores.
 
     ``weight`` is the conv's [Cout, Cin(, 1, 1, 1)]; with ``transpose=True`` the
     product is ``W^T . x`` (the conv's input gradient). ``aux`` is the residual
-    (BIAS_RESIDUAL) or the GELU pre-activation (GELU_GRAD), shaped like ``y``.
+    (BIAS_RESIDUAL) or the GELU pre-activation (GELU_GRAD, ROW_REDUCE,
+    AFFINE_GELU_GRAD), shaped like ``y``. ``prologue_coef`` ([N, K, 4] float64)
+    feeds GELU_AFFINE, ``epilogue_coef`` ([N, M, 2] float64) AFFINE_GELU_GRAD;
+    ROW_REDUCE writes ``row_partial`` ([N, M, slots, 2] float64, slots from
+    ``pointwise_row_slots``) and returns None.
     """
     _check_device(x, weight)
     _check_pointwise_tensor(x, "x")
@@ -321,27 +329,45 @@ def pointwise_conv(
     if x.shape[1] != k:
         raise ValueError(f"x has {x.shape[1]} channels, the weight expects {k}")
     n, v = x.shape[0], x[0, 0].numel()
-    y = x.new_empty((n, m, *x.shape[2:]))
+    out_shape = (n, m, *x.shape[2:])
+    y = None if epilogue == PW_EPILOGUE_ROW_REDUCE else x.new_empty(out_shape)
     if bias is not None:
         if bias.shape != (m,) or bias.dtype != torch.bfloat16:
             raise ValueError("bias must be a bfloat16 [Cout] tensor")
         bias = bias.contiguous()
     if aux is not None:
         _check_pointwise_tensor(aux, "aux")
-        if aux.shape != y.shape:
+        if tuple(aux.shape) != out_shape:
             raise ValueError("aux must have the output's shape")
     if blocks is None:
         blocks = pointwise_blocks(n, k, m, v)
+    if epilogue == PW_EPILOGUE_ROW_REDUCE:
+        slots = pointwise_row_slots(n, k, m, v, int(blocks))
+        if row_partial is None or row_partial.dtype != torch.float64 or row_partial.numel() != n * m * slots * 2:
+            raise ValueError("ROW_REDUCE needs a float64 row_partial of N * M * slots * 2 values")
+    for t, rows, name in ((prologue_coef, k * 4, "prologue_coef"), (epilogue_coef, m * 2, "epilogue_coef")):
+        if t is not None and (t.dtype != torch.float64 or not t.is_contiguous() or t.numel() != n * rows):
+            raise ValueError(f"{name} must be a contiguous float64 tensor of {n * rows} values")
     lib = _hip.load()
     _hip.check(
-        lib.mednext_pointwise_fwd(
-            x.data_ptr(), w2.data_ptr(), _hip.ptr(bias), _hip.ptr(aux), y.data_ptr(),
-            n, k, m, v, 1 if transpose else 0, prologue, epilogue, _hip.DTYPE_CODES[torch.bfloat16],
+        lib.mednext_pointwise_fwd_ex(
+            x.data_ptr(), w2.data_ptr(), _hip.ptr(bias), _hip.ptr(aux), _hip.ptr(y),
+            n, k, m, v, 1 if transpose else 0, prologue, epilogue, _hip.ptr(prologue_coef),
+            _hip.ptr(epilogue_coef), _hip.ptr(row_partial), _hip.DTYPE_CODES[torch.bfloat16],
             int(blocks), _hip.stream_of(x),
         ),
-        "mednext_pointwise_fwd",
+        "mednext_pointwise_fwd_ex",
     )
     return y
+
+
+@functools.lru_cache(maxsize=4096)
+def pointwise_row_slots(n: int, k: int, m: int, v: int, blocks: int = 0) -> int:
+    """Row-sum slots per (sample, row) of a ROW_REDUCE launch of this shape."""
+    slots = int(_hip.load().mednext_pointwise_row_slots(n, k, m, v, blocks))
+    if slots < 1:
+        raise ValueError("unsupported ROW_REDUCE shape")
+    return slots
 
 
 def pointwise_weight_grad(
@@ -351,8 +377,10 @@ def pointwise_weight_grad(
     prologue: int = PW_PROLOGUE_NONE,
     with_bias: bool = True,
     splits: int | None = None,
+    prologue_coef: Tensor | None = None,
 ) -> tuple[Tensor, Tensor | None]:
-    """(dW [Cout, Cin, 1, 1, 1], dB [Cout] or None) of ``y = W . prologue(x) + b``."""
+    """(dW [Cout, Cin, 1, 1, 1], dB [Cout] or None) of ``y = W . prologue(x) + b``
+    (``prologue_coef`` as for ``pointwise_conv``'s GELU_AFFINE)."""
     _check_device(grad_output, x)
     _check_pointwise_tensor(grad_output, "grad_output")
     _check_pointwise_tensor(x, "x")
@@ -366,12 +394,17 @@ def pointwise_weight_grad(
     ws = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
     dw = x.new_empty((m, k, 1, 1, 1))
     db = x.new_empty((m,)) if with_bias else None
+    if prologue_coef is not None and (
+        prologue_coef.dtype != torch.float64 or not prologue_coef.is_contiguous() or prologue_coef.numel() != n * k * 4
+    ):
+        raise ValueError(f"prologue_coef must be a contiguous float64 tensor of {n * k * 4} values")
     _hip.check(
-        lib.mednext_pointwise_wgrad(
+        lib.mednext_pointwise_wgrad_ex(
             grad_output.data_ptr(), x.data_ptr(), dw.data_ptr(), _hip.ptr(db), ws.data_ptr(), nbytes,
-            n, k, m, v, prologue, _hip.DTYPE_CODES[torch.bfloat16], int(splits), _hip.stream_of(x),
+            n, k, m, v, prologue, _hip.ptr(prologue_coef), _hip.DTYPE_CODES[torch.bfloat16], int(splits),
+            _hip.stream_of(x),
         ),
-        "mednext_pointwise_wgrad",
+        "mednext_pointwise_wgrad_ex",
     )
     return dw, db
 
@@ -1072,3 +1105,180 @@ def fused_global_response_norm3d(x: Tensor, gamma: Tensor, beta: Tensor, eps: fl
     if not math.isfinite(eps) or eps <= 0:
         raise ValueError("fused GRN requires eps to be finite and positive")
     return grn_forward_op(x, gamma, beta, float(eps))[0]
+
+
+def grn_stats(
+    x: Tensor, gamma: Tensor | None, beta: Tensor | None, eps: float = 1e-6, *, gelu_input: bool = False,
+    splits: int | None = None,
+) -> Tensor:
+    """GRN coefficients [N, C, 4] float64 = (1 + gamma r, beta, r, ||y_c||) of
+    y = x, or of y = bf16(GELU(x)) with ``gelu_input`` (bf16 x): the forward's
+    statistics without its output tensor."""
+    _check_device(x)
+    if x.ndim != 5 or not x.is_contiguous() or x.numel() == 0:
+        raise ValueError("a nonempty contiguous NCDHW input is required")
+    n, c = int(x.shape[0]), int(x.shape[1])
+    v = x.numel() // (n * c)
+    params = [p for p in (gamma, beta) if p is not None]
+    pdtype = params[0].dtype if params else torch.float32
+    for p in params:
+        if p.numel() != c or p.dtype != pdtype or not p.is_cuda or not p.is_contiguous():
+            raise ValueError("gamma / beta must be contiguous CUDA tensors of C values and one dtype")
+    coef = torch.empty((n, c, 4), device=x.device, dtype=torch.float64)
+    splits = group_norm_splits(n, c, v) if splits is None else int(splits)
+    lib = _hip.load()
+    nbytes = lib.mednext_grn_workspace_bytes(n, c, v, splits)
+    workspace = torch.empty((max(8, nbytes),), device=x.device, dtype=torch.uint8)
+    _hip.check(
+        lib.mednext_grn_stats(
+            x.data_ptr(), _hip.dtype_code(x.dtype), 1 if gelu_input else 0, _hip.ptr(gamma), _hip.ptr(beta),
+            _hip.dtype_code(pdtype), coef.data_ptr(), n, c, v, float(eps), splits, workspace.data_ptr(), nbytes,
+            _hip.stream_of(x),
+        ),
+        "mednext_grn_stats",
+    )
+    return coef
+
+
+def grn_backward_from_rows(
+    row_partial: Tensor, coef: Tensor, gamma: Tensor, eps: float = 1e-6
+) -> tuple[Tensor, Tensor, Tensor]:
+    """GRN backward coefficients [N, C, 2] float64 (dy multiplier, y_in
+    multiplier) and (dgamma, dbeta) shaped like gamma, from the row sums
+    (sum dz * y_in, sum dz) a ROW_REDUCE GEMM epilogue wrote."""
+    _check_device(row_partial, coef, gamma)
+    n, c = int(coef.shape[0]), int(coef.shape[1])
+    if row_partial.dtype != torch.float64 or row_partial.numel() % (n * c * 2):
+        raise ValueError("row_partial must be float64 [N, C, slots, 2]")
+    slots = row_partial.numel() // (n * c * 2)
+    out = torch.empty((n, c, 2), device=coef.device, dtype=torch.float64)
+    dgamma = torch.empty_like(gamma)
+    dbeta = torch.empty_like(gamma)
+    workspace = torch.empty((n * c * 4,), device=coef.device, dtype=torch.float64)
+    _hip.check(
+        _hip.load().mednext_grn_bwd_rows(
+            row_partial.data_ptr(), slots, coef.data_ptr(), gamma.data_ptr(), _hip.dtype_code(gamma.dtype),
+            out.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), n, c, float(eps), workspace.data_ptr(),
+            workspace.numel() * 8, _hip.stream_of(coef),
+        ),
+        "mednext_grn_bwd_rows",
+    )
+    return out, dgamma, dbeta
+
+
+# --------------------------------------------------- MedNeXt v2 fused expansion
+
+
+@torch.library.custom_op("mednext_accel_amd::grn_expansion", mutates_args=())
+def grn_expansion(
+    x: Tensor,
+    w1: Tensor,
+    b1: Tensor | None,
+    w2: Tensor,
+    b2: Tensor | None,
+    gamma: Tensor,
+    beta: Tensor,
+    residual: Tensor | None,
+    eps: float,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """MedNeXt v2 block expansion, fused: ``out = W2 . GRN(GELU(W1 . x + b1)) +
+    b2 (+ residual)`` (reference models/blocks_v2.py:44-45 with the GRN of
+    ops/grn.py:16-30 and the residual add of :48-55).
+
+    Returns ``(out, u, coef)``: ``u = W1 . x + b1`` (bf16) is the only hidden
+    tensor written; the GRN statistics of bf16(GELU(u)) come from one read of
+    it, and the project GEMM applies GELU and the GRN affine to u as it loads
+    it. ``coef`` [N, hidden, 4] float64 holds (1 + gamma r, beta, r, norm)."""
+    x = x.contiguous()
+    u = pointwise_conv(x, w1, b1, epilogue=PW_EPILOGUE_BIAS)
+    coef = grn_stats(u, gamma, beta, eps, gelu_input=True)
+    if residual is None:
+        out = pointwise_conv(u, w2, b2, prologue=PW_PROLOGUE_GELU_AFFINE, epilogue=PW_EPILOGUE_BIAS,
+                             prologue_coef=coef)
+    else:
+        out = pointwise_conv(u, w2, b2, aux=residual.contiguous(), prologue=PW_PROLOGUE_GELU_AFFINE,
+                             epilogue=PW_EPILOGUE_BIAS_RESIDUAL, prologue_coef=coef)
+    return out, u, coef
+
+
+@grn_expansion.register_fake
+def _(x, w1, b1, w2, b2, gamma, beta, residual, eps):
+    shape = (x.shape[0], w1.shape[0], *x.shape[2:])
+    return (
+        x.new_empty((x.shape[0], w2.shape[0], *x.shape[2:])),
+        x.new_empty(shape),
+        x.new_empty((x.shape[0], w1.shape[0], 4), dtype=torch.float64),
+    )
+
+
+@torch.library.custom_op("mednext_accel_amd::grn_expansion_backward", mutates_args=())
+def grn_expansion_backward(
+    grad_out: Tensor, x: Tensor, u: Tensor, coef: Tensor, w1: Tensor, w2: Tensor, gamma: Tensor, eps: float
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dx, dW1, db1, dW2, db2, dgamma, dbeta) of ``grn_expansion``. With
+    a = bf16(GELU(u)), z = GRN(a) and dz = W2^T . dout (never stored):
+    one transposed GEMM reduces the GRN row sums (sum dz * a, sum dz), a small
+    kernel turns them into the per-(n, c) GRN backward coefficients and the
+    gamma / beta gradients, a second transposed GEMM writes
+    du = (dz k1 + a k2) * GELU'(u); dW2 = dout . z^T reads u through the
+    GELU + GRN prologue; dW1 = du . x^T and dx = W1^T . du as for any conv."""
+    grad_out = grad_out.contiguous()
+    n, hidden = int(u.shape[0]), int(u.shape[1])
+    v = u[0, 0].numel()
+    cout = int(grad_out.shape[1])
+    blocks = pointwise_blocks(n, cout, hidden, v)
+    slots = pointwise_row_slots(n, cout, hidden, v, int(blocks))
+    rows = torch.empty((n, hidden, slots, 2), device=u.device, dtype=torch.float64)
+    pointwise_conv(grad_out, w2, aux=u, epilogue=PW_EPILOGUE_ROW_REDUCE, transpose=True, blocks=blocks,
+                   row_partial=rows)
+    bcoef, dgamma, dbeta = grn_backward_from_rows(rows, coef, gamma, eps)
+    du = pointwise_conv(grad_out, w2, aux=u, epilogue=PW_EPILOGUE_AFFINE_GELU_GRAD, transpose=True,
+                        epilogue_coef=bcoef)
+    dw2, db2 = pointwise_weight_grad(grad_out, u, prologue=PW_PROLOGUE_GELU_AFFINE, prologue_coef=coef)
+    dw1, db1 = pointwise_weight_grad(du, x.contiguous())
+    dx = pointwise_conv(du, w1, transpose=True)
+    return dx, dw1, db1, dw2, db2, dgamma, dbeta
+
+
+@grn_expansion_backward.register_fake
+def _(grad_out, x, u, coef, w1, w2, gamma, eps):
+    return (
+        torch.empty_like(x),
+        w1.new_empty(w1.shape),
+        w1.new_empty((w1.shape[0],)),
+        w2.new_empty(w2.shape),
+        w2.new_empty((w2.shape[0],)),
+        torch.empty_like(gamma),
+        torch.empty_like(gamma),
+    )
+
+
+def _setup_grn_expansion(ctx, inputs, output):
+    x, w1, b1, w2, b2, gamma, beta, residual, eps = inputs
+    _out, u, coef = output
+    ctx.mark_non_differentiable(u, coef)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(x, u, coef, w1, w2, gamma)
+    ctx.eps = eps
+    ctx.has_b1, ctx.has_b2, ctx.has_residual = b1 is not None, b2 is not None, residual is not None
+
+
+def _grn_expansion_backward(ctx, grad_out, _grad_u, _grad_coef):
+    if grad_out is None:
+        return (None,) * 9
+    x, u, coef, w1, w2, gamma = ctx.saved_tensors
+    dx, dw1, db1, dw2, db2, dgamma, dbeta = grn_expansion_backward(grad_out, x, u, coef, w1, w2, gamma, ctx.eps)
+    return (
+        dx,
+        dw1,
+        db1 if ctx.has_b1 else None,
+        dw2,
+        db2 if ctx.has_b2 else None,
+        dgamma,
+        dbeta,
+        grad_out if ctx.has_residual else None,
+        None,
+    )
+
+
+grn_expansion.register_autograd(_grn_expansion_backward, setup_context=_setup_grn_expansion)

@@ -41,7 +41,12 @@ from .blocks import OutputHead
 from .blocks_v2 import MedNeXtV2Block, MedNeXtV2DownBlock, MedNeXtV2UpBlock
 from .checkpointing import CheckpointConfig
 from .config_v2 import MedNeXtV2Config, get_mednext_v2_config
-from .grn import AdaptiveGlobalResponseNorm3d, GlobalResponseNorm3d, install_adaptive_grn
+from .grn import (
+    AdaptiveGlobalResponseNorm3d,
+    GlobalResponseNorm3d,
+    install_adaptive_grn,
+    install_fused_grn_expansions,
+)
 from .mednext_v1 import DeepSupervisionOutput, OptimizationSource, checkpoint_name, spatial_shape_for_role
 from .optimization.descriptors import OperatorDescriptor
 from .optimization.policies import PolicyRegistry
@@ -253,6 +258,7 @@ def configure_optimization(model: MedNeXtV2, optimization: OptimizationSource) -
     model_context = ModelOptimizationContext("mednext_v2", model.config.variant, checkpoint_name(model.checkpointing))
     install_adaptive_operators(model, resolver=resolver, model_context=model_context)
     install_adaptive_grn(model, resolver=resolver, model_context=model_context)
+    install_fused_grn_expansions(model, resolver=resolver, model_context=model_context)
     model.__dict__["_optimization_resolver"] = resolver
     model.__dict__["_optimization_model_context"] = model_context
     return model

@@ -242,6 +242,7 @@ def default_implementation_registry(*, triton_available: bool | None = None) -> 
         ("hip_pointwise_gemm", ("pointwise_conv3d", "conv_transpose3d"), ("training",), "numerical", False, _hip_pointwise, (*_TENSOR_GUARDS, "channels_supported")),
         ("hip_fused_expansion", ("mlp_expansion3d",), ("training",), "numerical", False, _hip_expansion, (*_TENSOR_GUARDS, "channels_supported")),
         ("hip_fused_grn", ("global_response_norm3d",), ("training",), "numerical", False, _hip_grn, _TENSOR_GUARDS),
+        ("hip_fused_grn_expansion", ("grn_expansion3d",), ("training",), "numerical", False, _hip_expansion, (*_TENSOR_GUARDS, "channels_supported")),
         ("pointwise_gemm_per_sample", ("pointwise_conv3d",), ("training",), "numerical", False, _pointwise_gemm, _TENSOR_GUARDS),
         ("triton_depthwise_dx", ("depthwise_conv3d",), ("backward_input",), "numerical", False, _no_triton, _DW_GUARDS),
         ("triton_split_dw", ("depthwise_conv3d",), ("backward_weight",), "numerical", False, _no_triton, _DW_GUARDS),

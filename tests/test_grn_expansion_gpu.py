@@ -1,0 +1,169 @@
+"""Fused MedNeXt v2 block expansion on the GPU: ``out = W2 . GRN(GELU(W1 . x +
+b1)) + b2 (+ residual)`` with GELU and GRN folded into the matrix-core GEMMs
+(hip_ops.grn_expansion), and each new GEMM mode on its own.
+
+Ground truth is the same chain in float64 on the same bf16 inputs (reference
+models/blocks_v2.py:44-45 with ops/grn.py:16-30). The bar is the bf16
+autocast one: every output and gradient within 2e-2 (rel-L2) of the truth, or
+no worse than twice the error of the reference's own unfused bf16 path
+(PyTorch convs, GELU and the GRN formula under autocast).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from helpers import BF16, check_against_truth, max_rel, rel_l2
+from mednext_accel_amd import global_response_norm3d_reference
+from mednext_accel_amd import hip_ops as P
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def chain(x, w1, b1, w2, b2, gamma, beta, residual, eps=1e-6):
+    u = F.conv3d(x, w1, b1)
+    z = global_response_norm3d_reference(F.gelu(u), gamma, beta, eps)
+    out = F.conv3d(z, w2, b2)
+    return out if residual is None else out + residual
+
+
+def make(n, c, hidden, cout, spatial, seed, residual=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(n, c, *spatial, generator=g)
+    w1 = torch.randn(hidden, c, 1, 1, 1, generator=g) / c**0.5
+    b1 = torch.randn(hidden, generator=g) * 0.1
+    w2 = torch.randn(cout, hidden, 1, 1, 1, generator=g) / hidden**0.5
+    b2 = torch.randn(cout, generator=g) * 0.1
+    gamma = torch.randn(1, hidden, 1, 1, 1, generator=g)
+    beta = torch.randn(1, hidden, 1, 1, 1, generator=g) * 0.5
+    res = torch.randn(n, cout, *spatial, generator=g) if residual else None
+    bf = [t.to(DEV, torch.bfloat16) for t in (x, w1, b1, w2, b2)]
+    gb = [t.to(DEV) for t in (gamma, beta)]
+    return bf, gb, (res.to(DEV, torch.bfloat16) if residual else None)
+
+
+CASES = [
+    (2, 32, 96, 32, (24, 24, 24), True),    # v2 stage 0: K = 96 project
+    (1, 64, 256, 64, (16, 16, 16), True),   # v2 stage 1: split-K project
+    (2, 8, 40, 12, (7, 9, 11), False),      # odd widths and volume, no residual
+    (1, 32, 128, 64, (12, 12, 12), False),  # down-block shape: Cout = 2 C
+]
+
+
+@pytest.mark.parametrize("n,c,hidden,cout,spatial,residual", CASES)
+def test_fused_expansion_matches_float64_chain(n, c, hidden, cout, spatial, residual):
+    print(f"[grn expansion] n={n} c={c} hidden={hidden} cout={cout} spatial={spatial} residual={residual}", flush=True)
+    (x, w1, b1, w2, b2), (gamma, beta), res = make(n, c, hidden, cout, spatial, hidden + cout, residual)
+    leaves = [t.clone().requires_grad_() for t in (x, w1, b1, w2, b2, gamma, beta)] + (
+        [res.clone().requires_grad_()] if residual else [])
+    hip_in = leaves
+    out, u, coef = P.grn_expansion(*hip_in[:7], hip_in[7] if residual else None, 1e-6)
+    assert out.dtype == torch.bfloat16 and u.dtype == torch.bfloat16 and coef.dtype == torch.float64
+    # reference path: the unfused chain under bf16 autocast (fp32 GRN parameters)
+    ref_in = [t.detach().float().clone().requires_grad_() if i in (5, 6) else t.detach().clone().requires_grad_()
+              for i, t in enumerate(leaves)]
+    with torch.autocast(DEV, dtype=torch.bfloat16):
+        ref_out = chain(*ref_in[:7], ref_in[7] if residual else None)
+    truth_in = [t.detach().double().clone().requires_grad_() for t in leaves]
+    truth = chain(*truth_in[:7], truth_in[7] if residual else None)
+    check_against_truth("output", out, ref_out, truth, BF16)
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(5)).to(DEV)
+    got = torch.autograd.grad(out, hip_in, g.bfloat16())
+    want = torch.autograd.grad(ref_out, ref_in, g.bfloat16())
+    exact = torch.autograd.grad(truth, truth_in, g.double())
+    names = ["x", "w1", "b1", "w2", "b2", "gamma", "beta", "residual"]
+    for name, a, b, t in zip(names, got, want, exact):
+        assert a.dtype == hip_in[names.index(name)].dtype, name
+        check_against_truth(name, a, b, t, BF16)
+
+
+def test_fused_expansion_is_bit_reproducible():
+    (x, w1, b1, w2, b2), (gamma, beta), res = make(1, 32, 96, 32, (20, 20, 20), 3)
+    runs = []
+    for _ in range(2):
+        leaves = [t.clone().requires_grad_() for t in (x, w1, b1, w2, b2, gamma, beta)]
+        out, _, _ = P.grn_expansion(*leaves, res, 1e-6)
+        grads = torch.autograd.grad(out, leaves, torch.ones_like(out))
+        runs.append((out, *grads))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
+def test_row_reduce_epilogue_matches_torch():
+    torch.manual_seed(11)
+    n, k, m, s = 2, 32, 96, 20
+    dy = torch.randn(n, k, s, s, s, device=DEV).bfloat16()
+    u = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
+    w = (torch.randn(k, m, 1, 1, 1, device=DEV) / m**0.5).bfloat16()  # conv weight [Cout=k][Cin=m]
+    v = s**3
+    slots = P.pointwise_row_slots(n, k, m, v, 0)
+    rows = torch.empty(n, m, slots, 2, device=DEV, dtype=torch.float64)
+    assert P.pointwise_conv(dy, w, aux=u, epilogue=P.PW_EPILOGUE_ROW_REDUCE, transpose=True, row_partial=rows) is None
+    dz = torch.einsum("km,nkv->nmv", w.double().view(k, m), dy.double().view(n, k, v))
+    a = F.gelu(u.float()).bfloat16().double().view(n, m, v)
+    sums = rows.sum(dim=2)
+    assert max_rel(sums[..., 0], (dz * a).sum(-1)) <= 1e-5
+    assert max_rel(sums[..., 1], dz.sum(-1)) <= 1e-5
+
+
+def test_affine_gelu_grad_epilogue_matches_torch():
+    torch.manual_seed(12)
+    n, k, m, s = 1, 64, 256, 12
+    dy = torch.randn(n, k, s, s, s, device=DEV).bfloat16()
+    u = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
+    w = (torch.randn(k, m, 1, 1, 1, device=DEV) / m**0.5).bfloat16()
+    c = torch.randn(n, m, 2, device=DEV, dtype=torch.float64)
+    du = P.pointwise_conv(dy, w, aux=u, epilogue=P.PW_EPILOGUE_AFFINE_GELU_GRAD, transpose=True, epilogue_coef=c)
+    v = s**3
+    dz = torch.einsum("km,nkv->nmv", w.double().view(k, m), dy.double().view(n, k, v))
+    uu = u.double().view(n, m, v).requires_grad_()
+    (dg,) = torch.autograd.grad(F.gelu(uu).sum(), uu)
+    a = F.gelu(u.float()).bfloat16().double().view(n, m, v)
+    want = (dz * c[..., :1] + a * c[..., 1:]) * dg
+    assert rel_l2(du.view(n, m, v), want) <= 8e-3
+
+
+def test_gelu_affine_prologue_forward_and_weight_grad():
+    torch.manual_seed(13)
+    n, k, m, s = 2, 96, 32, 16
+    u = torch.randn(n, k, s, s, s, device=DEV).bfloat16()
+    w = (torch.randn(m, k, 1, 1, 1, device=DEV) / k**0.5).bfloat16()
+    b = (torch.randn(m, device=DEV) * 0.1).bfloat16()
+    coef = torch.randn(n, k, 4, device=DEV, dtype=torch.float64)
+    coef[..., 0] = 1 + 0.3 * coef[..., 0]
+    y = P.pointwise_conv(u, w, b, prologue=P.PW_PROLOGUE_GELU_AFFINE, prologue_coef=coef)
+    v = s**3
+    z = F.gelu(u.float()).bfloat16().double().view(n, k, v) * coef[..., :1] + coef[..., 1:2]
+    want = torch.einsum("mk,nkv->nmv", w.double().view(m, k), z) + b.double()[None, :, None]
+    assert rel_l2(y.view(n, m, v), want) <= 8e-3
+    dy = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
+    dw, db = P.pointwise_weight_grad(dy, u, prologue=P.PW_PROLOGUE_GELU_AFFINE, prologue_coef=coef)
+    zb = z.bfloat16().double()  # the weight gradient rounds a * s + t per element
+    want_dw = torch.einsum("nmv,nkv->mk", dy.double().view(n, m, v), zb)
+    assert rel_l2(dw.view(m, k), want_dw) <= 8e-3
+    assert rel_l2(db, dy.double().sum(dim=(0, 2, 3, 4))) <= 8e-3
+
+
+def test_grn_stats_of_gelu_input():
+    torch.manual_seed(14)
+    u = torch.randn(2, 48, 10, 11, 12, device=DEV).bfloat16()
+    gamma = torch.randn(48, device=DEV)
+    beta = torch.randn(48, device=DEV)
+    coef = P.grn_stats(u, gamma, beta, 1e-6, gelu_input=True)
+    a = F.gelu(u.float()).bfloat16().double()
+    norms = a.flatten(2).norm(dim=2)
+    r = norms / (norms.sum(dim=1, keepdim=True) + 1e-6)
+    assert max_rel(coef[..., 3], norms) <= 1e-6
+    assert max_rel(coef[..., 2], r) <= 1e-6
+    assert max_rel(coef[..., 0], 1 + gamma.double() * r) <= 1e-6
+    assert max_rel(coef[..., 1], beta.double().expand(2, 48)) == 0
+
+
+def test_opcheck_grn_expansion():
+    (x, w1, b1, w2, b2), (gamma, beta), res = make(1, 8, 40, 8, (5, 6, 7), 21)
+    args = [t.clone().requires_grad_() for t in (x, w1, b1, w2, b2, gamma, beta)]
+    result = torch.library.opcheck(P.grn_expansion, (*args, res, 1e-6), raise_exception=False)
+    assert all(v == "SUCCESS" for v in result.values()), result

@@ -19,7 +19,7 @@ from torch.utils._python_dispatch import TorchDispatchMode
 from helpers import BF16, check_against_truth
 from mednext_accel_amd import MedNeXtV2, MedNeXtV2Block, get_mednext_v2_config, mednext_v2_base
 from mednext_accel_amd.adaptive import ModelOptimizationContext, install_adaptive_operators
-from mednext_accel_amd.grn import install_adaptive_grn
+from mednext_accel_amd.grn import install_adaptive_grn, install_fused_grn_expansions
 from mednext_accel_amd.mednext_v2 import configure_optimization
 from mednext_accel_amd.optimization import PolicyRegistry
 from mednext_accel_amd.step import make_training_step
@@ -31,6 +31,8 @@ GRN_BWD_OP = "mednext_accel_amd::grn_backward"
 DW_OP = "mednext_accel_amd::depthwise_conv3d_odd_regular"
 GN_OP = "mednext_accel_amd::group_norm_channels"
 PW_OP = "mednext_accel_amd::pointwise_conv3d"
+EXP_OP = "mednext_accel_amd::grn_expansion"
+EXP_BWD_OP = "mednext_accel_amd::grn_expansion_backward"
 MC = ModelOptimizationContext("mednext_v2", "base", "none")
 
 
@@ -53,9 +55,10 @@ def randomize_grn(model):
                 p.copy_(torch.randn(p.shape, generator=gen) * 0.5)
 
 
-@pytest.mark.parametrize("channels,size,ratio", [(32, 64, 3), (64, 32, 8)])
-def test_block_bf16_autocast_matches_reference_block(channels, size, ratio):
-    print(f"[v2 block] C={channels} S={size} R={ratio}", flush=True)
+@pytest.mark.parametrize("channels,size,ratio,fused", [(32, 64, 3, False), (64, 32, 8, False), (32, 64, 3, True),
+                                                       (64, 32, 4, True)])
+def test_block_bf16_autocast_matches_reference_block(channels, size, ratio, fused):
+    print(f"[v2 block] C={channels} S={size} R={ratio} fused={fused}", flush=True)
     torch.manual_seed(12)
     ref = MedNeXtV2Block(in_channels=channels, out_channels=channels, expansion_ratio=ratio).to(DEV).train()
     randomize_grn(ref)
@@ -64,6 +67,8 @@ def test_block_bf16_autocast_matches_reference_block(channels, size, ratio):
     resolver = PolicyRegistry().resolver()
     assert install_adaptive_operators(cand, resolver=resolver, model_context=MC) == 4
     assert install_adaptive_grn(cand, resolver=resolver, model_context=MC) == 1
+    if fused:
+        assert install_fused_grn_expansions(cand, resolver=resolver, model_context=MC) == 1
     x = torch.randn(2, channels, size, size, size, device=DEV, requires_grad=True)
     y = x.detach().clone().requires_grad_()
     z = x.detach().double().requires_grad_()
@@ -71,13 +76,17 @@ def test_block_bf16_autocast_matches_reference_block(channels, size, ratio):
         want = ref(x)
         with Observe() as seen:
             got = cand(y)
-    assert DW_OP in seen.ops and GN_OP in seen.ops and GRN_OP in seen.ops and PW_OP in seen.ops
+    assert DW_OP in seen.ops and GN_OP in seen.ops
+    if fused:
+        assert EXP_OP in seen.ops and GRN_OP not in seen.ops
+    else:
+        assert GRN_OP in seen.ops and PW_OP in seen.ops
     exact = truth(z)
     g = torch.randn_like(want)
     wants = torch.autograd.grad(want, (x, *ref.parameters()), g)
     with Observe() as seen_bwd:
         gots = torch.autograd.grad(got, (y, *cand.parameters()), g)
-    assert GRN_BWD_OP in seen_bwd.ops
+    assert (EXP_BWD_OP if fused else GRN_BWD_OP) in seen_bwd.ops
     exacts = torch.autograd.grad(exact, (z, *truth.parameters()), g.double())
     names = ["output", "x", *(n for n, _ in ref.named_parameters())]
     for name, a, b, t in zip(names, (got, *gots), (want, *wants), (exact, *exacts), strict=True):
@@ -133,7 +142,8 @@ def test_small_model_bf16_autocast_matches_reference_model():
             outs = cand(x)
         want = ref(x)
     exact = truth(x.double())
-    assert seen.ops.count(GRN_OP) == 17
+    assert seen.ops.count(GRN_OP) + seen.ops.count(EXP_OP) == 17
+    assert seen.ops.count(EXP_OP) > 0
     for i, (a, b, t) in enumerate(zip(outs, want, exact, strict=True)):
         check_against_truth(f"head {i}", a, b, t, BF16)
     for heads in (outs, want, exact):
@@ -161,7 +171,7 @@ def test_v2_base_training_step_matches_reference():
         losses.append(float(loss.detach()))
         norms.append(torch.stack([p.grad.float().norm() for p in model.parameters()]))
         if model is cand:
-            assert GRN_OP in seen.ops and GRN_BWD_OP in seen.ops and DW_OP in seen.ops and PW_OP in seen.ops
+            assert EXP_OP in seen.ops and EXP_BWD_OP in seen.ops and DW_OP in seen.ops and PW_OP in seen.ops
         del step
     print(f"  loss hip {losses[0]:.6f} reference {losses[1]:.6f}", flush=True)
     assert abs(losses[0] - losses[1]) / abs(losses[1]) < BF16
