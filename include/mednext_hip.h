@@ -170,11 +170,11 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
  * < 2 GiB, bf16-aligned tensors and a 16-byte aligned weight.
  * Prologue, applied to every x element as loaded:
  *   MEDNEXT_PW_PROLOGUE_GELU: x -> GELU(x) (exact erf form).
- *   MEDNEXT_PW_PROLOGUE_GELU_AFFINE: x -> a * s[n][k] + t[n][k], a = bf16(GELU(x)),
- *     (s, t) = entries 0 and 1 of the fp64 record prologue_coef[(n * K + k) * 4]
- *     (the layout mednext_grn_stats writes: GRN of the GELU output, folded in).
- *     The weight gradient rounds a * s + t to bf16 per element; the forward
- *     product computes the same W . (a s + t) as (W diag(s)) . a + W . t, with
+ *   MEDNEXT_PW_PROLOGUE_AFFINE: x -> x * s[n][k] + t[n][k], (s, t) = entries 0
+ *     and 1 of the fp64 record prologue_coef[(n * K + k) * 4] (the layout
+ *     mednext_grn_stats writes: a GRN folded into the GEMM that consumes it).
+ *     The weight gradient rounds x * s + t to bf16 per element; the forward
+ *     product computes the same W . (x s + t) as (W diag(s)) . x + W . t, with
  *     W diag(s) rounded to bf16 and W . t added to the bias in fp32
  *     (weight_layout 0 only).
  * Epilogue, applied to each accumulator y[n][m][v] (bias may be NULL):
@@ -183,17 +183,18 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
  *   BIAS_RESIDUAL: y = acc + bias[m] + aux[n][m][v]
  *   GELU_GRAD:     y = acc * GELU'(aux[n][m][v])   (bias unused)
  *   ROW_REDUCE:    y is not written; per row, row_partial receives the fp64
- *                  pair (sum_v acc * a, sum_v acc), a = bf16(GELU(aux)), one
- *                  pair per slot: row_partial[((n * M + m) * slots + slot) * 2]
+ *                  pair (sum_v acc * aux, sum_v acc), one pair per slot:
+ *                  row_partial[((n * M + m) * slots + slot) * 2]
  *                  (slots from mednext_pointwise_row_slots; bias unused)
- *   AFFINE_GELU_GRAD: y = (acc * c0 + a * c1) * GELU'(aux[n][m][v]) with
- *                  (c0, c1) = epilogue_coef[(n * M + m) * 2 + {0, 1}] (fp64)
- *                  and a = bf16(GELU(aux)) (bias unused)
+ *   AFFINE_SCALE:  y = (acc * c0 + aux * c1) * aux2[n][m][v] with
+ *                  (c0, c1) = epilogue_coef[(n * M + m) * 2 + {0, 1}] (fp64;
+ *                  bias unused)
+ *   BIAS_GELU_PAIR: y = GELU(acc + bias[m]) and y2 = GELU'(acc + bias[m])
  */
 enum mednext_pw_prologue {
   MEDNEXT_PW_PROLOGUE_NONE = 0,
   MEDNEXT_PW_PROLOGUE_GELU = 1,
-  MEDNEXT_PW_PROLOGUE_GELU_AFFINE = 2
+  MEDNEXT_PW_PROLOGUE_AFFINE = 2
 };
 enum mednext_pw_epilogue {
   MEDNEXT_PW_EPILOGUE_BIAS = 0,
@@ -201,7 +202,8 @@ enum mednext_pw_epilogue {
   MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL = 2,
   MEDNEXT_PW_EPILOGUE_GELU_GRAD = 3,
   MEDNEXT_PW_EPILOGUE_ROW_REDUCE = 4,
-  MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD = 5
+  MEDNEXT_PW_EPILOGUE_AFFINE_SCALE = 5,
+  MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR = 6
 };
 
 /* y = epilogue(op(W) . prologue(x)); blocks_per_sample = workgroups along V
@@ -217,17 +219,18 @@ int32_t mednext_pointwise_fwd(const void* x, const void* weight, const void* bia
                               int32_t weight_layout, int32_t prologue, int32_t epilogue,
                               int32_t dtype, int32_t blocks_per_sample, void* stream);
 
-/* mednext_pointwise_fwd with the coefficient tensors of the GELU_AFFINE
- * prologue and the ROW_REDUCE / AFFINE_GELU_GRAD epilogues (NULL where the
+/* mednext_pointwise_fwd with the extra operands of the AFFINE prologue and
+ * the ROW_REDUCE / AFFINE_SCALE / BIAS_GELU_PAIR epilogues (NULL where the
  * chosen mode does not use them). Together they run the MedNeXt v2 block
- * expansion project(GRN(GELU(expand(x)))) without materialising GELU or GRN
- * outputs: the forward of the project GEMM (reference models/blocks_v2.py:44-45
- * with ops/grn.py:16-30 between the GEMMs), and in the backward the GRN row sums
- * and the gradient through GRN and GELU (reference ops/_triton/grn.py:242-317
- * plus the GELU backward). */
+ * expansion project(GRN(GELU(expand(x)))) (reference models/blocks_v2.py:44-45
+ * with ops/grn.py:16-30 between the GEMMs) without a GRN output tensor: the
+ * expand GEMM writes GELU and GELU' of its output, the project GEMM applies the
+ * GRN affine as it loads, and in the backward one transposed GEMM reduces the
+ * GRN row sums and a second writes the gradient through GRN and GELU
+ * (reference ops/_triton/grn.py:242-317 plus the GELU backward). */
 int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* bias, const void* aux,
-                                 void* y, int64_t n, int64_t k, int64_t m, int64_t v,
-                                 int32_t weight_layout, int32_t prologue, int32_t epilogue,
+                                 const void* aux2, void* y, void* y2, int64_t n, int64_t k, int64_t m,
+                                 int64_t v, int32_t weight_layout, int32_t prologue, int32_t epilogue,
                                  const void* prologue_coef, const void* epilogue_coef,
                                  void* row_partial, int32_t dtype, int32_t blocks_per_sample,
                                  void* stream);
@@ -253,7 +256,7 @@ int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* gr
                                 int32_t dtype, int32_t splits, void* stream);
 
 /* mednext_pointwise_wgrad with the prologue's coefficient records (for
- * GELU_AFFINE: the GRN-normalised GELU output as the x operand). */
+ * AFFINE: the GRN output computed from its input as the x operand). */
 int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const void* x, void* grad_weight,
                                    void* grad_bias, void* workspace, size_t workspace_bytes,
                                    int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
@@ -278,11 +281,10 @@ int32_t mednext_grn_fwd(const void* x, int32_t x_dtype, const void* gamma, const
                         int64_t spatial, double eps, int32_t splits, void* workspace,
                         size_t workspace_bytes, void* stream);
 
-/* Statistics only (no output tensor): coef as mednext_grn_fwd writes it, of
- * x itself (gelu_input 0) or of bf16(GELU(x)) (gelu_input 1, bf16 x only: the
- * MedNeXt v2 expansion, whose GELU is fused into the next GEMM). Same
- * workspace as mednext_grn_fwd. */
-int32_t mednext_grn_stats(const void* x, int32_t x_dtype, int32_t gelu_input, const void* gamma,
+/* Statistics only (no output tensor): coef as mednext_grn_fwd writes it, for
+ * a consumer that applies the GRN itself (the AFFINE pointwise prologue).
+ * Same workspace as mednext_grn_fwd. */
+int32_t mednext_grn_stats(const void* x, int32_t x_dtype, const void* gamma,
                           const void* beta, int32_t param_dtype, void* coef, int64_t n, int64_t c,
                           int64_t spatial, double eps, int32_t splits, void* workspace,
                           size_t workspace_bytes, void* stream);

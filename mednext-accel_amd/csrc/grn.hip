@@ -15,7 +15,6 @@
 // and derives the per-(n, c) coefficients; (3) an elementwise pass applies
 // them. Rows stream as a scalar head, 16-byte vectors and a scalar tail, so any
 // volume is handled. All reductions are fixed-order (bit-reproducible).
-#include "activation.h"
 #include "common.h"
 
 namespace mednext {
@@ -77,9 +76,8 @@ __device__ inline void store_param(void* p, int dtype, int64_t i, double v) {
   }
 }
 
-// Pass 1 (forward): partial sum of squares per (row, split), of x or (GELU)
-// of bf16(GELU(x)) as the bf16 tensor torch's GELU would produce holds it.
-template <typename T, bool GELU = false>
+// Pass 1 (forward): partial sum of squares per (row, split).
+template <typename T>
 __global__ __launch_bounds__(kThreads) void grn_sumsq_kernel(const T* __restrict__ x, int64_t v, int splits,
                                                             int64_t chunk, bool vec_ok, double* __restrict__ part) {
   using Acc = typename AccOf<T>::type;
@@ -88,8 +86,7 @@ __global__ __launch_bounds__(kThreads) void grn_sumsq_kernel(const T* __restrict
   const RowSpan rs = row_span(ck.row * v + ck.begin, ck.end - ck.begin, vec_ok);
   Acc s = Acc(0);
   for (int64_t i = threadIdx.x; i < rs.scalar_count(); i += blockDim.x) {
-    Acc e = Cvt<T, Acc>::load(cp[rs.scalar_index(i)]);
-    if constexpr (GELU) e = gelu_bf16(e);
+    const Acc e = Cvt<T, Acc>::load(cp[rs.scalar_index(i)]);
     s += e * e;
   }
   for (int64_t j0 = threadIdx.x; j0 < rs.nvec; j0 += kUnroll * blockDim.x) {
@@ -107,11 +104,7 @@ __global__ __launch_bounds__(kThreads) void grn_sumsq_kernel(const T* __restrict
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
 #pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        Acc f = e[u][t];
-        if constexpr (GELU) f = gelu_bf16(f);  // gelu(0) = 0: padding stays zero
-        s += f * f;
-      }
+      for (int t = 0; t < 8; ++t) s += e[u][t] * e[u][t];
   }
   double a = s, b = 0.0;
   block_sum2(a, b);
@@ -370,12 +363,12 @@ size_t bwd_workspace(int64_t n, int64_t c, int splits) {
 }
 
 // Pass 1 + pass 2 only: coef without an output tensor.
-template <typename T, bool GELU>
+template <typename T>
 int grn_stats_typed(const void* x, const void* gamma, const void* beta, int pdtype, double* coef, int64_t n,
                     int64_t c, int64_t v, double eps, int splits, double* part, hipStream_t st) {
   const int64_t chunk = chunk_len(v, splits);
   const int64_t blocks = n * c * splits;
-  hipLaunchKernelGGL((grn_sumsq_kernel<T, GELU>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st,
+  hipLaunchKernelGGL((grn_sumsq_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st,
                      static_cast<const T*>(x), v, splits, chunk, aligned64(x), part);
   MEDNEXT_CHECK_LAUNCH();
   hipLaunchKernelGGL(grn_fwd_coef_kernel, dim3(static_cast<unsigned>(n)), dim3(kThreads), 0, st, part, c, splits,
@@ -494,26 +487,23 @@ extern "C" int32_t mednext_grn_bwd(const void* grad_output, int32_t dy_dtype, co
   return MEDNEXT_STATUS_UNSUPPORTED;
 }
 
-extern "C" int32_t mednext_grn_stats(const void* x, int32_t x_dtype, int32_t gelu_input, const void* gamma,
+extern "C" int32_t mednext_grn_stats(const void* x, int32_t x_dtype, const void* gamma,
                                      const void* beta, int32_t param_dtype, void* coef, int64_t n, int64_t c,
                                      int64_t spatial, double eps, int32_t splits, void* workspace,
                                      size_t workspace_bytes, void* stream) {
   if (int st = check_shape(n, c, spatial, splits)) return st;
   MEDNEXT_CHECK_ARG(x && coef, "null tensor pointer");
   MEDNEXT_CHECK_ARG(dtype_ok(x_dtype) && dtype_ok(param_dtype), "unsupported dtype");
-  MEDNEXT_CHECK_ARG(gelu_input == 0 || (gelu_input == 1 && x_dtype == MEDNEXT_DTYPE_BF16),
-                    "gelu_input must be 0, or 1 with a bf16 input");
   MEDNEXT_CHECK_ARG(eps > 0.0, "eps must be positive");
   MEDNEXT_CHECK_ARG(workspace && workspace_bytes >= fwd_workspace(n, c, splits), "workspace too small");
   auto* part = static_cast<double*>(workspace);
   auto* cf = static_cast<double*>(coef);
   auto s = static_cast<hipStream_t>(stream);
-  if (gelu_input) return grn_stats_typed<bf16_t, true>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
   switch (x_dtype) {
-    case MEDNEXT_DTYPE_F32: return grn_stats_typed<float, false>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
-    case MEDNEXT_DTYPE_F64: return grn_stats_typed<double, false>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
-    case MEDNEXT_DTYPE_F16: return grn_stats_typed<f16_t, false>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
-    default: return grn_stats_typed<bf16_t, false>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+    case MEDNEXT_DTYPE_F32: return grn_stats_typed<float>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+    case MEDNEXT_DTYPE_F64: return grn_stats_typed<double>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+    case MEDNEXT_DTYPE_F16: return grn_stats_typed<f16_t>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
+    default: return grn_stats_typed<bf16_t>(x, gamma, beta, param_dtype, cf, n, c, spatial, eps, splits, part, s);
   }
 }
 

@@ -63,36 +63,42 @@ __device__ inline uint4 gelu_vec(uint4 v) {
   return make_uint4(gelu_word(v.x), gelu_word(v.y), gelu_word(v.z), gelu_word(v.w));
 }
 
-// bf16(bf16(GELU(x)) * s + t) for the 8 values of one 16-byte group.
-__device__ inline uint32_t gelu_affine_word(uint32_t w, float s, float t) {
-  return pack_bf16x2(fmaf(gelu_bf16(bf16_lo(w)), s, t), fmaf(gelu_bf16(bf16_hi(w)), s, t));
+// bf16(x * s + t) for the 8 values of one 16-byte group.
+__device__ inline uint32_t affine_word(uint32_t w, float s, float t) {
+  return pack_bf16x2(fmaf(bf16_lo(w), s, t), fmaf(bf16_hi(w), s, t));
 }
-__device__ inline uint4 gelu_affine_vec(uint4 v, float s, float t) {
-  return make_uint4(gelu_affine_word(v.x, s, t), gelu_affine_word(v.y, s, t), gelu_affine_word(v.z, s, t),
-                    gelu_affine_word(v.w, s, t));
+__device__ inline uint4 affine_vec(uint4 v, float s, float t) {
+  return make_uint4(affine_word(v.x, s, t), affine_word(v.y, s, t), affine_word(v.z, s, t), affine_word(v.w, s, t));
 }
 
-// Coefficient tensors of the GELU_AFFINE prologue and the ROW_REDUCE /
-// AFFINE_GELU_GRAD epilogues (unused members are null).
+// Extra operands of the AFFINE prologue and the ROW_REDUCE / AFFINE_SCALE /
+// BIAS_GELU_PAIR epilogues (unused members are null).
 struct PwExtra {
   const double* pcoef;  // [N][K][4]: (s, t, ., .) per (sample, input channel)
   const double* ecoef;  // [N][M][2]: (c0, c1) per (sample, output row)
   double* rpart;        // [N][M][slots][2] row sums
+  const bf16_t* aux2;   // AFFINE_SCALE: second per-element operand, shaped like y
+  bf16_t* y2;           // BIAS_GELU_PAIR: second output, shaped like y
   int slots;
 };
 
-constexpr bool epi_has_aux(int epi) {
-  return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epi == MEDNEXT_PW_EPILOGUE_GELU_GRAD ||
-         epi == MEDNEXT_PW_EPILOGUE_ROW_REDUCE || epi == MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD;
+constexpr bool epi_has_bias(int epi) {
+  return epi == MEDNEXT_PW_EPILOGUE_BIAS || epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU ||
+         epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR;
 }
 
-// Per-row LDS vectors after the weight block: bias, then the AFFINE_GELU_GRAD
+constexpr bool epi_has_aux(int epi) {
+  return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epi == MEDNEXT_PW_EPILOGUE_GELU_GRAD ||
+         epi == MEDNEXT_PW_EPILOGUE_ROW_REDUCE || epi == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE;
+}
+
+// Per-row LDS vectors after the weight block: bias, then the AFFINE_SCALE
 // coefficients c0 and c1 (16 MT floats each).
 constexpr int kRowVecs = 3;
 
-// The forward GEMMs take GELU_AFFINE as W . (a s + t) = (W diag(s)) . a + W . t
-// with a = bf16(GELU(x)): the column scale goes into the LDS weight block
-// (load_weight_block), W . t into the row bias, and X only needs GELU.
+// The forward GEMMs take AFFINE as W . (x s + t) = (W diag(s)) . x + W . t:
+// the column scale goes into the LDS weight block (load_weight_block) and
+// W . t into the row bias, so X is used as loaded.
 // shift[r] = sum_k W[m0 + r][k] t[k] for the workgroup's 16 MT rows (weight
 // stored [M][K]); threads_per_row consecutive lanes share a row and combine
 // their strided partial sums with shuffles (fixed order).
@@ -113,53 +119,58 @@ __device__ void affine_row_shift(const bf16_t* __restrict__ w, const double* __r
   if (j == 0) shift[r] = acc;
 }
 
-// X slice rows through the prologue (GELU for GELU and, with the affine
-// folded into W and the bias, GELU_AFFINE).
+// X slice rows through the prologue (the AFFINE prologue is folded into W and
+// the bias, so only GELU touches X).
 template <int PRO>
 __device__ inline void apply_prologue(const uint4 (&r)[8], uint4 (&cur)[8]) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) cur[i] = PRO != MEDNEXT_PW_PROLOGUE_NONE ? gelu_vec(r[i]) : r[i];
+  for (int i = 0; i < 8; ++i) cur[i] = PRO == MEDNEXT_PW_PROLOGUE_GELU ? gelu_vec(r[i]) : r[i];
+}
+
+__device__ inline float bf16_at(const uint4& v, int j) {
+  const uint32_t wd = j / 2 == 0 ? v.x : j / 2 == 1 ? v.y : j / 2 == 2 ? v.z : v.w;
+  return (j & 1) ? bf16_hi(wd) : bf16_lo(wd);
 }
 
 // One output row's 8 accumulators through a value epilogue (not ROW_REDUCE).
-// `av` holds the row's 8 aux values (bf16), b the row bias, c0 / c1 the
-// AFFINE_GELU_GRAD coefficients.
+// `av` / `av2` hold the row's 8 aux / aux2 values (bf16), b the row bias,
+// c0 / c1 the AFFINE_SCALE coefficients. BIAS_GELU_PAIR leaves GELU in v and
+// GELU' in v2.
 template <int EPI>
-__device__ inline void epilogue_values(float (&v)[8], const uint4& av, float b, float c0, float c1) {
+__device__ inline void epilogue_values(float (&v)[8], float (&v2)[8], const uint4& av, const uint4& av2, float b,
+                                       float c0, float c1) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] += b;
   if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = gelu_f(v[j]);
-  } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD ||
-                       EPI == MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD) {
+  } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t wd = j / 2 == 0 ? av.x : j / 2 == 1 ? av.y : j / 2 == 2 ? av.z : av.w;
-      const float e = (j & 1) ? bf16_hi(wd) : bf16_lo(wd);
-      if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL) {
-        v[j] += e;
-      } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD) {
-        v[j] *= gelu_grad_f(e);
-      } else {
-        float g, dg;
-        gelu_pair(e, g, dg);
-        const float a = bf16_to_f32(f32_to_bf16(g));
-        v[j] = fmaf(v[j], c0, a * c1) * dg;
-      }
-    }
+    for (int j = 0; j < 8; ++j) gelu_pair(v[j], v[j], v2[j]);
+  } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] += bf16_at(av, j);
+  } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] *= gelu_grad_f(bf16_at(av, j));
+  } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = fmaf(v[j], c0, bf16_at(av, j) * c1) * bf16_at(av2, j);
   }
 }
 
-// ROW_REDUCE: add sum_j acc_j * bf16(GELU(aux_j)) and sum_j acc_j to (ra, rb).
+// ROW_REDUCE: add sum_j acc_j * aux_j and sum_j acc_j to (ra, rb).
 __device__ inline void row_reduce_add(const float (&v)[8], const uint4& av, float& ra, float& rb) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const uint32_t wd = j / 2 == 0 ? av.x : j / 2 == 1 ? av.y : j / 2 == 2 ? av.z : av.w;
-    const float a = gelu_bf16((j & 1) ? bf16_hi(wd) : bf16_lo(wd));
-    ra = fmaf(v[j], a, ra);
+    ra = fmaf(v[j], bf16_at(av, j), ra);
     rb += v[j];
   }
+}
+
+__device__ inline uint4 pack8(const float (&v)[8]) {
+  return make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                    pack_bf16x2(v[6], v[7]));
 }
 
 // Sum over the 16 lanes of a row group (lanes differing in bits 0-3), fixed order.
@@ -319,12 +330,11 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   const int bx = static_cast<int>(rest % g.wgs);
   const int64_t n = rest / g.wgs;
   const int m0 = mg * 16 * MT;
-  constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE;
+  constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_AFFINE;
   const double* const coef_n = kAffine ? ex.pcoef + n * g.K * 4 : nullptr;
   load_weight_block<MT>(w, pw_lds, g, m0, coef_n);
   // Row vectors of this row group as fp32 after the weight block (zero past
-  // M): bias (plus W . t for GELU_AFFINE), then the AFFINE_GELU_GRAD
-  // coefficients c0, c1.
+  // M): bias (plus W . t for AFFINE), then the AFFINE_SCALE coefficients c0, c1.
   float* const bias_lds = reinterpret_cast<float*>(pw_lds + static_cast<size_t>(16 * MT) * g.ks * 32);
   float* const c0_lds = bias_lds + 16 * MT;
   float* const c1_lds = c0_lds + 16 * MT;
@@ -335,10 +345,10 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   if (threadIdx.x < 16 * MT) {
     const int m = m0 + threadIdx.x;
     const bool in = m < g.M;
-    float b = (EPI <= MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
+    float b = (epi_has_bias(EPI) && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
     if constexpr (kAffine) b += c0_lds[threadIdx.x];
     bias_lds[threadIdx.x] = b;
-    if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD) {
+    if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) {
       c0_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2]) : 0.f;
       c1_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2 + 1]) : 0.f;
     }
@@ -348,10 +358,14 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_col = lane & 15, q = lane >> 4;
   const uint32_t V = g.V;
+  const int64_t yoff = n * g.M * static_cast<int64_t>(V);
   const __amdgpu_buffer_rsrc_t xr = slab_rsrc(x + n * g.K * static_cast<int64_t>(V), g.K * V * 2u);
-  const __amdgpu_buffer_rsrc_t yr = slab_rsrc(y + n * g.M * static_cast<int64_t>(V), g.M * V * 2u);
-  const bf16_t* auxn = aux != nullptr ? aux + n * g.M * static_cast<int64_t>(V) : nullptr;
-  const __amdgpu_buffer_rsrc_t ar = slab_rsrc(auxn != nullptr ? auxn : y, auxn != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t yr = slab_rsrc(y != nullptr ? y + yoff : x, y != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t y2r = slab_rsrc(ex.y2 != nullptr ? ex.y2 + yoff : x, ex.y2 != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t ar = slab_rsrc(aux != nullptr ? aux + yoff : x, aux != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t a2r =
+      slab_rsrc(ex.aux2 != nullptr ? ex.aux2 + yoff : x, ex.aux2 != nullptr ? g.M * V * 2u : 0u);
+  constexpr bool kAux2 = EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE;
   const int mtiles = min(MT, (g.M - m0 + 15) / 16);
   const uint4* frag = reinterpret_cast<const uint4*>(pw_lds) + lane;
   const int cstride = g.wgs * 4;
@@ -391,7 +405,9 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
       }
     }
   };
-  auto load_aux = [&](int chunk, uint4 (&av)[MT][4]) {
+  // aux rows, and for AFFINE_SCALE the aux2 rows in the upper half of av
+  // (av[MT][4] for aux, av[MT][4 + r] for aux2 when MT == 1).
+  auto load_aux = [&](int chunk, uint4 (&av)[MT][kAux2 ? 8 : 4]) {
     if constexpr (kAux) {
       const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
       const uint32_t nv = valid(chunk);
@@ -400,7 +416,9 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int m = m0 + 16 * mt + 4 * q + r;
-          av[mt][r] = load_group(ar, (static_cast<uint32_t>(min(m, g.M - 1)) * V + vl) * 2u, m < g.M ? nv : 0u);
+          const uint32_t off = (static_cast<uint32_t>(min(m, g.M - 1)) * V + vl) * 2u;
+          av[mt][r] = load_group(ar, off, m < g.M ? nv : 0u);
+          if constexpr (kAux2) av[mt][4 + r] = load_group(a2r, off, m < g.M ? nv : 0u);
         }
     }
   };
@@ -410,7 +428,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) rsa[mt][r] = rsb[mt][r] = 0.f;
-  auto epilogue = [&](int chunk, const f32x4_t (&acc)[MT][8], const uint4 (&av)[MT][4]) {
+  auto epilogue = [&](int chunk, const f32x4_t (&acc)[MT][8], const uint4 (&av)[MT][kAux2 ? 8 : 4]) {
     const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
     const uint32_t nv = valid(chunk);
 #pragma unroll
@@ -428,12 +446,14 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
           // Voxels past V and rows past M have zero accumulators: no masking.
           row_reduce_add(v, av[mt][r], rsa[mt][r], rsb[mt][r]);
         } else {
-          uint4 a4 = make_uint4(0u, 0u, 0u, 0u);
+          uint4 a4 = make_uint4(0u, 0u, 0u, 0u), b4 = a4;
           if constexpr (kAux) a4 = av[mt][r];
-          epilogue_values<EPI>(v, a4, bias_lds[lr], c0_lds[lr], c1_lds[lr]);
-          store_group(yr, (m * V + vl) * 2u, mrow < g.M ? nv : 0u,
-                      make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                                 pack_bf16x2(v[6], v[7])));
+          if constexpr (kAux2) b4 = av[mt][4 + r];
+          float v2[8];
+          epilogue_values<EPI>(v, v2, a4, b4, bias_lds[lr], c0_lds[lr], c1_lds[lr]);
+          const uint32_t nvr = mrow < g.M ? nv : 0u;
+          store_group(yr, (m * V + vl) * 2u, nvr, pack8(v));
+          if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR) store_group(y2r, (m * V + vl) * 2u, nvr, pack8(v2));
         }
       }
     }
@@ -471,7 +491,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
     auto process = [&](auto parity) {
       constexpr int P = decltype(parity)::value;
       constexpr int kAuxSlice = KS > 2 ? KS - 2 : 0;  // aux arrives during the last two slices
-      uint4 av[MT][4];
+      uint4 av[MT][kAux2 ? 8 : 4];
       f32x4_t acc[MT][8];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -502,7 +522,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   } else {
     const int ksteps = g.ks;
     for (; chunk < g.chunks; chunk += cstride) {
-      uint4 av[MT][4];
+      uint4 av[MT][kAux2 ? 8 : 4];
       load_aux(chunk, av);
       f32x4_t acc[MT][8];
 #pragma unroll
@@ -547,7 +567,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
   const int bx = static_cast<int>(rest % g.wgs);
   const int64_t n = rest / g.wgs;
   const int m0 = mg * 16 * MT;
-  constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE;
+  constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_AFFINE;
   const double* const coef_n = kAffine ? ex.pcoef + n * g.K * 4 : nullptr;
   load_weight_block<MT>(w, pw_lds, g, m0, coef_n);
   float* const bias_lds = reinterpret_cast<float*>(pw_lds + static_cast<size_t>(16 * MT) * g.ks * 32);
@@ -561,10 +581,10 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
   if (threadIdx.x < 16 * MT) {
     const int m = m0 + threadIdx.x;
     const bool in = m < g.M;
-    float b = (EPI <= MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
+    float b = (epi_has_bias(EPI) && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
     if constexpr (kAffine) b += c0_lds[threadIdx.x];
     bias_lds[threadIdx.x] = b;
-    if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD) {
+    if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) {
       c0_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2]) : 0.f;
       c1_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2 + 1]) : 0.f;
     }
@@ -574,10 +594,14 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_col = lane & 15, q = lane >> 4;
   const uint32_t V = g.V;
+  const int64_t yoff = n * g.M * static_cast<int64_t>(V);
   const __amdgpu_buffer_rsrc_t xr = slab_rsrc(x + n * g.K * static_cast<int64_t>(V), g.K * V * 2u);
-  const __amdgpu_buffer_rsrc_t yr = slab_rsrc(y + n * g.M * static_cast<int64_t>(V), g.M * V * 2u);
-  const bf16_t* auxn = aux != nullptr ? aux + n * g.M * static_cast<int64_t>(V) : nullptr;
-  const __amdgpu_buffer_rsrc_t ar = slab_rsrc(auxn != nullptr ? auxn : y, auxn != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t yr = slab_rsrc(y != nullptr ? y + yoff : x, y != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t y2r = slab_rsrc(ex.y2 != nullptr ? ex.y2 + yoff : x, ex.y2 != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t ar = slab_rsrc(aux != nullptr ? aux + yoff : x, aux != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t a2r =
+      slab_rsrc(ex.aux2 != nullptr ? ex.aux2 + yoff : x, ex.aux2 != nullptr ? g.M * V * 2u : 0u);
+  constexpr bool kAux2 = EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE;
   const int mtiles = min(MT, (g.M - m0 + 15) / 16);
   const uint4* frag = reinterpret_cast<const uint4*>(pw_lds) + lane;
   float rsa[MT], rsb[MT];  // ROW_REDUCE running sums of rows 16 mt + 4 q + wave
@@ -600,12 +624,14 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
         }
       }
     };
-    uint4 av[MT];
+    uint4 av[MT], av2[MT];
     if constexpr (kAux) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         const int m = m0 + 16 * mt + 4 * q + wave;
-        av[mt] = load_group(ar, (static_cast<uint32_t>(min(m, g.M - 1)) * V + vl) * 2u, m < g.M ? nv : 0u);
+        const uint32_t off = (static_cast<uint32_t>(min(m, g.M - 1)) * V + vl) * 2u;
+        av[mt] = load_group(ar, off, m < g.M ? nv : 0u);
+        if constexpr (kAux2) av2[mt] = load_group(a2r, off, m < g.M ? nv : 0u);
       }
     }
     f32x4_t acc[MT][8];
@@ -665,12 +691,14 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
       if constexpr (kReduce) {
         row_reduce_add(v, av[mt], rsa[mt], rsb[mt]);
       } else {
-        uint4 a4 = make_uint4(0u, 0u, 0u, 0u);
+        uint4 a4 = make_uint4(0u, 0u, 0u, 0u), b4 = a4;
         if constexpr (kAux) a4 = av[mt];
-        epilogue_values<EPI>(v, a4, bias_lds[lr], c0_lds[lr], c1_lds[lr]);
-        store_group(yr, (m * V + vl) * 2u, mrow < g.M ? nv : 0u,
-                    make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                               pack_bf16x2(v[6], v[7])));
+        if constexpr (kAux2) b4 = av2[mt];
+        float v2[8];
+        epilogue_values<EPI>(v, v2, a4, b4, bias_lds[lr], c0_lds[lr], c1_lds[lr]);
+        const uint32_t nvr = mrow < g.M ? nv : 0u;
+        store_group(yr, (m * V + vl) * 2u, nvr, pack8(v));
+        if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR) store_group(y2r, (m * V + vl) * 2u, nvr, pack8(v2));
       }
     }
     __syncthreads();  // the next chunk's turn 0 overwrites the sums read above
@@ -702,7 +730,7 @@ struct PwWGeom {
   uint32_t span;   // voxels per split (multiple of kWgStage)
   int mblocks, kblocks;
   int64_t stride;  // floats per partial slot: M * K + M
-  const double* pcoef;  // GELU_AFFINE prologue records [N][K][4] (else null)
+  const double* pcoef;  // AFFINE prologue records [N][K][4] (else null)
 };
 
 // dW[M][K] = sum_v dY[M][v] X[K][v] over one split's voxel range, for an output
@@ -742,10 +770,10 @@ __global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_ke
   const uint32_t vbeg = static_cast<uint32_t>(split) * g.span;
   const uint32_t vend = min(V, vbeg + g.span);
   const bool do_bias = k0 == 0;
-  // GELU_AFFINE: (s, t) of the tile's X rows in LDS (zero past K); voxels
-  // past the range load as zero and become t, which meets zero grad_output.
-  __shared__ float aff[PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE ? 2 * RK : 1];
-  if constexpr (PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) {
+  // AFFINE: (s, t) of the tile's X rows in LDS (zero past K); voxels past
+  // the range load as zero and become t, which meets zero grad_output.
+  __shared__ float aff[PRO == MEDNEXT_PW_PROLOGUE_AFFINE ? 2 * RK : 1];
+  if constexpr (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
     for (int i = threadIdx.x; i < RK; i += kPwThreads) {
       const int k = k0 + i;
       aff[i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4]) : 0.f;
@@ -795,8 +823,8 @@ __global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_ke
         }
       } else if (PRO == MEDNEXT_PW_PROLOGUE_GELU) {
         v = gelu_vec(v);  // gelu(0) = 0: missing voxels stay zero
-      } else if (PRO == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) {
-        v = gelu_affine_vec(v, aff[r - RM], aff[RK + r - RM]);
+      } else if (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
+        v = affine_vec(v, aff[r - RM], aff[RK + r - RM]);
       }
       *reinterpret_cast<uint4*>(tile + r * kWgPitch + 8 * grp) = v;
     }
@@ -935,17 +963,17 @@ using FwdKernel = void (*)(const bf16_t*, const bf16_t*, const bf16_t*, const bf
 constexpr int kSplitKSlices = 8;  // K >= 256: the four waves of a workgroup split K
 
 // Supported (prologue, epilogue) pairs: NONE with any epilogue, GELU with
-// BIAS .. GELU_GRAD, GELU_AFFINE with BIAS or BIAS_RESIDUAL.
+// BIAS .. GELU_GRAD, AFFINE with BIAS or BIAS_RESIDUAL.
 bool pro_epi_supported(int pro, int epi) {
-  if (pro == MEDNEXT_PW_PROLOGUE_NONE) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD;
+  if (pro == MEDNEXT_PW_PROLOGUE_NONE) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR;
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_GELU_GRAD;
-  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) return epi == MEDNEXT_PW_EPILOGUE_BIAS || epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL;
+  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) return epi == MEDNEXT_PW_EPILOGUE_BIAS || epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL;
   return false;
 }
 
 template <int MT>
 FwdKernel splitk_instance(int pro, int epi) {
-  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) {
+  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) {
     return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL ? pw_fwd_splitk_kernel<MT, 2, 2> : pw_fwd_splitk_kernel<MT, 2, 0>;
   }
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
@@ -962,14 +990,16 @@ FwdKernel splitk_instance(int pro, int epi) {
     case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_splitk_kernel<MT, 0, 2>;
     case MEDNEXT_PW_EPILOGUE_GELU_GRAD: return pw_fwd_splitk_kernel<MT, 0, 3>;
     case MEDNEXT_PW_EPILOGUE_ROW_REDUCE: return pw_fwd_splitk_kernel<MT, 0, 4>;
-    default: return pw_fwd_splitk_kernel<MT, 0, 5>;
+    case MEDNEXT_PW_EPILOGUE_AFFINE_SCALE: return pw_fwd_splitk_kernel<MT, 0, 5>;
+    default: return pw_fwd_splitk_kernel<MT, 0, 6>;
   }
 }
 
 // Four-tile row groups are only used by epilogues without an aux tensor.
 template <int KS, int MT>
 FwdKernel fwd_instance_noaux(int pro, int epi) {
-  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) return pw_fwd_kernel<KS, MT, 2, 0>;
+  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) return pw_fwd_kernel<KS, MT, 2, 0>;
+  if (epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR) return pw_fwd_kernel<KS, MT, 0, 6>;
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
     return epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU ? pw_fwd_kernel<KS, MT, 1, 1> : pw_fwd_kernel<KS, MT, 1, 0>;
   }
@@ -978,7 +1008,7 @@ FwdKernel fwd_instance_noaux(int pro, int epi) {
 
 template <int KS, int MT>
 FwdKernel fwd_instance(int pro, int epi) {
-  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) {
+  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) {
     return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL ? pw_fwd_kernel<KS, MT, 2, 2> : pw_fwd_kernel<KS, MT, 2, 0>;
   }
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
@@ -995,7 +1025,8 @@ FwdKernel fwd_instance(int pro, int epi) {
     case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_kernel<KS, MT, 0, 2>;
     case MEDNEXT_PW_EPILOGUE_GELU_GRAD: return pw_fwd_kernel<KS, MT, 0, 3>;
     case MEDNEXT_PW_EPILOGUE_ROW_REDUCE: return pw_fwd_kernel<KS, MT, 0, 4>;
-    default: return pw_fwd_kernel<KS, MT, 0, 5>;
+    case MEDNEXT_PW_EPILOGUE_AFFINE_SCALE: return pw_fwd_kernel<KS, MT, 0, 5>;
+    default: return pw_fwd_kernel<KS, MT, 0, 6>;
   }
 }
 
@@ -1008,6 +1039,7 @@ int pick_mt(int64_t k, int64_t m, int epi) {
   const bool aux = epi_has_aux(epi);
   auto fits = [&](int mt) { return static_cast<size_t>(16 * mt) * ks * 32 * 2 <= kMaxWeightLds; };
   if (ks >= kSplitKSlices) return m > 16 && fits(2) ? 2 : 1;
+  if (epi == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) return 1;  // two aux rows per output row
   if (!aux && ks == 1 && m > 32 && fits(4)) return 4;
   if (m > 16 && fits(2)) return 2;
   return 1;
@@ -1031,7 +1063,7 @@ using WgradKernel = void (*)(const bf16_t*, const bf16_t*, float*, PwWGeom);
 
 template <int TM, int TK>
 WgradKernel wgrad_instance(int pro) {
-  if (pro == MEDNEXT_PW_PROLOGUE_GELU_AFFINE) return pw_wgrad_kernel<TM, TK, 2>;
+  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) return pw_wgrad_kernel<TM, TK, 2>;
   return pro == MEDNEXT_PW_PROLOGUE_GELU ? pw_wgrad_kernel<TM, TK, 1> : pw_wgrad_kernel<TM, TK, 0>;
 }
 
@@ -1101,8 +1133,8 @@ extern "C" int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, 
 }
 
 extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* bias, const void* aux,
-                                            void* y, int64_t n, int64_t k, int64_t m, int64_t v,
-                                            int32_t weight_layout, int32_t prologue, int32_t epilogue,
+                                            const void* aux2, void* y, void* y2, int64_t n, int64_t k, int64_t m,
+                                            int64_t v, int32_t weight_layout, int32_t prologue, int32_t epilogue,
                                             const void* prologue_coef, const void* epilogue_coef,
                                             void* row_partial, int32_t dtype, int32_t blocks_per_sample,
                                             void* stream) {
@@ -1113,16 +1145,19 @@ extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, c
   MEDNEXT_CHECK_ARG(weight_layout == 0 || weight_layout == 1, "weight_layout must be 0 ([M][K]) or 1 ([K][M])");
   MEDNEXT_CHECK_ARG(pro_epi_supported(prologue, epilogue), "unsupported prologue / epilogue combination");
   MEDNEXT_CHECK_ARG(!epi_has_aux(epilogue) || aux != nullptr, "this epilogue needs the aux tensor");
-  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_GELU_AFFINE || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
-                    "the GELU_AFFINE prologue needs 8-byte aligned coefficient records");
-  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_GELU_AFFINE || weight_layout == 0,
-                    "the GELU_AFFINE prologue takes a [M][K] weight");
-  MEDNEXT_CHECK_ARG(epilogue != MEDNEXT_PW_EPILOGUE_AFFINE_GELU_GRAD ||
+  MEDNEXT_CHECK_ARG(epilogue != MEDNEXT_PW_EPILOGUE_AFFINE_SCALE || aux2 != nullptr, "AFFINE_SCALE needs aux2");
+  MEDNEXT_CHECK_ARG(epilogue != MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR || y2 != nullptr, "BIAS_GELU_PAIR needs y2");
+  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_AFFINE || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
+                    "the AFFINE prologue needs 8-byte aligned coefficient records");
+  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_AFFINE || weight_layout == 0,
+                    "the AFFINE prologue takes a [M][K] weight");
+  MEDNEXT_CHECK_ARG(epilogue != MEDNEXT_PW_EPILOGUE_AFFINE_SCALE ||
                         (epilogue_coef != nullptr && aligned(epilogue_coef, 8)),
-                    "the AFFINE_GELU_GRAD epilogue needs 8-byte aligned coefficients");
+                    "the AFFINE_SCALE epilogue needs 8-byte aligned coefficients");
   MEDNEXT_CHECK_ARG(!reduce || (row_partial != nullptr && aligned(row_partial, 8)),
                     "the ROW_REDUCE epilogue needs an 8-byte aligned row_partial buffer");
   MEDNEXT_CHECK_ARG(aligned(x, 2) && (y == nullptr || aligned(y, 2)) && (aux == nullptr || aligned(aux, 2)) &&
+                        (aux2 == nullptr || aligned(aux2, 2)) && (y2 == nullptr || aligned(y2, 2)) &&
                         aligned(weight, 16) && (bias == nullptr || aligned(bias, 2)),
                     "pointwise tensors must be bf16-aligned and the weight 16-byte aligned");
   MEDNEXT_CHECK_ARG(blocks_per_sample >= 0, "blocks_per_sample must be >= 0 (0 = automatic)");
@@ -1133,7 +1168,8 @@ extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, c
   const size_t lds = static_cast<size_t>(16 * mt) * p.g.ks * 32 * 2 + kRowVecs * 16 * mt * sizeof(float) +
                      (p.splitk ? static_cast<size_t>(mt) * 8 * 4 * 64 * sizeof(float) : 0);
   PwExtra ex{static_cast<const double*>(prologue_coef), static_cast<const double*>(epilogue_coef),
-             static_cast<double*>(row_partial), p.slots};
+             static_cast<double*>(row_partial), static_cast<const bf16_t*>(aux2), static_cast<bf16_t*>(y2),
+             p.slots};
   hipLaunchKernelGGL(pick_fwd(k, mt, prologue, epilogue), dim3(static_cast<unsigned>(p.blocks)), dim3(kPwThreads),
                      lds, static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(x),
                      static_cast<const bf16_t*>(weight), static_cast<const bf16_t*>(bias),
@@ -1148,8 +1184,8 @@ extern "C" int32_t mednext_pointwise_fwd(const void* x, const void* weight, cons
                                          int32_t dtype, int32_t blocks_per_sample, void* stream) {
   MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU, "bad prologue");
   MEDNEXT_CHECK_ARG(epilogue >= MEDNEXT_PW_EPILOGUE_BIAS && epilogue <= MEDNEXT_PW_EPILOGUE_GELU_GRAD, "bad epilogue");
-  return mednext_pointwise_fwd_ex(x, weight, bias, aux, y, n, k, m, v, weight_layout, prologue, epilogue, nullptr,
-                                  nullptr, nullptr, dtype, blocks_per_sample, stream);
+  return mednext_pointwise_fwd_ex(x, weight, bias, aux, nullptr, y, nullptr, n, k, m, v, weight_layout, prologue,
+                                  epilogue, nullptr, nullptr, nullptr, dtype, blocks_per_sample, stream);
 }
 
 namespace {
@@ -1183,10 +1219,10 @@ extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const voi
   if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
   MEDNEXT_CHECK_ARG(grad_output != nullptr && x != nullptr && grad_weight != nullptr, "null tensor pointer");
   MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU ||
-                        prologue == MEDNEXT_PW_PROLOGUE_GELU_AFFINE,
+                        prologue == MEDNEXT_PW_PROLOGUE_AFFINE,
                     "bad prologue");
-  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_GELU_AFFINE || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
-                    "the GELU_AFFINE prologue needs 8-byte aligned coefficient records");
+  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_AFFINE || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
+                    "the AFFINE prologue needs 8-byte aligned coefficient records");
   MEDNEXT_CHECK_ARG(splits >= 1 && splits <= 65535, "splits must be in [1, 65535]");
   MEDNEXT_CHECK_ARG(aligned(grad_output, 2) && aligned(x, 2) && aligned(grad_weight, 2) &&
                         (grad_bias == nullptr || aligned(grad_bias, 2)),

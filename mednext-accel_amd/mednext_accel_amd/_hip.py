@@ -61,7 +61,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "mednext_pointwise_fwd_ex": (
         _i32,
-        (_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p),
+        (_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p),
     ),
     "mednext_pointwise_row_slots": (_i64, (_i64, _i64, _i64, _i64, _i32)),
     "mednext_pointwise_wgrad_workspace_bytes": (c_size_t, (_i64, _i64, _i64, _i64, _i32)),
@@ -84,7 +84,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
     "mednext_grn_stats": (
         _i32,
-        (_p, _i32, _i32, _p, _p, _i32, _p, _i64, _i64, _i64, c_double, _i32, _p, c_size_t, _p),
+        (_p, _i32, _p, _p, _i32, _p, _i64, _i64, _i64, c_double, _i32, _p, c_size_t, _p),
     ),
     "mednext_grn_bwd_rows": (
         _i32,

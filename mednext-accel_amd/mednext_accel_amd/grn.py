@@ -122,10 +122,11 @@ class AdaptiveGRNExpansion:
     modules as without it.
     """
 
-    #: Widest hidden layer the fused path takes: the project GEMM recomputes
-    #: GELU and the GRN affine per 32-row output group, which pays while the
-    #: hidden tensor's HBM passes it saves dominate (MI355X, MedNeXt v2 Base).
-    max_hidden = 512
+    #: Widest hidden layer the fused path takes; wider expansions (the
+    #: MedNeXt v2 Base stage-3/4 blocks: small volumes, K >= 2048) run the
+    #: separate operators. Measured on MI355X (v2 Base 128^3 step): 61.4 ms
+    #: unfused, 54.0-56.2 ms up to 512, 53.6-54.1 ms up to 1024, 54.3 ms up to 2048.
+    max_hidden = 1024
 
     def __init__(self, block: nn.Module, resolver: PolicyResolver, model_context: ModelOptimizationContext,
                  *, role: str | None = None) -> None:
@@ -168,7 +169,7 @@ class AdaptiveGRNExpansion:
         b1 = b.expand.bias.to(dt) if b.expand.bias is not None else None
         b2 = b.project.bias.to(dt) if b.project.bias is not None else None
         fuse_residual = residual is not None and residual.dtype == dt and residual.is_contiguous()
-        out, _u, _coef = _hip_ops().grn_expansion(
+        out, _a, _dgelu, _coef = _hip_ops().grn_expansion(
             h.to(dt), w1, b1, w2, b2, b.grn.gamma, b.grn.beta, residual if fuse_residual else None, float(b.grn.eps)
         )
         if residual is not None and not fuse_residual:

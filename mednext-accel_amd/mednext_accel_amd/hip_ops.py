@@ -275,9 +275,9 @@ def group_norm_backward(
 
 # --------------------------------------------------------------------- pointwise
 
-PW_PROLOGUE_NONE, PW_PROLOGUE_GELU, PW_PROLOGUE_GELU_AFFINE = 0, 1, 2
+PW_PROLOGUE_NONE, PW_PROLOGUE_GELU, PW_PROLOGUE_AFFINE = 0, 1, 2
 PW_EPILOGUE_BIAS, PW_EPILOGUE_BIAS_GELU, PW_EPILOGUE_BIAS_RESIDUAL, PW_EPILOGUE_GELU_GRAD = 0, 1, 2, 3
-PW_EPILOGUE_ROW_REDUCE, PW_EPILOGUE_AFFINE_GELU_GRAD = 4, 5
+PW_EPILOGUE_ROW_REDUCE, PW_EPILOGUE_AFFINE_SCALE, PW_EPILOGUE_BIAS_GELU_PAIR = 4, 5, 6
 
 
 def _weight2d(weight: Tensor) -> Tensor:
@@ -308,16 +308,19 @@ def pointwise_conv(
     prologue_coef: Tensor | None = None,
     epilogue_coef: Tensor | None = None,
     row_partial: Tensor | None = None,
-) -> Tensor | None:
+    aux2: Tensor | None = None,
+) -> Tensor | tuple[Tensor, Tensor] | None:
     """``y = epilogue(W . prologue(x) [+ b])`` per sample on the matrix cores.
 
     ``weight`` is the conv's [Cout, Cin(, 1, 1, 1)]; with ``transpose=True`` the
-    product is ``W^T . x`` (the conv's input gradient). ``aux`` is the residual
-    (BIAS_RESIDUAL) or the GELU pre-activation (GELU_GRAD, ROW_REDUCE,
-    AFFINE_GELU_GRAD), shaped like ``y``. ``prologue_coef`` ([N, K, 4] float64)
-    feeds GELU_AFFINE, ``epilogue_coef`` ([N, M, 2] float64) AFFINE_GELU_GRAD;
-    ROW_REDUCE writes ``row_partial`` ([N, M, slots, 2] float64, slots from
-    ``pointwise_row_slots``) and returns None.
+    product is ``W^T . x`` (the conv's input gradient). ``aux`` (and ``aux2``
+    for AFFINE_SCALE) are per-element operands shaped like ``y``: the residual
+    (BIAS_RESIDUAL), the GELU pre-activation (GELU_GRAD), the row-sum weights
+    (ROW_REDUCE). ``prologue_coef`` ([N, K, 4] float64) feeds AFFINE,
+    ``epilogue_coef`` ([N, M, 2] float64) AFFINE_SCALE. ROW_REDUCE writes
+    ``row_partial`` ([N, M, slots, 2] float64, slots from
+    ``pointwise_row_slots``) and returns None; BIAS_GELU_PAIR returns
+    ``(GELU(y), GELU'(y))``.
     """
     _check_device(x, weight)
     _check_pointwise_tensor(x, "x")
@@ -331,14 +334,16 @@ def pointwise_conv(
     n, v = x.shape[0], x[0, 0].numel()
     out_shape = (n, m, *x.shape[2:])
     y = None if epilogue == PW_EPILOGUE_ROW_REDUCE else x.new_empty(out_shape)
+    y2 = x.new_empty(out_shape) if epilogue == PW_EPILOGUE_BIAS_GELU_PAIR else None
     if bias is not None:
         if bias.shape != (m,) or bias.dtype != torch.bfloat16:
             raise ValueError("bias must be a bfloat16 [Cout] tensor")
         bias = bias.contiguous()
-    if aux is not None:
-        _check_pointwise_tensor(aux, "aux")
-        if tuple(aux.shape) != out_shape:
-            raise ValueError("aux must have the output's shape")
+    for t, name in ((aux, "aux"), (aux2, "aux2")):
+        if t is not None:
+            _check_pointwise_tensor(t, name)
+            if tuple(t.shape) != out_shape:
+                raise ValueError(f"{name} must have the output's shape")
     if blocks is None:
         blocks = pointwise_blocks(n, k, m, v)
     if epilogue == PW_EPILOGUE_ROW_REDUCE:
@@ -351,14 +356,14 @@ def pointwise_conv(
     lib = _hip.load()
     _hip.check(
         lib.mednext_pointwise_fwd_ex(
-            x.data_ptr(), w2.data_ptr(), _hip.ptr(bias), _hip.ptr(aux), _hip.ptr(y),
+            x.data_ptr(), w2.data_ptr(), _hip.ptr(bias), _hip.ptr(aux), _hip.ptr(aux2), _hip.ptr(y), _hip.ptr(y2),
             n, k, m, v, 1 if transpose else 0, prologue, epilogue, _hip.ptr(prologue_coef),
             _hip.ptr(epilogue_coef), _hip.ptr(row_partial), _hip.DTYPE_CODES[torch.bfloat16],
             int(blocks), _hip.stream_of(x),
         ),
         "mednext_pointwise_fwd_ex",
     )
-    return y
+    return (y, y2) if y2 is not None else y
 
 
 @functools.lru_cache(maxsize=4096)
@@ -380,7 +385,7 @@ def pointwise_weight_grad(
     prologue_coef: Tensor | None = None,
 ) -> tuple[Tensor, Tensor | None]:
     """(dW [Cout, Cin, 1, 1, 1], dB [Cout] or None) of ``y = W . prologue(x) + b``
-    (``prologue_coef`` as for ``pointwise_conv``'s GELU_AFFINE)."""
+    (``prologue_coef`` as for ``pointwise_conv``'s AFFINE)."""
     _check_device(grad_output, x)
     _check_pointwise_tensor(grad_output, "grad_output")
     _check_pointwise_tensor(x, "x")
@@ -1108,12 +1113,10 @@ def fused_global_response_norm3d(x: Tensor, gamma: Tensor, beta: Tensor, eps: fl
 
 
 def grn_stats(
-    x: Tensor, gamma: Tensor | None, beta: Tensor | None, eps: float = 1e-6, *, gelu_input: bool = False,
-    splits: int | None = None,
+    x: Tensor, gamma: Tensor | None, beta: Tensor | None, eps: float = 1e-6, *, splits: int | None = None
 ) -> Tensor:
-    """GRN coefficients [N, C, 4] float64 = (1 + gamma r, beta, r, ||y_c||) of
-    y = x, or of y = bf16(GELU(x)) with ``gelu_input`` (bf16 x): the forward's
-    statistics without its output tensor."""
+    """GRN coefficients [N, C, 4] float64 = (1 + gamma r, beta, r, ||x_c||):
+    the forward's statistics without its output tensor."""
     _check_device(x)
     if x.ndim != 5 or not x.is_contiguous() or x.numel() == 0:
         raise ValueError("a nonempty contiguous NCDHW input is required")
@@ -1131,7 +1134,7 @@ def grn_stats(
     workspace = torch.empty((max(8, nbytes),), device=x.device, dtype=torch.uint8)
     _hip.check(
         lib.mednext_grn_stats(
-            x.data_ptr(), _hip.dtype_code(x.dtype), 1 if gelu_input else 0, _hip.ptr(gamma), _hip.ptr(beta),
+            x.data_ptr(), _hip.dtype_code(x.dtype), _hip.ptr(gamma), _hip.ptr(beta),
             _hip.dtype_code(pdtype), coef.data_ptr(), n, c, v, float(eps), splits, workspace.data_ptr(), nbytes,
             _hip.stream_of(x),
         ),
@@ -1180,25 +1183,25 @@ def grn_expansion(
     beta: Tensor,
     residual: Tensor | None,
     eps: float,
-) -> tuple[Tensor, Tensor, Tensor]:
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     """MedNeXt v2 block expansion, fused: ``out = W2 . GRN(GELU(W1 . x + b1)) +
     b2 (+ residual)`` (reference models/blocks_v2.py:44-45 with the GRN of
     ops/grn.py:16-30 and the residual add of :48-55).
 
-    Returns ``(out, u, coef)``: ``u = W1 . x + b1`` (bf16) is the only hidden
-    tensor written; the GRN statistics of bf16(GELU(u)) come from one read of
-    it, and the project GEMM applies GELU and the GRN affine to u as it loads
-    it. ``coef`` [N, hidden, 4] float64 holds (1 + gamma r, beta, r, norm)."""
+    Returns ``(out, a, dgelu, coef)``: the expand GEMM writes a = GELU(u) and
+    dgelu = GELU'(u) (u = W1 . x + b1, bf16; the backward needs nothing else of
+    u), the GRN statistics of a come from one read of it, and the project GEMM
+    applies the GRN affine as it loads a (no GRN output tensor).
+    ``coef`` [N, hidden, 4] float64 holds (1 + gamma r, beta, r, norm)."""
     x = x.contiguous()
-    u = pointwise_conv(x, w1, b1, epilogue=PW_EPILOGUE_BIAS)
-    coef = grn_stats(u, gamma, beta, eps, gelu_input=True)
+    a, dgelu = pointwise_conv(x, w1, b1, epilogue=PW_EPILOGUE_BIAS_GELU_PAIR)
+    coef = grn_stats(a, gamma, beta, eps)
     if residual is None:
-        out = pointwise_conv(u, w2, b2, prologue=PW_PROLOGUE_GELU_AFFINE, epilogue=PW_EPILOGUE_BIAS,
-                             prologue_coef=coef)
+        out = pointwise_conv(a, w2, b2, prologue=PW_PROLOGUE_AFFINE, epilogue=PW_EPILOGUE_BIAS, prologue_coef=coef)
     else:
-        out = pointwise_conv(u, w2, b2, aux=residual.contiguous(), prologue=PW_PROLOGUE_GELU_AFFINE,
+        out = pointwise_conv(a, w2, b2, aux=residual.contiguous(), prologue=PW_PROLOGUE_AFFINE,
                              epilogue=PW_EPILOGUE_BIAS_RESIDUAL, prologue_coef=coef)
-    return out, u, coef
+    return out, a, dgelu, coef
 
 
 @grn_expansion.register_fake
@@ -1207,41 +1210,43 @@ def _(x, w1, b1, w2, b2, gamma, beta, residual, eps):
     return (
         x.new_empty((x.shape[0], w2.shape[0], *x.shape[2:])),
         x.new_empty(shape),
+        x.new_empty(shape),
         x.new_empty((x.shape[0], w1.shape[0], 4), dtype=torch.float64),
     )
 
 
 @torch.library.custom_op("mednext_accel_amd::grn_expansion_backward", mutates_args=())
 def grn_expansion_backward(
-    grad_out: Tensor, x: Tensor, u: Tensor, coef: Tensor, w1: Tensor, w2: Tensor, gamma: Tensor, eps: float
+    grad_out: Tensor, x: Tensor, a: Tensor, dgelu: Tensor, coef: Tensor, w1: Tensor, w2: Tensor, gamma: Tensor,
+    eps: float,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
     """(dx, dW1, db1, dW2, db2, dgamma, dbeta) of ``grn_expansion``. With
-    a = bf16(GELU(u)), z = GRN(a) and dz = W2^T . dout (never stored):
-    one transposed GEMM reduces the GRN row sums (sum dz * a, sum dz), a small
-    kernel turns them into the per-(n, c) GRN backward coefficients and the
-    gamma / beta gradients, a second transposed GEMM writes
-    du = (dz k1 + a k2) * GELU'(u); dW2 = dout . z^T reads u through the
-    GELU + GRN prologue; dW1 = du . x^T and dx = W1^T . du as for any conv."""
+    z = GRN(a) and dz = W2^T . dout (never stored): one transposed GEMM reduces
+    the GRN row sums (sum dz * a, sum dz), a small kernel turns them into the
+    per-(n, c) GRN backward coefficients (k1, k2) and the gamma / beta
+    gradients, a second transposed GEMM writes du = (dz k1 + a k2) * GELU'(u);
+    dW2 = dout . z^T reads a through the GRN affine prologue; dW1 = du . x^T
+    and dx = W1^T . du as for any conv."""
     grad_out = grad_out.contiguous()
-    n, hidden = int(u.shape[0]), int(u.shape[1])
-    v = u[0, 0].numel()
+    n, hidden = int(a.shape[0]), int(a.shape[1])
+    v = a[0, 0].numel()
     cout = int(grad_out.shape[1])
     blocks = pointwise_blocks(n, cout, hidden, v)
     slots = pointwise_row_slots(n, cout, hidden, v, int(blocks))
-    rows = torch.empty((n, hidden, slots, 2), device=u.device, dtype=torch.float64)
-    pointwise_conv(grad_out, w2, aux=u, epilogue=PW_EPILOGUE_ROW_REDUCE, transpose=True, blocks=blocks,
+    rows = torch.empty((n, hidden, slots, 2), device=a.device, dtype=torch.float64)
+    pointwise_conv(grad_out, w2, aux=a, epilogue=PW_EPILOGUE_ROW_REDUCE, transpose=True, blocks=blocks,
                    row_partial=rows)
     bcoef, dgamma, dbeta = grn_backward_from_rows(rows, coef, gamma, eps)
-    du = pointwise_conv(grad_out, w2, aux=u, epilogue=PW_EPILOGUE_AFFINE_GELU_GRAD, transpose=True,
+    du = pointwise_conv(grad_out, w2, aux=a, aux2=dgelu, epilogue=PW_EPILOGUE_AFFINE_SCALE, transpose=True,
                         epilogue_coef=bcoef)
-    dw2, db2 = pointwise_weight_grad(grad_out, u, prologue=PW_PROLOGUE_GELU_AFFINE, prologue_coef=coef)
+    dw2, db2 = pointwise_weight_grad(grad_out, a, prologue=PW_PROLOGUE_AFFINE, prologue_coef=coef)
     dw1, db1 = pointwise_weight_grad(du, x.contiguous())
     dx = pointwise_conv(du, w1, transpose=True)
     return dx, dw1, db1, dw2, db2, dgamma, dbeta
 
 
 @grn_expansion_backward.register_fake
-def _(grad_out, x, u, coef, w1, w2, gamma, eps):
+def _(grad_out, x, a, dgelu, coef, w1, w2, gamma, eps):
     return (
         torch.empty_like(x),
         w1.new_empty(w1.shape),
@@ -1255,19 +1260,21 @@ def _(grad_out, x, u, coef, w1, w2, gamma, eps):
 
 def _setup_grn_expansion(ctx, inputs, output):
     x, w1, b1, w2, b2, gamma, beta, residual, eps = inputs
-    _out, u, coef = output
-    ctx.mark_non_differentiable(u, coef)
+    _out, a, dgelu, coef = output
+    ctx.mark_non_differentiable(a, dgelu, coef)
     ctx.set_materialize_grads(False)
-    ctx.save_for_backward(x, u, coef, w1, w2, gamma)
+    ctx.save_for_backward(x, a, dgelu, coef, w1, w2, gamma)
     ctx.eps = eps
     ctx.has_b1, ctx.has_b2, ctx.has_residual = b1 is not None, b2 is not None, residual is not None
 
 
-def _grn_expansion_backward(ctx, grad_out, _grad_u, _grad_coef):
+def _grn_expansion_backward(ctx, grad_out, _grad_a, _grad_dgelu, _grad_coef):
     if grad_out is None:
         return (None,) * 9
-    x, u, coef, w1, w2, gamma = ctx.saved_tensors
-    dx, dw1, db1, dw2, db2, dgamma, dbeta = grn_expansion_backward(grad_out, x, u, coef, w1, w2, gamma, ctx.eps)
+    x, a, dgelu, coef, w1, w2, gamma = ctx.saved_tensors
+    dx, dw1, db1, dw2, db2, dgamma, dbeta = grn_expansion_backward(
+        grad_out, x, a, dgelu, coef, w1, w2, gamma, ctx.eps
+    )
     return (
         dx,
         dw1,

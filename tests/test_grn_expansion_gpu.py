@@ -1,6 +1,6 @@
 """Fused MedNeXt v2 block expansion on the GPU: ``out = W2 . GRN(GELU(W1 . x +
 b1)) + b2 (+ residual)`` with GELU and GRN folded into the matrix-core GEMMs
-(hip_ops.grn_expansion), and each new GEMM mode on its own.
+(hip_ops.grn_expansion), and each GEMM mode it uses on its own.
 
 Ground truth is the same chain in float64 on the same bf16 inputs (reference
 models/blocks_v2.py:44-45 with ops/grn.py:16-30). The bar is the bf16
@@ -50,6 +50,7 @@ CASES = [
     (1, 64, 256, 64, (16, 16, 16), True),   # v2 stage 1: split-K project
     (2, 8, 40, 12, (7, 9, 11), False),      # odd widths and volume, no residual
     (1, 32, 128, 64, (12, 12, 12), False),  # down-block shape: Cout = 2 C
+    (1, 128, 1024, 128, (16, 16, 16), True),  # v2 stage 2: split-K project, K = 128 backward GEMMs
 ]
 
 
@@ -60,8 +61,8 @@ def test_fused_expansion_matches_float64_chain(n, c, hidden, cout, spatial, resi
     leaves = [t.clone().requires_grad_() for t in (x, w1, b1, w2, b2, gamma, beta)] + (
         [res.clone().requires_grad_()] if residual else [])
     hip_in = leaves
-    out, u, coef = P.grn_expansion(*hip_in[:7], hip_in[7] if residual else None, 1e-6)
-    assert out.dtype == torch.bfloat16 and u.dtype == torch.bfloat16 and coef.dtype == torch.float64
+    out, a, dgelu, coef = P.grn_expansion(*hip_in[:7], hip_in[7] if residual else None, 1e-6)
+    assert out.dtype == a.dtype == dgelu.dtype == torch.bfloat16 and coef.dtype == torch.float64
     # reference path: the unfused chain under bf16 autocast (fp32 GRN parameters)
     ref_in = [t.detach().float().clone().requires_grad_() if i in (5, 6) else t.detach().clone().requires_grad_()
               for i, t in enumerate(leaves)]
@@ -85,7 +86,7 @@ def test_fused_expansion_is_bit_reproducible():
     runs = []
     for _ in range(2):
         leaves = [t.clone().requires_grad_() for t in (x, w1, b1, w2, b2, gamma, beta)]
-        out, _, _ = P.grn_expansion(*leaves, res, 1e-6)
+        out, _, _, _ = P.grn_expansion(*leaves, res, 1e-6)
         grads = torch.autograd.grad(out, leaves, torch.ones_like(out))
         runs.append((out, *grads))
     for a, b in zip(*runs):
@@ -96,65 +97,78 @@ def test_row_reduce_epilogue_matches_torch():
     torch.manual_seed(11)
     n, k, m, s = 2, 32, 96, 20
     dy = torch.randn(n, k, s, s, s, device=DEV).bfloat16()
-    u = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
+    a = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
     w = (torch.randn(k, m, 1, 1, 1, device=DEV) / m**0.5).bfloat16()  # conv weight [Cout=k][Cin=m]
     v = s**3
     slots = P.pointwise_row_slots(n, k, m, v, 0)
     rows = torch.empty(n, m, slots, 2, device=DEV, dtype=torch.float64)
-    assert P.pointwise_conv(dy, w, aux=u, epilogue=P.PW_EPILOGUE_ROW_REDUCE, transpose=True, row_partial=rows) is None
+    assert P.pointwise_conv(dy, w, aux=a, epilogue=P.PW_EPILOGUE_ROW_REDUCE, transpose=True, row_partial=rows) is None
     dz = torch.einsum("km,nkv->nmv", w.double().view(k, m), dy.double().view(n, k, v))
-    a = F.gelu(u.float()).bfloat16().double().view(n, m, v)
     sums = rows.sum(dim=2)
-    assert max_rel(sums[..., 0], (dz * a).sum(-1)) <= 1e-5
+    assert max_rel(sums[..., 0], (dz * a.double().view(n, m, v)).sum(-1)) <= 1e-5
     assert max_rel(sums[..., 1], dz.sum(-1)) <= 1e-5
 
 
-def test_affine_gelu_grad_epilogue_matches_torch():
+@pytest.mark.parametrize("k,m,s", [(64, 256, 12), (32, 96, 9), (96, 192, 8), (128, 64, 8), (320, 40, 6)])
+def test_affine_scale_epilogue_matches_torch(k, m, s):
     torch.manual_seed(12)
-    n, k, m, s = 1, 64, 256, 12
+    n = 2
     dy = torch.randn(n, k, s, s, s, device=DEV).bfloat16()
-    u = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
+    a = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
+    d = torch.rand(n, m, s, s, s, device=DEV).bfloat16()
     w = (torch.randn(k, m, 1, 1, 1, device=DEV) / m**0.5).bfloat16()
     c = torch.randn(n, m, 2, device=DEV, dtype=torch.float64)
-    du = P.pointwise_conv(dy, w, aux=u, epilogue=P.PW_EPILOGUE_AFFINE_GELU_GRAD, transpose=True, epilogue_coef=c)
+    du = P.pointwise_conv(dy, w, aux=a, aux2=d, epilogue=P.PW_EPILOGUE_AFFINE_SCALE, transpose=True,
+                          epilogue_coef=c)
     v = s**3
     dz = torch.einsum("km,nkv->nmv", w.double().view(k, m), dy.double().view(n, k, v))
-    uu = u.double().view(n, m, v).requires_grad_()
-    (dg,) = torch.autograd.grad(F.gelu(uu).sum(), uu)
-    a = F.gelu(u.float()).bfloat16().double().view(n, m, v)
-    want = (dz * c[..., :1] + a * c[..., 1:]) * dg
+    want = (dz * c[..., :1] + a.double().view(n, m, v) * c[..., 1:]) * d.double().view(n, m, v)
     assert rel_l2(du.view(n, m, v), want) <= 8e-3
 
 
-def test_gelu_affine_prologue_forward_and_weight_grad():
+@pytest.mark.parametrize("k,m,s", [(32, 96, 20), (64, 256, 10), (8, 40, 7)])
+def test_bias_gelu_pair_epilogue_matches_torch(k, m, s):
+    torch.manual_seed(15)
+    n = 2
+    x = torch.randn(n, k, s, s, s, device=DEV).bfloat16()
+    w = (torch.randn(m, k, 1, 1, 1, device=DEV) / k**0.5).bfloat16()
+    b = (torch.randn(m, device=DEV) * 0.3).bfloat16()
+    g, dg = P.pointwise_conv(x, w, b, epilogue=P.PW_EPILOGUE_BIAS_GELU_PAIR)
+    u = (F.conv3d(x.double(), w.double(), b.double())).requires_grad_()
+    want = F.gelu(u)
+    (want_d,) = torch.autograd.grad(want.sum(), u)
+    assert rel_l2(g, want) <= 8e-3
+    assert rel_l2(dg, want_d) <= 8e-3
+
+
+def test_affine_prologue_forward_and_weight_grad():
     torch.manual_seed(13)
     n, k, m, s = 2, 96, 32, 16
-    u = torch.randn(n, k, s, s, s, device=DEV).bfloat16()
+    a = torch.randn(n, k, s, s, s, device=DEV).bfloat16()
     w = (torch.randn(m, k, 1, 1, 1, device=DEV) / k**0.5).bfloat16()
     b = (torch.randn(m, device=DEV) * 0.1).bfloat16()
     coef = torch.randn(n, k, 4, device=DEV, dtype=torch.float64)
     coef[..., 0] = 1 + 0.3 * coef[..., 0]
-    y = P.pointwise_conv(u, w, b, prologue=P.PW_PROLOGUE_GELU_AFFINE, prologue_coef=coef)
+    y = P.pointwise_conv(a, w, b, prologue=P.PW_PROLOGUE_AFFINE, prologue_coef=coef)
     v = s**3
-    z = F.gelu(u.float()).bfloat16().double().view(n, k, v) * coef[..., :1] + coef[..., 1:2]
+    z = a.double().view(n, k, v) * coef[..., :1] + coef[..., 1:2]
     want = torch.einsum("mk,nkv->nmv", w.double().view(m, k), z) + b.double()[None, :, None]
     assert rel_l2(y.view(n, m, v), want) <= 8e-3
     dy = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
-    dw, db = P.pointwise_weight_grad(dy, u, prologue=P.PW_PROLOGUE_GELU_AFFINE, prologue_coef=coef)
-    zb = z.bfloat16().double()  # the weight gradient rounds a * s + t per element
+    dw, db = P.pointwise_weight_grad(dy, a, prologue=P.PW_PROLOGUE_AFFINE, prologue_coef=coef)
+    zb = z.bfloat16().double()  # the weight gradient rounds x * s + t per element
     want_dw = torch.einsum("nmv,nkv->mk", dy.double().view(n, m, v), zb)
     assert rel_l2(dw.view(m, k), want_dw) <= 8e-3
     assert rel_l2(db, dy.double().sum(dim=(0, 2, 3, 4))) <= 8e-3
 
 
-def test_grn_stats_of_gelu_input():
+def test_grn_stats_match_torch():
     torch.manual_seed(14)
-    u = torch.randn(2, 48, 10, 11, 12, device=DEV).bfloat16()
+    x = torch.randn(2, 48, 10, 11, 12, device=DEV).bfloat16()
     gamma = torch.randn(48, device=DEV)
     beta = torch.randn(48, device=DEV)
-    coef = P.grn_stats(u, gamma, beta, 1e-6, gelu_input=True)
-    a = F.gelu(u.float()).bfloat16().double()
-    norms = a.flatten(2).norm(dim=2)
+    coef = P.grn_stats(x, gamma, beta, 1e-6)
+    norms = x.double().flatten(2).norm(dim=2)
     r = norms / (norms.sum(dim=1, keepdim=True) + 1e-6)
     assert max_rel(coef[..., 3], norms) <= 1e-6
     assert max_rel(coef[..., 2], r) <= 1e-6
