@@ -190,6 +190,8 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
  *                  (c0, c1) = epilogue_coef[(n * M + m) * 2 + {0, 1}] (fp64;
  *                  bias unused)
  *   BIAS_GELU_PAIR: y = GELU(acc + bias[m]) and y2 = GELU'(acc + bias[m])
+ *   AUX_SCALE:     y = acc * aux[n][m][v]   (bias unused; with aux = GELU'(h)
+ *                  stored by BIAS_GELU_PAIR, the input gradient through GELU)
  */
 enum mednext_pw_prologue {
   MEDNEXT_PW_PROLOGUE_NONE = 0,
@@ -203,7 +205,8 @@ enum mednext_pw_epilogue {
   MEDNEXT_PW_EPILOGUE_GELU_GRAD = 3,
   MEDNEXT_PW_EPILOGUE_ROW_REDUCE = 4,
   MEDNEXT_PW_EPILOGUE_AFFINE_SCALE = 5,
-  MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR = 6
+  MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR = 6,
+  MEDNEXT_PW_EPILOGUE_AUX_SCALE = 7
 };
 
 /* y = epilogue(op(W) . prologue(x)); blocks_per_sample = workgroups along V

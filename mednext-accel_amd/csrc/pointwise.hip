@@ -89,7 +89,8 @@ constexpr bool epi_has_bias(int epi) {
 
 constexpr bool epi_has_aux(int epi) {
   return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epi == MEDNEXT_PW_EPILOGUE_GELU_GRAD ||
-         epi == MEDNEXT_PW_EPILOGUE_ROW_REDUCE || epi == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE;
+         epi == MEDNEXT_PW_EPILOGUE_ROW_REDUCE || epi == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE ||
+         epi == MEDNEXT_PW_EPILOGUE_AUX_SCALE;
 }
 
 // Per-row LDS vectors after the weight block: bias, then the AFFINE_SCALE
@@ -153,6 +154,9 @@ __device__ inline void epilogue_values(float (&v)[8], float (&v2)[8], const uint
   } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_GELU_GRAD) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] *= gelu_grad_f(bf16_at(av, j));
+  } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AUX_SCALE) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] *= bf16_at(av, j);
   } else if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = fmaf(v[j], c0, bf16_at(av, j) * c1) * bf16_at(av2, j);
@@ -965,7 +969,7 @@ constexpr int kSplitKSlices = 8;  // K >= 256: the four waves of a workgroup spl
 // Supported (prologue, epilogue) pairs: NONE with any epilogue, GELU with
 // BIAS .. GELU_GRAD, AFFINE with BIAS or BIAS_RESIDUAL.
 bool pro_epi_supported(int pro, int epi) {
-  if (pro == MEDNEXT_PW_PROLOGUE_NONE) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR;
+  if (pro == MEDNEXT_PW_PROLOGUE_NONE) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_AUX_SCALE;
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_GELU_GRAD;
   if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) return epi == MEDNEXT_PW_EPILOGUE_BIAS || epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL;
   return false;
@@ -991,7 +995,8 @@ FwdKernel splitk_instance(int pro, int epi) {
     case MEDNEXT_PW_EPILOGUE_GELU_GRAD: return pw_fwd_splitk_kernel<MT, 0, 3>;
     case MEDNEXT_PW_EPILOGUE_ROW_REDUCE: return pw_fwd_splitk_kernel<MT, 0, 4>;
     case MEDNEXT_PW_EPILOGUE_AFFINE_SCALE: return pw_fwd_splitk_kernel<MT, 0, 5>;
-    default: return pw_fwd_splitk_kernel<MT, 0, 6>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR: return pw_fwd_splitk_kernel<MT, 0, 6>;
+    default: return pw_fwd_splitk_kernel<MT, 0, 7>;
   }
 }
 
@@ -1026,7 +1031,8 @@ FwdKernel fwd_instance(int pro, int epi) {
     case MEDNEXT_PW_EPILOGUE_GELU_GRAD: return pw_fwd_kernel<KS, MT, 0, 3>;
     case MEDNEXT_PW_EPILOGUE_ROW_REDUCE: return pw_fwd_kernel<KS, MT, 0, 4>;
     case MEDNEXT_PW_EPILOGUE_AFFINE_SCALE: return pw_fwd_kernel<KS, MT, 0, 5>;
-    default: return pw_fwd_kernel<KS, MT, 0, 6>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR: return pw_fwd_kernel<KS, MT, 0, 6>;
+    default: return pw_fwd_kernel<KS, MT, 0, 7>;
   }
 }
 

@@ -277,7 +277,7 @@ def group_norm_backward(
 
 PW_PROLOGUE_NONE, PW_PROLOGUE_GELU, PW_PROLOGUE_AFFINE = 0, 1, 2
 PW_EPILOGUE_BIAS, PW_EPILOGUE_BIAS_GELU, PW_EPILOGUE_BIAS_RESIDUAL, PW_EPILOGUE_GELU_GRAD = 0, 1, 2, 3
-PW_EPILOGUE_ROW_REDUCE, PW_EPILOGUE_AFFINE_SCALE, PW_EPILOGUE_BIAS_GELU_PAIR = 4, 5, 6
+PW_EPILOGUE_ROW_REDUCE, PW_EPILOGUE_AFFINE_SCALE, PW_EPILOGUE_BIAS_GELU_PAIR, PW_EPILOGUE_AUX_SCALE = 4, 5, 6, 7
 
 
 def _weight2d(weight: Tensor) -> Tensor:
@@ -767,6 +767,83 @@ def _mlp_backward(ctx, grad_out, _grad_h):
 
 
 mlp_expansion.register_autograd(_mlp_backward, setup_context=_setup_mlp)
+
+
+@torch.library.custom_op("mednext_accel_amd::mlp_expansion_stored", mutates_args=())
+def mlp_expansion_stored(
+    x: Tensor, w1: Tensor, b1: Tensor | None, w2: Tensor, b2: Tensor | None, residual: Tensor | None
+) -> tuple[Tensor, Tensor, Tensor]:
+    """``mlp_expansion`` with GELU evaluated once: the expand GEMM writes
+    ``a = GELU(h)`` and ``dgelu = GELU'(h)`` (bf16) instead of h, the project
+    GEMM reads a as it is, and the backward needs no GELU at all (its input
+    gradient multiplies by the stored GELU'). Returns ``(out, a, dgelu)``.
+    Pays where the recomputing variant evaluates GELU once per 32-row output
+    group of a wide project GEMM."""
+    x = x.contiguous()
+    a, dgelu = pointwise_conv(x, w1, b1, epilogue=PW_EPILOGUE_BIAS_GELU_PAIR)
+    if residual is None:
+        out = pointwise_conv(a, w2, b2, epilogue=PW_EPILOGUE_BIAS)
+    else:
+        out = pointwise_conv(a, w2, b2, aux=residual.contiguous(), epilogue=PW_EPILOGUE_BIAS_RESIDUAL)
+    return out, a, dgelu
+
+
+@mlp_expansion_stored.register_fake
+def _(x, w1, b1, w2, b2, residual):
+    h = x.new_empty((x.shape[0], w1.shape[0], *x.shape[2:]))
+    return x.new_empty((x.shape[0], w2.shape[0], *x.shape[2:])), h, torch.empty_like(h)
+
+
+@torch.library.custom_op("mednext_accel_amd::mlp_expansion_stored_backward", mutates_args=())
+def mlp_expansion_stored_backward(
+    grad_out: Tensor, x: Tensor, a: Tensor, dgelu: Tensor, w1: Tensor, w2: Tensor
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dx, dW1, db1, dW2, db2) of ``mlp_expansion_stored``:
+    dh = (W2^T . dout) * GELU'(h); dW2 = dout . a^T; dW1 = dh . x^T; dx = W1^T . dh."""
+    grad_out = grad_out.contiguous()
+    dh = pointwise_conv(grad_out, w2, aux=dgelu, epilogue=PW_EPILOGUE_AUX_SCALE, transpose=True)
+    dw2, db2 = pointwise_weight_grad(grad_out, a)
+    dw1, db1 = pointwise_weight_grad(dh, x.contiguous())
+    dx = pointwise_conv(dh, w1, transpose=True)
+    return dx, dw1, db1, dw2, db2
+
+
+@mlp_expansion_stored_backward.register_fake
+def _(grad_out, x, a, dgelu, w1, w2):
+    return (
+        torch.empty_like(x),
+        w1.new_empty(w1.shape),
+        w1.new_empty((w1.shape[0],)),
+        w2.new_empty(w2.shape),
+        w2.new_empty((w2.shape[0],)),
+    )
+
+
+def _setup_mlp_stored(ctx, inputs, output):
+    x, w1, b1, w2, b2, residual = inputs
+    _out, a, dgelu = output
+    ctx.mark_non_differentiable(a, dgelu)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(x, a, dgelu, w1, w2)
+    ctx.has_b1, ctx.has_b2, ctx.has_residual = b1 is not None, b2 is not None, residual is not None
+
+
+def _mlp_stored_backward(ctx, grad_out, _grad_a, _grad_dgelu):
+    if grad_out is None:
+        return None, None, None, None, None, None
+    x, a, dgelu, w1, w2 = ctx.saved_tensors
+    dx, dw1, db1, dw2, db2 = mlp_expansion_stored_backward(grad_out, x, a, dgelu, w1, w2)
+    return (
+        dx,
+        dw1,
+        db1 if ctx.has_b1 else None,
+        dw2,
+        db2 if ctx.has_b2 else None,
+        grad_out if ctx.has_residual else None,
+    )
+
+
+mlp_expansion_stored.register_autograd(_mlp_stored_backward, setup_context=_setup_mlp_stored)
 
 
 # ------------------------------------------------------------ stride-2 depthwise

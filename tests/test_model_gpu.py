@@ -37,6 +37,7 @@ DX_OP = "mednext_accel_amd::depthwise_input_grad_odd_regular"
 DWG_OP = "mednext_accel_amd::depthwise_weight_grad_odd_regular"
 GN_OP = "mednext_accel_amd::group_norm_channels"
 MLP_OP = "mednext_accel_amd::mlp_expansion"
+MLP_STORED_OP = "mednext_accel_amd::mlp_expansion_stored"
 
 
 class Observe(TorchDispatchMode):
@@ -172,7 +173,7 @@ def test_block_cfg2_bf16_autocast_matches_reference_block(channels, size, ratio)
         want = ref(x)
         with Observe() as seen:
             got = cand(y)
-    assert DW_OP in seen.ops and GN_OP in seen.ops and MLP_OP in seen.ops
+    assert DW_OP in seen.ops and GN_OP in seen.ops and (MLP_OP in seen.ops or MLP_STORED_OP in seen.ops)
     exact = truth(z)
     g = torch.randn_like(want)
     wants = torch.autograd.grad(want, (x, *ref.parameters()), g)
@@ -222,7 +223,7 @@ def test_base_training_step_128_bf16_matches_reference():
         losses.append(float(loss))
         if model is cand:
             assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops and GN_OP in seen.ops
-            assert MLP_OP in seen.ops
+            assert MLP_OP in seen.ops and MLP_STORED_OP in seen.ops
         del step
     assert abs(losses[0] - losses[1]) / abs(losses[1]) < BF16
     for (name, p), q in zip(cand.named_parameters(), ref.parameters(), strict=True):
@@ -253,7 +254,8 @@ def test_large_k5_checkpointed_step_matches_reference():
         losses.append(float(loss.detach()))
         norms.append(torch.stack([p.grad.float().norm() for p in model.parameters()]))
         if model is cand:
-            assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops and MLP_OP in seen.ops
+            assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops
+            assert MLP_OP in seen.ops and MLP_STORED_OP in seen.ops
         del step
     assert abs(losses[0] - losses[1]) / abs(losses[1]) < BF16
     assert torch.isfinite(norms[0]).all()

@@ -149,12 +149,14 @@ def test_stage_shapes_against_torch_fp32(cin, cout, size):
     assert max_rel(db, rdb) <= BF16
 
 
-@pytest.mark.parametrize("residual", [True, False])
-def test_fused_mlp_expansion_matches_unfused_fp32(residual):
-    """mlp_expansion = project(GELU(expand(x))) + residual, fwd + bwd, vs the
-    same composition in fp32 PyTorch on the bf16-rounded operands."""
+@pytest.mark.parametrize("stored", [False, True])
+@pytest.mark.parametrize("residual,c,r,s", [(True, 32, 2, 32), (False, 32, 2, 32), (True, 64, 3, 20), (True, 96, 4, 9)])
+def test_fused_mlp_expansion_matches_unfused_fp32(residual, c, r, s, stored):
+    """mlp_expansion (GELU recomputed from h) and mlp_expansion_stored (GELU
+    and GELU' stored by the expand GEMM) = project(GELU(expand(x))) + residual,
+    fwd + bwd, vs the same composition in fp32 PyTorch on the bf16-rounded
+    operands."""
     gen = torch.Generator(device=DEV).manual_seed(2)
-    c, r, s = 32, 2, 32
     x = torch.randn(1, c, s, s, s, generator=gen, device=DEV).bfloat16()
     res = torch.randn(1, c, s, s, s, generator=gen, device=DEV).bfloat16()
     w1 = (torch.randn(r * c, c, 1, 1, 1, generator=gen, device=DEV) * c**-0.5).bfloat16()
@@ -162,7 +164,8 @@ def test_fused_mlp_expansion_matches_unfused_fp32(residual):
     w2 = (torch.randn(c, r * c, 1, 1, 1, generator=gen, device=DEV) * (r * c) ** -0.5).bfloat16()
     b2 = (torch.randn(c, generator=gen, device=DEV) * 0.1).bfloat16()
     leaves = [t.clone().requires_grad_() for t in (x, w1, b1, w2, b2, res)]
-    out, _h = hip_ops.mlp_expansion(*leaves[:5], leaves[5] if residual else None)
+    op = hip_ops.mlp_expansion_stored if stored else hip_ops.mlp_expansion
+    out = op(*leaves[:5], leaves[5] if residual else None)[0]
     ref_leaves = [t.float().requires_grad_() for t in (x, w1, b1, w2, b2, res)]
     xf, w1f, b1f, w2f, b2f, rf = ref_leaves
     ref = F.conv3d(F.gelu(F.conv3d(xf, w1f, b1f)), w2f, b2f) + (rf if residual else 0)
@@ -184,6 +187,7 @@ def test_opcheck_pointwise_ops():
     w2 = (torch.randn(32, 64, 1, 1, 1, generator=gen, device=DEV) / 8).bfloat16().requires_grad_()
     res = torch.randn(1, 32, 2, 4, 8, generator=gen, device=DEV).bfloat16().requires_grad_()
     torch.library.opcheck(hip_ops.mlp_expansion, (x, w, b, w2, None, res))
+    torch.library.opcheck(hip_ops.mlp_expansion_stored, (x, w, b, w2, None, res))
 
 
 def test_channels_above_2048_are_rejected_and_not_selected():
