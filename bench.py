@@ -189,29 +189,10 @@ def time_copy_ceiling(torch) -> dict:
         events.append((a, b))
     torch.cuda.synchronize()
     ms = statistics.median(a.elapsed_time(b) for a, b in events)
-    # Read-only reference: a full fp32 sum of 2^28 bf16 elements (512 MiB read,
-    # 4 bytes written), rotating over two buffers.
-    srcs = [pairs[0][0], pairs[1][0], pairs[0][1].copy_(pairs[0][0]), pairs[1][1].copy_(pairs[1][0])]
-    big = [torch.cat(srcs[0:2]), torch.cat(srcs[2:4])]
-    del srcs
-    for i in range(4):
-        torch.sum(big[i % 2], dtype=torch.float32)
-    torch.cuda.synchronize()
-    events = []
-    for i in range(20):
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        torch.sum(big[i % 2], dtype=torch.float32)
-        b.record()
-        events.append((a, b))
-    torch.cuda.synchronize()
-    read_ms = statistics.median(a.elapsed_time(b) for a, b in events)
-    del pairs, big
+    del pairs
     torch.cuda.empty_cache()
     return {"kernel": "torch.neg, 2^27 bf16 (512 MiB moved)", "us": round(ms * 1000, 2),
-            "gbs": round(2 * n * 2 / (ms * 1e-3) / 1e9, 1),
-            "read_kernel": "torch.sum(dtype=float32), 2^28 bf16 (512 MiB read)",
-            "read_us": round(read_ms * 1000, 2), "read_gbs": round(2 * n * 2 / (read_ms * 1e-3) / 1e9, 1)}
+            "gbs": round(2 * n * 2 / (ms * 1e-3) / 1e9, 1)}
 
 
 def time_train_step(args, torch, optimization: str, variant: str = "base", steps: int | None = None,
@@ -527,7 +508,6 @@ def main() -> int:
         "traffic": load_traffic(dominant, args.kernel_size) if (args.channels, args.size) == (32, 128) else None,
         "copy_ceiling_gbs": ceiling["gbs"],
         "frac_of_copy_ceiling": round(achieved / ceiling["gbs"], 4),
-        "read_ceiling_gbs": ceiling["read_gbs"],
         "algorithmic_bytes_per_launch": dw["bytes_per_phase"],
     }
     result = {
