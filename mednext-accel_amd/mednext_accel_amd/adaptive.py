@@ -237,11 +237,15 @@ class _AdaptiveModule(nn.Module):
 
 
 class AdaptivePointwise3d(_AdaptiveModule):
-    """1x1x1 stride-1 convolution wrapper (reference ops/adaptive.py:125-200).
+    """1x1x1 convolution wrapper (reference ops/adaptive.py:125-200).
 
-    Besides the reference's ``nn.Conv3d`` it also takes a 1x1x1 stride-1
+    Besides the reference's stride-1 ``nn.Conv3d`` it takes a 1x1x1
     ``nn.ConvTranspose3d`` (the MedNeXt output heads, whose weight is stored
-    [Cin, Cout, 1, 1, 1]); ``transposed`` records which one it holds."""
+    [Cin, Cout, 1, 1, 1]; ``transposed`` records which one it holds) and the
+    stride-2 forms of both, the down / up blocks' residual convolutions: a
+    stride-2 1x1 conv is the GEMM on every second voxel of each dimension, a
+    stride-2 1x1 transposed conv (output 2s - 1) the GEMM written to the even
+    voxels with the bias alone at the odd ones."""
 
     _mednext_accel_backend_kind = "pointwise_gemm"
 
@@ -283,21 +287,36 @@ class AdaptivePointwise3d(_AdaptiveModule):
     def forward(self, x: Tensor) -> Tensor:
         context = _context_from_tensor(x, self.model_context, training=self.training)
         decision = self.resolver.resolve(self.descriptor, context, context.phase)
+        strided = self.stride != (1, 1, 1)
         if decision.implementation == "hip_pointwise_gemm" and _gemm_guards(x, self.in_channels, self.out_channels):
             dt = torch.bfloat16
             bias = self.bias.to(dt) if self.bias is not None else None
-            op = _hip_ops().pointwise_conv_transpose3d if self.transposed else _hip_ops().pointwise_conv3d
-            return op(x.to(dt), self.weight.to(dt), bias)
+            ops = _hip_ops()
+            if not strided:
+                op = ops.pointwise_conv_transpose3d if self.transposed else ops.pointwise_conv3d
+                return op(x.to(dt), self.weight.to(dt), bias)
+            if not self.transposed:
+                # Every second voxel, gathered once (autograd scatters its gradient back).
+                return ops.pointwise_conv3d(x[:, :, ::2, ::2, ::2].to(dt).contiguous(), self.weight.to(dt), bias)
+            y = ops.pointwise_conv_transpose3d(x.to(dt), self.weight.to(dt), bias)
+            full = tuple(2 * s - 1 for s in x.shape[2:])
+            if bias is None:
+                out = y.new_zeros((x.shape[0], self.out_channels, *full))
+            else:
+                out = bias.view(1, -1, 1, 1, 1).expand(x.shape[0], self.out_channels, *full).contiguous()
+            out[:, :, ::2, ::2, ::2] = y
+            return out
         if self.transposed:
-            return F.conv_transpose3d(x, self.weight, self.bias)
+            return F.conv_transpose3d(x, self.weight, self.bias, stride=self.stride)
         if (
             decision.implementation == "pointwise_gemm_per_sample"
+            and not strided
             and torch.is_grad_enabled()
             and x.ndim == 5
             and x.is_contiguous()
         ):
             return self._gemm(x)
-        return F.conv3d(x, self.weight, self.bias)
+        return F.conv3d(x, self.weight, self.bias, stride=self.stride)
 
 
 class AdaptiveDepthwise3d(_AdaptiveModule):
@@ -511,14 +530,15 @@ class AdaptiveExpansion:
 
 
 def _pointwise_eligible(module: nn.Module) -> bool:
-    """1x1x1 stride-1 Conv3d (reference ops/adaptive.py:323-332) or the same
-    geometry as a ConvTranspose3d without output padding (the output heads)."""
+    """1x1x1 stride-1 Conv3d (reference ops/adaptive.py:323-332), the same
+    geometry as a ConvTranspose3d without output padding (the output heads),
+    and both at stride 2 (the down / up blocks' residual convolutions)."""
     if type(module) is nn.ConvTranspose3d and module.output_padding != (0, 0, 0):
         return False
     return (
         type(module) in (nn.Conv3d, nn.ConvTranspose3d)
         and module.kernel_size == (1, 1, 1)
-        and module.stride == (1, 1, 1)
+        and module.stride in ((1, 1, 1), (2, 2, 2))
         and module.padding == (0, 0, 0)
         and module.dilation == (1, 1, 1)
         and module.groups == 1

@@ -155,12 +155,16 @@ def _hip_group_norm(descriptor, context, phase: str) -> str | None:
 
 
 def _pointwise_geometry(descriptor) -> bool:
-    """1x1x1 stride-1 convolution; ``transpose`` covers a 1x1x1 ConvTranspose3d,
-    which is the same product with the weight read transposed."""
+    """1x1x1 convolution: stride 1 (``regular``), stride 2 (``downsample``, the
+    GEMM on every second voxel), or a 1x1x1 ConvTranspose3d at stride 1 or 2
+    (``transpose``, the same product with the weight read transposed)."""
+    stride_ok = descriptor.stride == (1, 1, 1) or (
+        descriptor.stride == (2, 2, 2) and descriptor.direction in ("downsample", "transpose")
+    )
     return (
-        descriptor.direction in ("regular", "transpose")
+        descriptor.direction in ("regular", "downsample", "transpose")
         and descriptor.kernel_size == (1, 1, 1)
-        and descriptor.stride == (1, 1, 1)
+        and stride_ok
         and descriptor.padding == (0, 0, 0)
         and descriptor.dilation == (1, 1, 1)
         and descriptor.groups == 1

@@ -8,6 +8,8 @@ autocast tolerance (normwise max relative error <= 2e-2).
 
 from __future__ import annotations
 
+import copy
+
 import numpy as np
 import pytest
 import torch
@@ -298,3 +300,35 @@ def test_pointwise_argument_errors():
         hip_ops.pointwise_conv(x.transpose(3, 4), w)  # non-contiguous
     with pytest.raises(hip_ops._hip.HipLibraryError):
         hip_ops.pointwise_conv(x, w, aux=None, epilogue=PW_EPILOGUE_BIAS_RESIDUAL)  # missing aux
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+@pytest.mark.parametrize("cin,cout,spatial", [(32, 64, (16, 16, 16)), (64, 32, (9, 10, 11)), (16, 8, (7, 8, 9))])
+def test_stride2_residual_convs_match_native(transposed, cin, cout, spatial):
+    """The down block's Conv3d(k=1, stride=2) and the up block's
+    ConvTranspose3d(k=1, stride=2) residual convolutions through the wrapper
+    (gather / scatter around the matrix-core GEMM) vs PyTorch's own convs under
+    bf16 autocast: output and all gradients within the bf16 bound."""
+    from mednext_accel_amd.adaptive import AdaptivePointwise3d, ModelOptimizationContext
+    from mednext_accel_amd.optimization import PolicyRegistry
+
+    torch.manual_seed(cin + cout)
+    if transposed:
+        ref = torch.nn.ConvTranspose3d(cin, cout, kernel_size=1, stride=2).to(DEV)
+    else:
+        ref = torch.nn.Conv3d(cin, cout, kernel_size=1, stride=2).to(DEV)
+    cand = AdaptivePointwise3d(
+        copy.deepcopy(ref), PolicyRegistry().resolver(), ModelOptimizationContext("mednext_v1", "base", "none")
+    ).train()
+    x = torch.randn(2, cin, *spatial, device=DEV, requires_grad=True)
+    y = x.detach().clone().requires_grad_()
+    with torch.autocast(DEV, dtype=torch.bfloat16):
+        want = ref(x)
+        got = cand(y)
+    assert got.shape == want.shape and got.dtype == want.dtype == torch.bfloat16
+    assert max_rel(got, want) <= BF16
+    g = torch.randn_like(want)
+    wants = torch.autograd.grad(want, (x, ref.weight, ref.bias), g)
+    gots = torch.autograd.grad(got, (y, cand.weight, cand.bias), g)
+    for name, a, b in zip(("x", "weight", "bias"), gots, wants):
+        assert max_rel(a, b) <= BF16, name
