@@ -8,7 +8,7 @@ import sys
 
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(prog="python -m mednext_accel_amd.profiling", description=__doc__)
-    ap.add_argument("--variant", default="base", choices=("small", "base", "medium", "large"))
+    ap.add_argument("--variant", default="base", choices=("small", "base", "medium", "large", "v2-base", "v2-wide"))
     ap.add_argument("--size", type=int, default=128, help="cubic input size the stage shapes derive from")
     ap.add_argument("--kernel-size", type=int, action="append", dest="kernel_sizes",
                     help="depthwise kernel size (repeatable; default 3)")

@@ -1,4 +1,5 @@
-"""Workload matrix: the operator contexts of one MedNeXt v1 variant and the
+"""Workload matrix: the operator contexts of one MedNeXt variant (v1 small /
+base / medium / large, or v2 base / wide as ``v2-base`` / ``v2-wide``) and the
 candidate (implementation, launch recipe) pairs measured for each
 (reference profiling/matrix.py:154-320, ``build_workload_cases``).
 
@@ -7,7 +8,9 @@ depthwise convolutions of every resolution stage (per phase: forward, input
 gradient, weight gradient), GroupNorm(C, C) and the block expansions' 1x1x1
 convolutions. Depthwise candidates are the gfx950 default recipe and its
 neighbours (the other matrix-core tile widths, half and double the D-run);
-every context also carries the ``reference`` (native PyTorch) candidate.
+every context also carries the ``reference`` (native PyTorch) candidate, and
+the 1x1x1 convolutions the per-sample GEMM (``pointwise_gemm_per_sample``,
+the reference's own alternative) besides the matrix-core kernels.
 """
 
 from __future__ import annotations
@@ -16,6 +19,7 @@ from dataclasses import dataclass, field
 
 from .. import tiles
 from ..config import get_mednext_v1_config
+from ..config_v2 import get_mednext_v2_config
 
 DEPTHWISE_PHASES = {
     "forward": ("hip_depthwise_fwd", "forward"),
@@ -53,8 +57,13 @@ class KernelCase:
 
 def stage_shapes(variant: str = "base", size: int = 128, base_channels: int = 32) -> list[tuple[int, int, int]]:
     """(channels, spatial size, expansion ratio) of the five resolution stages
-    (encoder stages 0-3 and the bottleneck) of a MedNeXt v1 variant."""
-    cfg = get_mednext_v1_config(variant, in_channels=1, out_channels=3, base_channels=base_channels)
+    (encoder stages 0-3 and the bottleneck) of a MedNeXt v1 variant, or of
+    MedNeXt v2 for ``v2-base`` / ``v2-wide`` (whose width the variant fixes)."""
+    if variant.startswith("v2-"):
+        cfg = get_mednext_v2_config(variant[3:], in_channels=1, out_channels=3)
+        base_channels = cfg.base_channels
+    else:
+        cfg = get_mednext_v1_config(variant, in_channels=1, out_channels=3, base_channels=base_channels)
     out = []
     for stage in range(5):
         s = size >> stage
@@ -113,7 +122,7 @@ def build_workload_cases(
         if "pointwise_conv3d" in families:
             hidden = ratio * channels
             for cin, cout in ((channels, hidden), (hidden, channels)):
-                impls = ["reference"]
+                impls = ["reference", "pointwise_gemm_per_sample"]
                 if tiles.pointwise_supported(cin, cout, s**3):
                     impls.append("hip_pointwise_gemm")
                 for impl in impls:

@@ -43,10 +43,16 @@ def test_workload_matrix_candidates_are_valid_recipes():
     fwd = [c for c in cases if c.family == "depthwise_conv3d" and c.phase == "forward" and c.in_channels == 32]
     default = tiles.depthwise_recipe(1, 32, (128, 128, 128), 3, "bfloat16", "forward")
     assert any(c.parameter_map == dict(zip(("engine", "tile_w", "depth_chunk"), default)) for c in fwd)
-    # Hidden widths beyond the matrix-core limit keep only the reference candidate.
+    # Hidden widths beyond the matrix-core limit keep only the library candidates.
     big = [c for c in build_workload_cases("large", size=128) if c.family == "pointwise_conv3d" and 4096 in
            (c.in_channels, c.out_channels)]
-    assert big and all(c.implementation == "reference" for c in big)
+    assert big and {c.implementation for c in big} == {"reference", "pointwise_gemm_per_sample"}
+    # Every 1x1x1 context offers the per-sample GEMM; v2 contexts use the v2 widths and ratios.
+    pw = [c for c in cases if c.family == "pointwise_conv3d"]
+    assert {c.implementation for c in pw} == {"reference", "pointwise_gemm_per_sample", "hip_pointwise_gemm"}
+    v2 = {(c.in_channels, c.out_channels) for c in build_workload_cases("v2-base", size=128)
+          if c.family == "pointwise_conv3d"}
+    assert (32, 96) in v2 and (512, 4096) in v2 and (4096, 512) in v2
 
 
 def test_validation_accepts_equal_and_rejects_bad_components():
