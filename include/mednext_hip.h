@@ -173,8 +173,9 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
  *   MEDNEXT_PW_PROLOGUE_AFFINE: x -> x * s[n][k] + t[n][k], (s, t) = entries 0
  *     and 1 of the fp64 record prologue_coef[(n * K + k) * 4] (the layout
  *     mednext_grn_stats writes: a GRN folded into the GEMM that consumes it).
- *     The weight gradient rounds x * s + t to bf16 per element; the forward
- *     product computes the same W . (x s + t) as (W diag(s)) . x + W . t, with
+ *     The weight gradient and the tiled forward kernel (mednext_pw_kernels)
+ *     round x * s + t to bf16 per element; the streaming forward kernels
+ *     compute the same W . (x s + t) as (W diag(s)) . x + W . t, with
  *     W diag(s) rounded to bf16 and W . t added to the bias in fp32
  *     (weight_layout 0 only).
  * Epilogue, applied to each accumulator y[n][m][v] (bias may be NULL):
@@ -237,6 +238,27 @@ int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* 
                                  const void* prologue_coef, const void* epilogue_coef,
                                  void* row_partial, int32_t dtype, int32_t blocks_per_sample,
                                  void* stream);
+
+/* Kernel family for mednext_pointwise_fwd(_ex). The streaming kernels keep X
+ * out of LDS and read it once per group of 16-64 output rows; the tiled
+ * kernel stages X and the weight through LDS for 64 or 128 output rows at a
+ * time (K % 32 == 0, M % 16 == 0, no GELU prologue, no ROW_REDUCE, and
+ * blocks_per_sample == 0). AUTO takes the tiled kernel for K >= 256 where
+ * the streaming plan would read X twice or more and the tiled grid has at
+ * least 256 workgroups; TILED takes it wherever it applies; STREAMING never. The tiled
+ * kernel applies the AFFINE prologue to X (bf16(x s + t) per element). No
+ * counterpart in the reference (its GEMMs are library calls); process-wide,
+ * for measurement and tests. */
+enum mednext_pw_kernels {
+  MEDNEXT_PW_KERNELS_AUTO = 0,
+  MEDNEXT_PW_KERNELS_STREAMING = 1,
+  MEDNEXT_PW_KERNELS_TILED = 2
+};
+int32_t mednext_pointwise_set_kernels(int32_t choice);
+/* 1 if a launch of this shape and mode (blocks_per_sample 0) runs the tiled
+ * kernel under the current choice, else 0. */
+int32_t mednext_pointwise_uses_tiled(int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
+                                     int32_t epilogue);
 
 /* Slots per (sample, row) the ROW_REDUCE epilogue writes for this launch
  * shape (0 on invalid arguments). */

@@ -31,6 +31,7 @@
 //
 // GELU is the exact (erf) form (activation.h).
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 
 #include "activation.h"
@@ -722,6 +723,224 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
   }
 }
 
+// ------------------------------------------------------------- tiled product
+//
+// The kernels above keep X out of LDS, so a workgroup of 16 MT output rows
+// reads its X columns once per row group: at wide M (the GRN input gradients,
+// M = 4C) or deep K (the project GEMMs of the wide expansions) X is read
+// M / (16 MT) times. The tiled kernel shares each X tile across 64 MT output
+// rows instead. Workgroup = rows [m0, m0 + 64 MT) x one 128-voxel chunk; wave w
+// owns rows m0 + 16 MT w .. + 16 MT. K advances in steps of two 32-channel
+// slices through a double-buffered LDS stage:
+//   waves 0, 1  load X slice 2 s + w (eight 16-byte loads per lane, as in
+//               pw_fwd_kernel), apply the prologue, transpose in registers and
+//               store the eight B operands (the whole workgroup's for that
+//               slice) to LDS;
+//   waves 2, 3  load weight slice 2 s + w - 2 for all 64 MT rows into LDS in
+//               A-fragment order ([K][M] weights through the same 8x8 register
+//               transpose);
+//   all waves   one barrier, then MT x 8 MFMAs per slice from LDS.
+// The next step's loads are issued before the MFMAs of this one. The AFFINE
+// prologue is applied to X (bf16(x s + t) per channel, coefficients staged in
+// LDS), so no per-launch weight folding is needed. Requirements (checked by
+// the host): K % 32 == 0, M % 16 == 0, no ROW_REDUCE epilogue.
+constexpr int kTileSlices = 2;
+
+template <int MT, int PRO, int EPI>
+__global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_t* __restrict__ x,
+                                                                     const bf16_t* __restrict__ w,
+                                                                     const bf16_t* __restrict__ bias,
+                                                                     const bf16_t* __restrict__ aux,
+                                                                     bf16_t* __restrict__ y, PwGeom g, PwExtra ex) {
+  static_assert(MT == 1 || MT == 2, "tiled product: 64 or 128 rows per workgroup");
+  static_assert(EPI != MEDNEXT_PW_EPILOGUE_ROW_REDUCE, "ROW_REDUCE runs the streaming kernels");
+  constexpr int BM = 64 * MT;
+  constexpr int F16 = 4 * MT;  // 16-row fragments per workgroup
+  constexpr int XS = 8 * 64;   // uint4 per X slice: eight B operands x 64 lanes
+  constexpr int WS = F16 * 64; // uint4 per weight slice
+  constexpr int STAGE = kTileSlices * (XS + WS);
+  constexpr bool kAux = epi_has_aux(EPI);
+  constexpr bool kAux2 = EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE;
+  constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_AFFINE;
+  extern __shared__ __align__(16) uint16_t pw_lds[];
+  uint4* const stages = reinterpret_cast<uint4*>(pw_lds);
+  float* const bias_lds = reinterpret_cast<float*>(stages + 2 * STAGE);
+  float* const c0_lds = bias_lds + BM;
+  float* const c1_lds = c0_lds + BM;
+  float* const kcoef = c1_lds + BM;  // AFFINE: (s, t) per input channel
+
+  const int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int mg = static_cast<int>(lin % g.mgroups);
+  const int64_t rest = lin / g.mgroups;
+  const int chunk = static_cast<int>(rest % g.chunks);
+  const int64_t n = rest / g.chunks;
+  const int m0 = mg * BM;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n_col = lane & 15, q = lane >> 4;
+
+  for (int r = threadIdx.x; r < BM; r += kPwThreads) {
+    const int m = m0 + r;
+    const bool in = m < g.M;
+    bias_lds[r] = (epi_has_bias(EPI) && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
+    if constexpr (kAux2) {
+      c0_lds[r] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2]) : 0.f;
+      c1_lds[r] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2 + 1]) : 0.f;
+    }
+  }
+  if constexpr (kAffine) {
+    const double* __restrict__ coef_n = ex.pcoef + n * g.K * 4;
+    for (int k = threadIdx.x; k < g.K; k += kPwThreads) {
+      kcoef[2 * k] = static_cast<float>(coef_n[k * 4]);
+      kcoef[2 * k + 1] = static_cast<float>(coef_n[k * 4 + 1]);
+    }
+  }
+
+  const uint32_t V = g.V;
+  const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
+  const uint32_t nv = vl < V ? min(8u, V - vl) : 0u;
+  const __amdgpu_buffer_rsrc_t xr = slab_rsrc(x + n * g.K * static_cast<int64_t>(V), g.K * V * 2u);
+  const __amdgpu_buffer_rsrc_t wr = slab_rsrc(w, static_cast<uint32_t>(g.M) * g.K * 2u);
+  const bool loads_x = wave < kTileSlices;
+  // Weight loaders: [M][K] -> lane = (q, row in fragment), one 16-byte load per
+  // fragment; [K][M] -> lane = (q, 8-row octet), eight row loads + transpose.
+  const int wslot = wave - kTileSlices;
+  constexpr int kOctets = BM / 8;  // 8-row octets of the workgroup
+  constexpr int kPairs = 4 * kOctets;  // (q, octet) pairs, <= 64
+  const int oct = lane >> 2, oq = lane & 3;
+
+  uint4 rg[8];  // the loads of one slice (X rows or weight fragments)
+  auto load_slice = [&](int slice) {
+    if (loads_x) {
+      const uint32_t row0 = 32u * slice + 8u * q;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t off = ((row0 + i) * V + vl) * 2u;
+        rg[i] = (nv == 8u || nv == 0u) ? buf_load16(xr, nv != 0u ? off : kOob) : load_group(xr, off, nv);
+      }
+    } else if (!g.wt) {
+#pragma unroll
+      for (int f = 0; f < 8; ++f) {
+        const uint32_t m = static_cast<uint32_t>(m0 + 16 * f + n_col);
+        const uint32_t off = (m * static_cast<uint32_t>(g.K) + 32u * slice + 8u * q) * 2u;
+        rg[f] = (f < F16 && m < static_cast<uint32_t>(g.M)) ? buf_load16(wr, off) : make_uint4(0u, 0u, 0u, 0u);
+      }
+    } else {
+      const int m = m0 + 8 * oct;
+      const bool ok = lane < kPairs && m < g.M;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t k = 32u * slice + 8u * oq + e;
+        rg[e] = ok ? buf_load16(wr, (k * static_cast<uint32_t>(g.M) + m) * 2u) : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+  auto store_slice = [&](int slice, uint4* stage) {
+    if (loads_x) {
+      uint4 cur[8];
+      if constexpr (kAffine) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int k = 32 * slice + 8 * q + i;
+          cur[i] = affine_vec(rg[i], kcoef[2 * k], kcoef[2 * k + 1]);
+        }
+      } else {
+        apply_prologue<PRO>(rg, cur);
+      }
+      uint4 bv[8];
+      transpose8x8(cur, bv);
+      uint4* dst = stage + wave * XS + lane;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dst[j * 64] = bv[j];
+    } else {
+      uint4* dst = stage + kTileSlices * XS + wslot * WS;
+      if (!g.wt) {
+#pragma unroll
+        for (int f = 0; f < F16; ++f) dst[f * 64 + lane] = rg[f];
+      } else if (lane < kPairs) {
+        uint4 bv[8];
+        transpose8x8(rg, bv);  // bv[c] = 8 channels of row m0 + 8 oct + c
+        uint4* frag = dst + (oct >> 1) * 64 + oq * 16 + 8 * (oct & 1);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) frag[c] = bv[c];
+      }
+    }
+  };
+
+  f32x4_t acc[MT][8];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const bool rows_live = m0 + 16 * MT * wave < g.M;
+  // The epilogue's per-element operands are loaded before the K loop, so
+  // their latency hides behind it (zeros for tiles past M).
+  const int64_t yoff = n * g.M * static_cast<int64_t>(V);
+  const __amdgpu_buffer_rsrc_t ar = slab_rsrc(aux != nullptr ? aux + yoff : y, aux != nullptr ? g.M * V * 2u : 0u);
+  const __amdgpu_buffer_rsrc_t a2r =
+      slab_rsrc(ex.aux2 != nullptr ? ex.aux2 + yoff : y, ex.aux2 != nullptr ? g.M * V * 2u : 0u);
+  uint4 av[MT][4], av2[MT][4];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const bool live = m0 + 16 * MT * wave + 16 * mt < g.M;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      av[mt][r] = av2[mt][r] = make_uint4(0u, 0u, 0u, 0u);
+      const uint32_t off = (static_cast<uint32_t>(m0 + 16 * MT * wave + 16 * mt + 4 * q + r) * V + vl) * 2u;
+      if constexpr (kAux) av[mt][r] = load_group(ar, off, live ? nv : 0u);
+      if constexpr (kAux2) av2[mt][r] = load_group(a2r, off, live ? nv : 0u);
+    }
+  }
+  const int steps = (g.ks + kTileSlices - 1) / kTileSlices;
+  const int my_slice = loads_x ? wave : wslot;
+  if (my_slice < g.ks) load_slice(my_slice);
+  __syncthreads();  // row vectors and AFFINE coefficients
+  for (int s = 0; s < steps; ++s) {
+    uint4* const stage = stages + (s & 1) * STAGE;
+    const int slice = kTileSlices * s + my_slice;
+    if (slice < g.ks) store_slice(slice, stage);
+    if (slice + kTileSlices < g.ks) load_slice(slice + kTileSlices);
+    __syncthreads();
+    if (rows_live) {
+#pragma unroll
+      for (int sl = 0; sl < kTileSlices; ++sl) {
+        if (kTileSlices * s + sl < g.ks) {
+          const uint4* xs = stage + sl * XS + lane;
+          const uint4* ws = stage + kTileSlices * XS + sl * WS + (MT * wave) * 64 + lane;
+          uint4 a[MT];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) a[mt] = ws[mt * 64];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint4 b = xs[j * 64];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt][j] = mfma16x16x32(a[mt], b, acc[mt][j]);
+          }
+        }
+      }
+    }
+  }
+  if (!rows_live) return;
+
+  const __amdgpu_buffer_rsrc_t yr = slab_rsrc(y + yoff, g.M * V * 2u);
+  const __amdgpu_buffer_rsrc_t y2r = slab_rsrc(ex.y2 != nullptr ? ex.y2 + yoff : y, ex.y2 != nullptr ? g.M * V * 2u : 0u);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int lr0 = 16 * MT * wave + 16 * mt + 4 * q;
+    if (m0 + 16 * MT * wave + 16 * mt >= g.M) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int lr = lr0 + r;
+      float v[8], v2[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = acc[mt][j][r];
+      epilogue_values<EPI>(v, v2, av[mt][r], av2[mt][r], bias_lds[lr], c0_lds[lr], c1_lds[lr]);
+      const uint32_t off = (static_cast<uint32_t>(m0 + lr) * V + vl) * 2u;
+      store_group(yr, off, nv, pack8(v));
+      if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR) store_group(y2r, off, nv, pack8(v2));
+    }
+  }
+}
+
 // ---------------------------------------------------------------- weight grad
 
 constexpr int kWgStage = 128;   // voxels per LDS stage (4 waves x one 32-voxel MFMA step)
@@ -1051,6 +1270,29 @@ int pick_mt(int64_t k, int64_t m, int epi) {
   return 1;
 }
 
+template <int MT>
+FwdKernel tiled_instance(int pro, int epi) {
+  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) {
+    return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL ? pw_fwd_tiled_kernel<MT, 2, 2> : pw_fwd_tiled_kernel<MT, 2, 0>;
+  }
+  switch (epi) {
+    case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_tiled_kernel<MT, 0, 0>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_tiled_kernel<MT, 0, 1>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_tiled_kernel<MT, 0, 2>;
+    case MEDNEXT_PW_EPILOGUE_GELU_GRAD: return pw_fwd_tiled_kernel<MT, 0, 3>;
+    case MEDNEXT_PW_EPILOGUE_AFFINE_SCALE: return pw_fwd_tiled_kernel<MT, 0, 5>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR: return pw_fwd_tiled_kernel<MT, 0, 6>;
+    default: return pw_fwd_tiled_kernel<MT, 0, 7>;
+  }
+}
+
+// Shapes and modes the tiled product takes: whole 32-channel slices, whole
+// 16-row fragments, no GELU prologue (its K is always small here) and no
+// ROW_REDUCE (its slots are per streaming workgroup).
+bool tiled_eligible(int64_t k, int64_t m, int pro, int epi) {
+  return k % 32 == 0 && m % 16 == 0 && pro != MEDNEXT_PW_PROLOGUE_GELU && epi != MEDNEXT_PW_EPILOGUE_ROW_REDUCE;
+}
+
 FwdKernel pick_fwd(int64_t k, int mt, int pro, int epi) {
   const int64_t ks = cdiv(k, 32);
   if (ks >= kSplitKSlices) return mt == 1 ? splitk_instance<1>(pro, epi) : splitk_instance<2>(pro, epi);
@@ -1130,7 +1372,69 @@ FwdPlan plan_fwd(int64_t n, int64_t k, int64_t m, int64_t v, int epi, int32_t bl
   return p;
 }
 
+// Process-wide choice between the streaming and the tiled forward kernels
+// (MEDNEXT_PW_KERNELS_*), for measurement and tests.
+std::atomic<int> g_product_kernels{MEDNEXT_PW_KERNELS_AUTO};
+
+// Automatic choice: the tiled product for the deep products the streaming
+// plan would split over K (K >= 256) when that plan reads X at least twice
+// (one pass per 16 MT-row group) and the tiled grid still fills the chip.
+// Measured on MI355X at the MedNeXt shapes: the tiled kernel takes 0.35-0.7
+// of the split-K time there, but loses at K <= 128 with aux-reading
+// epilogues (their time is the epilogue's traffic, which the persistent
+// streaming kernels overlap better) and on grids of under 256 workgroups.
+constexpr int kTiledMinRereads = 2;
+constexpr int64_t kTiledMinBlocks = 256;
+
+int tiled_mt(int64_t m) { return m > 64 ? 2 : 1; }
+
+bool tiled_pays(const FwdPlan& p, int64_t n, int64_t m) {
+  const int64_t blocks = n * cdiv(m, 64 * tiled_mt(m)) * p.g.chunks;
+  return p.splitk && p.g.mgroups >= kTiledMinRereads && blocks >= kTiledMinBlocks;
+}
+
+int32_t launch_tiled(const void* x, const void* weight, const void* bias, const void* aux, void* y, const PwExtra& ex,
+                     int64_t n, int64_t k, int64_t m, int64_t v, int32_t weight_layout, int32_t prologue,
+                     int32_t epilogue, void* stream) {
+  const int mt = tiled_mt(m);
+  PwGeom g{};
+  g.K = static_cast<int>(k);
+  g.M = static_cast<int>(m);
+  g.ks = static_cast<int>(k / 32);
+  g.V = static_cast<uint32_t>(v);
+  g.chunks = static_cast<int>(cdiv(v, kChunk));
+  g.mgroups = static_cast<int>(cdiv(m, 64 * mt));
+  g.wgs = 1;
+  g.wt = weight_layout;
+  const int64_t blocks = n * g.mgroups * g.chunks;
+  MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
+  const size_t stage = static_cast<size_t>(kTileSlices) * (8 * 64 + 4 * mt * 64) * 16;
+  const size_t lds = 2 * stage + 3 * 64 * mt * sizeof(float) +
+                     (prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? 2 * static_cast<size_t>(k) * sizeof(float) : 0);
+  FwdKernel fn = mt == 1 ? tiled_instance<1>(prologue, epilogue) : tiled_instance<2>(prologue, epilogue);
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds, static_cast<hipStream_t>(stream),
+                     static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(weight),
+                     static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(aux), static_cast<bf16_t*>(y), g, ex);
+  MEDNEXT_CHECK_LAUNCH();
+  return MEDNEXT_STATUS_OK;
+}
+
 }  // namespace
+
+extern "C" int32_t mednext_pointwise_set_kernels(int32_t choice) {
+  MEDNEXT_CHECK_ARG(choice >= MEDNEXT_PW_KERNELS_AUTO && choice <= MEDNEXT_PW_KERNELS_TILED,
+                    "choice must be MEDNEXT_PW_KERNELS_AUTO, _STREAMING or _TILED");
+  g_product_kernels.store(choice, std::memory_order_relaxed);
+  return MEDNEXT_STATUS_OK;
+}
+
+extern "C" int32_t mednext_pointwise_uses_tiled(int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
+                                                int32_t epilogue) {
+  if (n < 1 || k < 1 || k > kMaxK || m < 1 || v < 1 || !pro_epi_supported(prologue, epilogue)) return 0;
+  const int choice = g_product_kernels.load(std::memory_order_relaxed);
+  if (choice == MEDNEXT_PW_KERNELS_STREAMING || !tiled_eligible(k, m, prologue, epilogue)) return 0;
+  return choice == MEDNEXT_PW_KERNELS_TILED || tiled_pays(plan_fwd(n, k, m, v, epilogue, 0), n, m) ? 1 : 0;
+}
 
 extern "C" int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, int64_t v,
                                                int32_t blocks_per_sample) {
@@ -1167,15 +1471,18 @@ extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, c
                         aligned(weight, 16) && (bias == nullptr || aligned(bias, 2)),
                     "pointwise tensors must be bf16-aligned and the weight 16-byte aligned");
   MEDNEXT_CHECK_ARG(blocks_per_sample >= 0, "blocks_per_sample must be >= 0 (0 = automatic)");
+  PwExtra ex{static_cast<const double*>(prologue_coef), static_cast<const double*>(epilogue_coef),
+             static_cast<double*>(row_partial), static_cast<const bf16_t*>(aux2), static_cast<bf16_t*>(y2), 0};
+  if (blocks_per_sample == 0 && mednext_pointwise_uses_tiled(n, k, m, v, prologue, epilogue)) {
+    return launch_tiled(x, weight, bias, aux, y, ex, n, k, m, v, weight_layout, prologue, epilogue, stream);
+  }
   FwdPlan p = plan_fwd(n, k, m, v, epilogue, blocks_per_sample);
   p.g.wt = weight_layout;
+  ex.slots = p.slots;
   MEDNEXT_CHECK_ARG(p.blocks < (int64_t{1} << 31), "grid too large");
   const int mt = p.mt;
   const size_t lds = static_cast<size_t>(16 * mt) * p.g.ks * 32 * 2 + kRowVecs * 16 * mt * sizeof(float) +
                      (p.splitk ? static_cast<size_t>(mt) * 8 * 4 * 64 * sizeof(float) : 0);
-  PwExtra ex{static_cast<const double*>(prologue_coef), static_cast<const double*>(epilogue_coef),
-             static_cast<double*>(row_partial), static_cast<const bf16_t*>(aux2), static_cast<bf16_t*>(y2),
-             p.slots};
   hipLaunchKernelGGL(pick_fwd(k, mt, prologue, epilogue), dim3(static_cast<unsigned>(p.blocks)), dim3(kPwThreads),
                      lds, static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(x),
                      static_cast<const bf16_t*>(weight), static_cast<const bf16_t*>(bias),

@@ -64,6 +64,8 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         (_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p),
     ),
     "mednext_pointwise_row_slots": (_i64, (_i64, _i64, _i64, _i64, _i32)),
+    "mednext_pointwise_set_kernels": (_i32, (_i32,)),
+    "mednext_pointwise_uses_tiled": (_i32, (_i64, _i64, _i64, _i64, _i32, _i32)),
     "mednext_pointwise_wgrad_workspace_bytes": (c_size_t, (_i64, _i64, _i64, _i64, _i32)),
     "mednext_pointwise_wgrad_ex": (
         _i32,
@@ -99,7 +101,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -278,6 +278,21 @@ def group_norm_backward(
 PW_PROLOGUE_NONE, PW_PROLOGUE_GELU, PW_PROLOGUE_AFFINE = 0, 1, 2
 PW_EPILOGUE_BIAS, PW_EPILOGUE_BIAS_GELU, PW_EPILOGUE_BIAS_RESIDUAL, PW_EPILOGUE_GELU_GRAD = 0, 1, 2, 3
 PW_EPILOGUE_ROW_REDUCE, PW_EPILOGUE_AFFINE_SCALE, PW_EPILOGUE_BIAS_GELU_PAIR, PW_EPILOGUE_AUX_SCALE = 4, 5, 6, 7
+#: Forward kernel family (include/mednext_hip.h ``mednext_pw_kernels``): the
+#: library's automatic choice, the streaming kernels only, or the LDS-tiled
+#: kernel wherever it applies.
+PW_KERNELS_AUTO, PW_KERNELS_STREAMING, PW_KERNELS_TILED = 0, 1, 2
+
+
+def set_pointwise_kernels(choice: int) -> None:
+    """Process-wide choice of the forward kernel family (``PW_KERNELS_*``)."""
+    _hip.check(_hip.load().mednext_pointwise_set_kernels(int(choice)), "mednext_pointwise_set_kernels")
+
+
+def pointwise_uses_tiled(n: int, k: int, m: int, v: int, prologue: int = 0, epilogue: int = 0) -> bool:
+    """Whether a ``pointwise_conv`` of this shape and mode (automatic launch
+    shape) runs the tiled kernel under the current choice."""
+    return bool(_hip.load().mednext_pointwise_uses_tiled(n, k, m, v, prologue, epilogue))
 
 
 def _weight2d(weight: Tensor) -> Tensor:

@@ -61,3 +61,33 @@ def test_abi_version_and_error_slot():
     assert lib.mednext_depthwise3d_wgrad_workspace_bytes(1, 32, 128, 128, 128, 3, 0, 1, 64, 16) == 0
     assert lib.mednext_depthwise3d_wgrad_workspace_bytes(1, 32, 128, 128, 40, 3, 3, 1, 64, 16) == 0
     assert lib.mednext_group_norm_workspace_bytes(1, 32, 128**3, 32) == 1 * 32 * 33 * 2 * 8
+
+
+def test_pointwise_kernel_choice_is_host_logic():
+    """The forward kernel family is chosen on the host from the shape and mode
+    alone (no device query): tiled for K >= 256 where the streaming plan would
+    re-read X and the tiled grid fills the chip."""
+    from mednext_accel_amd import hip_ops as P
+
+    uses = P.pointwise_uses_tiled
+    try:
+        P.set_pointwise_kernels(P.PW_KERNELS_AUTO)
+        assert uses(2, 1024, 128, 32768)                 # GRN project backward: dx = W1^T du
+        assert uses(2, 256, 2048, 4096)                  # expand of a 2048-wide hidden layer
+        assert uses(2, 256, 64, 64**3, P.PW_PROLOGUE_AFFINE, P.PW_EPILOGUE_BIAS_RESIDUAL)  # GRN project
+        assert not uses(2, 128, 1024, 32768, 0, P.PW_EPILOGUE_AFFINE_SCALE)  # K = 128: epilogue-bound
+        assert not uses(2, 32, 96, 128**3)               # expand at K = 32: X read twice
+        assert not uses(2, 2048, 256, 512)               # too few 128-voxel chunks to fill the chip
+        assert not uses(2, 1024, 120, 32768)             # M % 16 != 0
+        assert not uses(2, 1000, 128, 32768)             # K % 32 != 0
+        assert not uses(2, 1024, 128, 32768, P.PW_PROLOGUE_GELU, 0)
+        assert not uses(2, 128, 1024, 32768, 0, P.PW_EPILOGUE_ROW_REDUCE)
+        P.set_pointwise_kernels(P.PW_KERNELS_TILED)
+        assert uses(2, 32, 96, 128**3) and uses(2, 2048, 256, 512)
+        assert not uses(2, 1024, 120, 32768)
+        P.set_pointwise_kernels(P.PW_KERNELS_STREAMING)
+        assert not uses(2, 1024, 128, 32768)
+        with pytest.raises(_hip.HipLibraryError):
+            P.set_pointwise_kernels(3)
+    finally:
+        P.set_pointwise_kernels(P.PW_KERNELS_AUTO)
