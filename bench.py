@@ -60,9 +60,12 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--v2-steps", type=int, default=10)
     ap.add_argument("--v2-warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="CPU baseline time budget")
+    ap.add_argument("--no-graph-step", action="store_true",
+                    help="skip the HIP-graph-captured variants of the training steps")
     ap.add_argument("--train-only", action="store_true", help="time only the training step(s) of --train-variants")
     ap.add_argument("--train-variants", default="base,large,v2",
-                    help="comma list of base / large / v2 for --train-only (--no-large-step / --no-v2-step drop one)")
+                    help="comma list of base / large / v2 (eager) and base-graph / large-graph / v2-graph (captured) for "
+                         "--train-only (--no-large-step / --no-v2-step drop the eager large / v2)")
     ap.add_argument(
         "--sweep",
         action="store_true",
@@ -196,15 +199,18 @@ def time_copy_ceiling(torch) -> dict:
 
 
 def time_train_step(args, torch, optimization: str, variant: str = "base", steps: int | None = None,
-                    warmup: int | None = None) -> dict:
+                    warmup: int | None = None, graph: bool = False) -> dict:
     """MedNeXt training step at 1x1xS^3 in bf16 autocast with AdamW, the
     reference's step protocol (benchmarks/implementations.py:133-190): event
     median over the timed steps. ``base``: MedNeXt-Base k3, no checkpointing
     (configs[3]); ``large``: MedNeXt-Large k5 with expansion-branch
     checkpointing on all stages; ``v2``: MedNeXt v2 Base (GRN in
-    every expansion), no checkpointing."""
+    every expansion), no checkpointing. ``graph``: the whole step (forward,
+    loss, backward, AdamW with device-side step counters) captured once as a
+    HIP graph after the warm-up steps and replayed; every replay does the
+    full step's work."""
     from mednext_accel_amd import CheckpointConfig, mednext_base, mednext_large, mednext_v2_base
-    from mednext_accel_amd.step import make_training_step
+    from mednext_accel_amd.step import GraphedTrainingStep, make_training_step
 
     steps = args.train_steps if steps is None else steps
     warmup = args.train_warmup if warmup is None else warmup
@@ -218,9 +224,12 @@ def time_train_step(args, torch, optimization: str, variant: str = "base", steps
         model = mednext_base(in_channels=1, out_channels=3, kernel_size=3, deep_supervision=True,
                              optimization=optimization)
     model = model.cuda().train()
-    step = make_training_step(model, size=args.train_size, device="cuda")
-    for _ in range(warmup):
-        step()
+    step = make_training_step(model, size=args.train_size, device="cuda", capturable=graph)
+    if graph:
+        step = GraphedTrainingStep(step, warmup=max(1, warmup))
+    else:
+        for _ in range(warmup):
+            step()
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
     events = []
@@ -240,6 +249,8 @@ def time_train_step(args, torch, optimization: str, variant: str = "base", steps
         "peak_allocated_mib": round(torch.cuda.max_memory_allocated() / 2**20, 1),
         "final_loss": round(float(step.last_loss.detach()), 5),
     }
+    if graph:
+        result["captured"] = "hip_graph"
     del step, model
     torch.cuda.empty_cache()
     return result
@@ -486,6 +497,14 @@ def main() -> int:
                                                           args.large_warmup)
         if "v2" in variants and not args.no_v2_step:
             out["train_step_v2_hip"] = time_train_step(args, torch, "auto", "v2", args.v2_steps, args.v2_warmup)
+        if "base-graph" in variants:
+            out["train_step_hip_graph"] = time_train_step(args, torch, "auto", graph=True)
+        if "large-graph" in variants:
+            out["train_step_large_hip_graph"] = time_train_step(args, torch, "auto", "large", args.large_steps,
+                                                                args.large_warmup, graph=True)
+        if "v2-graph" in variants:
+            out["train_step_v2_hip_graph"] = time_train_step(args, torch, "auto", "v2", args.v2_steps,
+                                                             args.v2_warmup, graph=True)
         print(json.dumps(out))
         return 0
     dw = time_depthwise(args, torch, hip_ops, lead)
@@ -538,6 +557,7 @@ def main() -> int:
     }
     if not args.no_train_step:
         ours = time_train_step(args, torch, "auto")
+        ours_graph = None if args.no_graph_step else time_train_step(args, torch, "auto", graph=True)
         eager = None if args.no_eager_step else time_train_step(args, torch, "reference")
         result["train_step"] = {
             "model": (
@@ -547,11 +567,16 @@ def main() -> int:
             "steps": args.train_steps,
             "warmup": args.train_warmup,
             "hip": ours,
+            "hip_graph": ours_graph,
             "reference_eager": eager,
             "speedup_vs_reference_eager": round(eager["median_step_ms"] / ours["median_step_ms"], 3) if eager else None,
+            "graph_speedup_vs_reference_eager": round(eager["median_step_ms"] / ours_graph["median_step_ms"], 3)
+            if eager and ours_graph else None,
         }
         if not args.no_large_step:
             big = time_train_step(args, torch, "auto", "large", args.large_steps, args.large_warmup)
+            big_graph = None if args.no_graph_step else time_train_step(
+                args, torch, "auto", "large", args.large_steps, args.large_warmup, graph=True)
             big_eager = None if args.no_eager_step else time_train_step(
                 args, torch, "reference", "large", max(3, args.large_steps // 2), 2)
             result["train_step_large"] = {
@@ -560,12 +585,17 @@ def main() -> int:
                     "checkpointing on all stages, bf16 autocast, AdamW lr 1e-3 (BASELINE configs[4])"
                 ),
                 "hip": big,
+                "hip_graph": big_graph,
                 "reference_eager": big_eager,
                 "speedup_vs_reference_eager": round(big_eager["median_step_ms"] / big["median_step_ms"], 3)
                 if big_eager else None,
+                "graph_speedup_vs_reference_eager": round(big_eager["median_step_ms"] / big_graph["median_step_ms"], 3)
+                if big_eager and big_graph else None,
             }
     if not args.no_train_step and not args.no_v2_step:
         v2 = time_train_step(args, torch, "auto", "v2", args.v2_steps, args.v2_warmup)
+        v2_graph = None if args.no_graph_step else time_train_step(
+            args, torch, "auto", "v2", args.v2_steps, args.v2_warmup, graph=True)
         v2_eager = None if args.no_eager_step else time_train_step(
             args, torch, "reference", "v2", max(3, args.v2_steps // 2), 2)
         result["train_step_v2"] = {
@@ -574,9 +604,12 @@ def main() -> int:
                 "bf16 autocast, AdamW lr 1e-3, random init, synthetic N(0,1) input and uniform labels"
             ),
             "hip": v2,
+            "hip_graph": v2_graph,
             "reference_eager": v2_eager,
             "speedup_vs_reference_eager": round(v2_eager["median_step_ms"] / v2["median_step_ms"], 3)
             if v2_eager else None,
+            "graph_speedup_vs_reference_eager": round(v2_eager["median_step_ms"] / v2_graph["median_step_ms"], 3)
+            if v2_eager and v2_graph else None,
         }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, torch)

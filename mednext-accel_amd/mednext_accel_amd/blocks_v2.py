@@ -59,14 +59,14 @@ class MedNeXtV2Block(nn.Module):
                 h = self.norm(d, out_dtype=torch.bfloat16)
                 residual = x if self.use_residual else None
                 if self.checkpoint_expansion and self.training and torch.is_grad_enabled():
-                    return checkpoint(fused, h, residual, use_reentrant=False)
+                    return checkpoint(fused, h, residual, use_reentrant=False, preserve_rng_state=False)
                 return fused(h, residual)
             return self._finish(self.norm(d), x)
         return self._finish(self.norm(self.depthwise(x)), x)
 
     def _finish(self, h: Tensor, x: Tensor) -> Tensor:
         if self.checkpoint_expansion and self.training and torch.is_grad_enabled():
-            h = checkpoint(self._expansion_forward, h, use_reentrant=False)
+            h = checkpoint(self._expansion_forward, h, use_reentrant=False, preserve_rng_state=False)
         else:
             h = self._expansion_forward(h)
         return h + x if self.use_residual else h

@@ -134,7 +134,7 @@ class MedNeXtV2(nn.Module):
         cfg = self.checkpointing
         whole_block = cfg is not None and cfg.checkpoints_blocks and cfg.includes(stage)
         if whole_block and self.training and torch.is_grad_enabled():
-            return checkpoint(module, x, use_reentrant=False)
+            return checkpoint(module, x, use_reentrant=False, preserve_rng_state=False)
         return module(x)
 
     def _run_stage(self, modules: nn.Sequential, x: Tensor, stage: int) -> Tensor:

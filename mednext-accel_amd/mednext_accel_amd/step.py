@@ -24,6 +24,10 @@ class TrainingStep:
     sample: Tensor
     targets: dict[tuple[int, ...], Tensor]
     autocast_dtype: torch.dtype | None = torch.bfloat16
+    #: Autocast's cast cache (reuses a weight's bf16 copy within a forward).
+    #: A captured step disables it: cached casts would be graph-pool tensors
+    #: held across the capture boundary.
+    autocast_cache: bool = True
     last_loss: Tensor | None = field(default=None, init=False)
 
     def loss(self, outputs) -> Tensor:
@@ -35,11 +39,14 @@ class TrainingStep:
         self.optimizer.zero_grad(set_to_none=True)
         device = self.sample.device.type
         enabled = self.autocast_dtype is not None
-        with torch.autocast(device, dtype=self.autocast_dtype or torch.bfloat16, enabled=enabled):
+        with torch.autocast(device, dtype=self.autocast_dtype or torch.bfloat16, enabled=enabled,
+                            cache_enabled=self.autocast_cache):
             loss = self.loss(self.model(self.sample))
         loss.backward()
         self.optimizer.step()
-        self.last_loss = loss
+        # Detached: a kept loss must not hold the step's autograd graph (and
+        # its gradient-accumulation nodes) alive into the next step.
+        self.last_loss = loss.detach()
         return loss
 
 
@@ -54,8 +61,11 @@ def make_training_step(
     lr: float = 1e-3,
     autocast_dtype: torch.dtype | None = torch.bfloat16,
     device: torch.device | str | None = None,
+    capturable: bool = False,
 ) -> TrainingStep:
-    """Synthetic inputs (seeded on the CPU generator, then moved) and AdamW."""
+    """Synthetic inputs (seeded on the CPU generator, then moved) and AdamW
+    (``capturable=True``: its step counters live on the device, as a captured
+    step needs)."""
     device = torch.device(device) if device is not None else next(model.parameters()).device
     gen = torch.Generator().manual_seed(seed)
     sample = torch.randn(batch, in_channels, size, size, size, generator=gen).to(device)
@@ -71,5 +81,51 @@ def make_training_step(
         if s % 2:
             break
         s //= 2
-    optimizer = torch.optim.AdamW(model.parameters(), lr=lr)
+    optimizer = torch.optim.AdamW(model.parameters(), lr=lr, capturable=capturable)
     return TrainingStep(model, optimizer, sample, targets, autocast_dtype)
+
+
+class GraphedTrainingStep:
+    """A ``TrainingStep`` captured once as a HIP graph and replayed.
+
+    Every replay runs the whole step's kernels (zero-free gradient writes,
+    forward, loss, backward, AdamW) from one host call, so the step no longer
+    waits on Python and per-launch host work. The inputs, the targets and
+    every intermediate are fixed device buffers (the graph's private pool);
+    the parameters and optimizer state are updated in place as in eager
+    mode. Capture needs a capturable optimizer (``make_training_step(...,
+    capturable=True)``) and a step without host synchronisation.
+    """
+
+    def __init__(self, step: TrainingStep, *, warmup: int = 3) -> None:
+        device = step.sample.device
+        if device.type != "cuda":
+            raise ValueError("a captured training step needs a GPU")
+        for group in step.optimizer.param_groups:
+            if not group.get("capturable", False):
+                raise ValueError("capture needs an optimizer built with capturable=True")
+        step.autocast_cache = False
+        self.step = step
+        # Eager warm-up on a side stream (default priority): lazily created
+        # state (optimizer moments, library handles, cached plans) exists
+        # before capture and the capture stream starts from a quiet device.
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):
+                step()
+        torch.cuda.current_stream(device).wait_stream(side)
+        torch.cuda.synchronize(device)
+        step.optimizer.zero_grad(set_to_none=True)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.loss = step().detach()
+
+    @property
+    def last_loss(self) -> Tensor:
+        """The loss buffer the graph writes (valid after a replay)."""
+        return self.loss
+
+    def __call__(self) -> Tensor:
+        self.graph.replay()
+        return self.loss
