@@ -1386,17 +1386,22 @@ std::atomic<int> g_product_kernels{MEDNEXT_PW_KERNELS_AUTO};
 constexpr int kTiledMinRereads = 2;
 constexpr int64_t kTiledMinBlocks = 256;
 
-int tiled_mt(int64_t m) { return m > 64 ? 2 : 1; }
+int64_t tiled_blocks(int64_t n, int64_t m, int64_t v, int mt) { return n * cdiv(m, 64 * mt) * cdiv(v, kChunk); }
 
-bool tiled_pays(const FwdPlan& p, int64_t n, int64_t m) {
-  const int64_t blocks = n * cdiv(m, 64 * tiled_mt(m)) * p.g.chunks;
-  return p.splitk && p.g.mgroups >= kTiledMinRereads && blocks >= kTiledMinBlocks;
+// 128-row workgroups (X read once per 128 rows) unless M <= 64 or they would
+// leave the chip short of workgroups; then 64-row ones.
+int tiled_mt(int64_t n, int64_t m, int64_t v) {
+  return m > 64 && tiled_blocks(n, m, v, 2) >= kTiledMinBlocks ? 2 : 1;
+}
+
+bool tiled_pays(const FwdPlan& p, int64_t n, int64_t m, int64_t v) {
+  return p.splitk && p.g.mgroups >= kTiledMinRereads && tiled_blocks(n, m, v, tiled_mt(n, m, v)) >= kTiledMinBlocks;
 }
 
 int32_t launch_tiled(const void* x, const void* weight, const void* bias, const void* aux, void* y, const PwExtra& ex,
                      int64_t n, int64_t k, int64_t m, int64_t v, int32_t weight_layout, int32_t prologue,
                      int32_t epilogue, void* stream) {
-  const int mt = tiled_mt(m);
+  const int mt = tiled_mt(n, m, v);
   PwGeom g{};
   g.K = static_cast<int>(k);
   g.M = static_cast<int>(m);
@@ -1433,7 +1438,7 @@ extern "C" int32_t mednext_pointwise_uses_tiled(int64_t n, int64_t k, int64_t m,
   if (n < 1 || k < 1 || k > kMaxK || m < 1 || v < 1 || !pro_epi_supported(prologue, epilogue)) return 0;
   const int choice = g_product_kernels.load(std::memory_order_relaxed);
   if (choice == MEDNEXT_PW_KERNELS_STREAMING || !tiled_eligible(k, m, prologue, epilogue)) return 0;
-  return choice == MEDNEXT_PW_KERNELS_TILED || tiled_pays(plan_fwd(n, k, m, v, epilogue, 0), n, m) ? 1 : 0;
+  return choice == MEDNEXT_PW_KERNELS_TILED || tiled_pays(plan_fwd(n, k, m, v, epilogue, 0), n, m, v) ? 1 : 0;
 }
 
 extern "C" int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, int64_t v,

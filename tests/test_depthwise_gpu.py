@@ -191,6 +191,39 @@ def test_deterministic_weight_grad():
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
+def test_mfma_weight_grad_repeats_and_replays():
+    """The MFMA weight gradient (partials kernel + fixed-order finish kernel):
+    back-to-back launches, a launch of another shape in between and HIP-graph
+    replays (with eager work between them) all give the first launch's bits,
+    and those match the oracle."""
+    print("[depthwise mfma wgrad repeats / replays]", flush=True)
+    gen = torch.Generator().manual_seed(19)
+    xc = torch.randn(2, 24, 16, 64, 64, generator=gen).bfloat16()
+    dyc = torch.randn(2, 24, 16, 64, 64, generator=gen).bfloat16()
+    x, dy = xc.to(DEV), dyc.to(DEV)
+    recipe = [1, 64, 4]
+    first = hip_ops.depthwise_weight_grad(x, dy, 3, recipe)
+    xn, dyn = xc.double().numpy(), dyc.double().numpy()
+    assert max_rel(first[0], odw.weight_grad(xn, dyn, 3)) <= BF16
+    assert max_rel(first[1], odw.bias_grad(dyn)) <= BF16
+    hip_ops.depthwise_weight_grad(x[:1, :5].contiguous(), dy[:1, :5].contiguous(), 3, [1, 32, 16])
+    again = hip_ops.depthwise_weight_grad(x, dy, 3, recipe)
+    assert torch.equal(first[0], again[0]) and torch.equal(first[1], again[1])
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        hip_ops.depthwise_weight_grad(x, dy, 3, recipe)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = hip_ops.depthwise_weight_grad(x, dy, 3, recipe)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured[0], first[0]) and torch.equal(captured[1], first[1])
+        hip_ops.depthwise_weight_grad(x[:1, :5].contiguous(), dy[:1, :5].contiguous(), 3, [1, 32, 16])
+
+
 def test_launcher_argument_errors():
     x = torch.randn(1, 2, 4, 4, 4, device=DEV)
     with pytest.raises(ValueError):

@@ -3,8 +3,8 @@ next to the streaming kernels on the same inputs.
 
 Every case runs twice: with the streaming kernels only and with the tiled
 kernel forced wherever it applies (``set_pointwise_kernels``). Shapes cover
-one and two 64-row halves per workgroup (M <= 64 and M > 64), workgroups whose
-last waves have no live rows (M = 48, 80), several row groups (M = 272), odd
+64- and 128-row workgroups, workgroups whose last waves have no live rows
+(M = 48, 80), several row groups (M = 272), odd
 slice counts (K = 32, 96), both weight layouts, and ragged volumes (V % 128
 and V % 8 non-zero). The bar is the one of the other GEMM-mode tests:
 rel-L2 <= 8e-3 against the same chain in float64 on the bf16 inputs.
@@ -45,12 +45,16 @@ def product(w2, x, transpose):
     return torch.matmul(a, x.flatten(2))
 
 
-# (n, k, m, spatial): K input rows of the product, M output rows.
+# (n, k, m, spatial): K input rows of the product, M output rows. Grids of
+# fewer than 256 128-row workgroups run 64-row ones (the first four shapes);
+# the last two are large enough for 128-row workgroups.
 SHAPES = [
-    (2, 256, 128, (8, 8, 9)),    # two slices per step, V = 576 (partial chunk)
-    (1, 96, 80, (3, 5, 7)),      # odd slice count, M = 80: wave 3 idle, V % 8 != 0
-    (2, 32, 48, (4, 6, 11)),     # one slice, M = 48 (64-row workgroup, one wave idle)
-    (1, 512, 272, (2, 4, 16)),   # three row groups, the last one 16 rows
+    (2, 256, 128, (8, 8, 9)),     # two slices per step, V = 576 (partial chunk)
+    (1, 96, 80, (3, 5, 7)),       # odd slice count, M = 80, V % 8 != 0
+    (2, 32, 48, (4, 6, 11)),      # one slice, M = 48 (one wave idle)
+    (1, 512, 272, (2, 4, 16)),    # five 64-row groups, the last one 16 rows
+    (1, 96, 80, (15, 33, 67)),    # 128-row workgroups: M = 80 (waves 2-3 partly idle), V % 8 != 0
+    (1, 512, 272, (16, 32, 64)),  # 128-row workgroups, three row groups, the last one 16 rows
 ]
 
 
@@ -127,7 +131,8 @@ def test_transposed_modes(n, k, m, spatial, mode):
         assert rel_l2(out.cpu().flatten(2), want) <= TOL
 
 
-@pytest.mark.parametrize("n,k,m,spatial", [(2, 96, 32, (5, 6, 7)), (1, 1024, 128, (4, 8, 8)), (2, 256, 80, (8, 8, 9))])
+@pytest.mark.parametrize("n,k,m,spatial", [(2, 96, 32, (5, 6, 7)), (1, 1024, 128, (4, 8, 8)), (2, 256, 80, (8, 8, 9)),
+                                            (1, 1024, 128, (16, 32, 64))])
 @pytest.mark.parametrize("residual", [False, True])
 def test_affine_prologue(n, k, m, spatial, residual):
     """The GRN-consuming project GEMM: W . (x s + t) + b (+ residual). The
