@@ -246,9 +246,12 @@ int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* 
  * blocks_per_sample == 0). AUTO takes the tiled kernel for K >= 256 where
  * the streaming plan would read X twice or more and the tiled grid has at
  * least 256 workgroups; TILED takes it wherever it applies; STREAMING never. The tiled
- * kernel applies the AFFINE prologue to X (bf16(x s + t) per element). No
- * counterpart in the reference (its GEMMs are library calls); process-wide,
- * for measurement and tests. */
+ * kernel applies the AFFINE prologue to X (bf16(x s + t) per element). The
+ * same choice governs the weight gradient's tile: AUTO uses 128 x 128
+ * workgroup tiles when M >= 128, K >= 128 and the grid keeps at least 256
+ * workgroups, TILED whenever both sides exceed 32,
+ * STREAMING never (64 x 64 at most). No counterpart in the reference (its
+ * GEMMs are library calls); process-wide, for measurement and tests. */
 enum mednext_pw_kernels {
   MEDNEXT_PW_KERNELS_AUTO = 0,
   MEDNEXT_PW_KERNELS_STREAMING = 1,

@@ -1121,6 +1121,158 @@ __global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_ke
   }
 }
 
+// Wide weight-gradient tile: 128 dW rows x 128 columns per workgroup, so X is
+// read once per 128 rows of M and dY once per 128 columns of K (the 64 x 64
+// kernel above reads them twice as often; at the MedNeXt v2 hidden widths
+// that is 3-7x the algorithmic traffic). Per 128-voxel stage the 256 tile rows
+// (128 dY, 128 X) go through LDS exactly as above, but the waves split the
+// output instead of the voxels: wave w owns the 64 x 64 quadrant
+// (w / 2, w % 2) and runs 4 x 4 MFMA tiles over all four 32-voxel steps of the
+// stage. No cross-wave reduction is needed; each wave stores its quadrant of
+// the split's partial directly.
+constexpr int kWgWideRows = 128;
+
+template <int PRO>
+__global__ __launch_bounds__(kPwThreads, 2) void pw_wgrad_wide_kernel(const bf16_t* __restrict__ dy,
+                                                                      const bf16_t* __restrict__ x,
+                                                                      float* __restrict__ partial, PwWGeom g) {
+  constexpr int RM = kWgWideRows, RK = kWgWideRows, ROWS = RM + RK;
+  constexpr int NLD = ROWS * (kWgStage / 8) / kPwThreads;  // 16 loads of 16 bytes per thread per stage
+  static_assert(NLD * kPwThreads == ROWS * (kWgStage / 8), "rows must fill the workgroup");
+  extern __shared__ __align__(16) uint16_t wg_lds[];
+  uint16_t* const tile = wg_lds;
+  float* const aff = reinterpret_cast<float*>(wg_lds + ROWS * kWgPitch);  // AFFINE (s, t) of the X rows
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = lane & 15, q = lane >> 4;
+  const int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int tl = static_cast<int>(lin % (g.mblocks * g.kblocks));
+  const int64_t rest = lin / (g.mblocks * g.kblocks);
+  const int split = static_cast<int>(rest % g.splits);
+  const int64_t n = rest / g.splits;
+  const int m0 = (tl / g.kblocks) * RM;
+  const int k0 = (tl % g.kblocks) * RK;
+  const uint32_t V = g.V;
+  const __amdgpu_buffer_rsrc_t dr = slab_rsrc(dy + n * g.M * static_cast<int64_t>(V), g.M * V * 2u);
+  const __amdgpu_buffer_rsrc_t xr = slab_rsrc(x + n * g.K * static_cast<int64_t>(V), g.K * V * 2u);
+  const uint32_t vbeg = static_cast<uint32_t>(split) * g.span;
+  const uint32_t vend = min(V, vbeg + g.span);
+  const bool do_bias = k0 == 0;
+  if constexpr (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
+    for (int i = threadIdx.x; i < RK; i += kPwThreads) {
+      const int k = k0 + i;
+      aff[i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4]) : 0.f;
+      aff[RK + i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4 + 1]) : 0.f;
+    }
+    __syncthreads();
+  }
+
+  // Load slot u: tile row r = tid / 16 + 16 u (slots 0-7 dY rows, 8-15 X
+  // rows), voxels 8 (tid % 16) .. + 7 of the stage.
+  const int grp = threadIdx.x & 15;
+  uint32_t rbase[NLD];
+  bool rok[NLD];
+#pragma unroll
+  for (int u = 0; u < NLD; ++u) {
+    const int r = (threadIdx.x >> 4) + 16 * u;
+    const int row = r < RM ? m0 + r : k0 + (r - RM);
+    rok[u] = r < RM ? row < g.M : row < g.K;
+    rbase[u] = static_cast<uint32_t>(rok[u] ? row : 0) * V * 2u;
+  }
+  auto load = [&](uint32_t v, uint4 (&regs)[NLD]) {
+    const uint32_t vv = v + 8u * grp;
+    const uint32_t nv = vv < vend ? min(8u, vend - vv) : 0u;
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+      const __amdgpu_buffer_rsrc_t rs = u < NLD / 2 ? dr : xr;
+      if (nv == 8u || nv == 0u) {
+        regs[u] = buf_load16(rs, nv != 0u && rok[u] ? rbase[u] + vv * 2u : kOob);
+      } else {
+        regs[u] = load_group(rs, rbase[u] + vv * 2u, rok[u] ? nv : 0u);
+      }
+    }
+  };
+  float dbs[NLD / 2];
+#pragma unroll
+  for (int u = 0; u < NLD / 2; ++u) dbs[u] = 0.f;
+  auto stash = [&](const uint4 (&regs)[NLD]) {
+#pragma unroll
+    for (int u = 0; u < NLD; ++u) {
+      const int r = (threadIdx.x >> 4) + 16 * u;
+      uint4 v = regs[u];
+      if (u < NLD / 2) {
+        if (do_bias) {
+          dbs[u] += (bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y)) +
+                    (bf16_lo(v.z) + bf16_hi(v.z)) + (bf16_lo(v.w) + bf16_hi(v.w));
+        }
+      } else if (PRO == MEDNEXT_PW_PROLOGUE_GELU) {
+        v = gelu_vec(v);  // gelu(0) = 0: missing voxels stay zero
+      } else if (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
+        v = affine_vec(v, aff[r - RM], aff[RK + r - RM]);
+      }
+      *reinterpret_cast<uint4*>(tile + r * kWgPitch + 8 * grp) = v;
+    }
+  };
+
+  const int wm = wave >> 1, wk = wave & 1;  // this wave's 64 x 64 quadrant
+  f32x4_t acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint4 regs[NLD];
+  uint32_t v = vbeg;
+  load(v, regs);
+  while (v < vend) {
+    stash(regs);
+    __syncthreads();
+    load(v + kWgStage, regs);  // next stage in flight during the MFMAs
+#pragma unroll
+    for (int st = 0; st < kWgStage / 32; ++st) {
+      uint4 bf[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        bf[b] = *reinterpret_cast<const uint4*>(tile + (RM + 64 * wk + 16 * b + c) * kWgPitch + 32 * st + 8 * q);
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const uint4 af = *reinterpret_cast<const uint4*>(tile + (64 * wm + 16 * a + c) * kWgPitch + 32 * st + 8 * q);
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = mfma16x16x32(af, bf[b], acc[a][b]);
+      }
+    }
+    __syncthreads();
+    v += kWgStage;
+  }
+
+  float* out = partial + (n * g.splits + split) * g.stride;
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = m0 + 64 * wm + 16 * a + 4 * q + r;
+      if (m >= g.M) continue;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int k = k0 + 64 * wk + 16 * b + c;
+        if (k < g.K) out[static_cast<int64_t>(m) * g.K + k] = acc[a][b][r];
+      }
+    }
+  if (do_bias) {
+    // Row sums: the 16 threads of a row are 16 consecutive lanes of one wave.
+#pragma unroll
+    for (int u = 0; u < NLD / 2; ++u) {
+      float sum = dbs[u];
+      sum += __shfl_xor(sum, 1);
+      sum += __shfl_xor(sum, 2);
+      sum += __shfl_xor(sum, 4);
+      sum += __shfl_xor(sum, 8);
+      const int m = m0 + (threadIdx.x >> 4) + 16 * u;
+      if (grp == 0 && m < g.M) out[static_cast<int64_t>(g.M) * g.K + m] = sum;
+    }
+  }
+}
+
 // dW / dB = fixed-order fp64 sum of the per-split partials, in two passes so
 // the reduction spreads over the whole GPU. Pass 1: block (eb, r) sums slot
 // range r of R (slots r, r + R, ...) for 64 consecutive outputs; its four
@@ -1555,16 +1707,35 @@ extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const voi
   g.span = static_cast<uint32_t>(wgrad_span(v, splits));
   g.splits = static_cast<int>(cdiv(v, static_cast<int64_t>(g.span)));
   const int tm = tiles_for(m), tk = tiles_for(k);
-  g.mblocks = static_cast<int>(cdiv(m, 16 * tm));
-  g.kblocks = static_cast<int>(cdiv(k, 16 * tk));
+  // 128 x 128 tiles where both sides fill them and the grid still has
+  // kTiledMinBlocks workgroups (any 64 x 64 shape under TILED).
+  const int choice = g_product_kernels.load(std::memory_order_relaxed);
+  const int64_t wide_blocks = n * g.splits * cdiv(m, kWgWideRows) * cdiv(k, kWgWideRows);
+  const bool wide = choice != MEDNEXT_PW_KERNELS_STREAMING &&
+                    (choice == MEDNEXT_PW_KERNELS_TILED
+                         ? tm == 4 && tk == 4
+                         : m >= kWgWideRows && k >= kWgWideRows && wide_blocks >= kTiledMinBlocks);
+  const int side_m = wide ? kWgWideRows : 16 * tm, side_k = wide ? kWgWideRows : 16 * tk;
+  g.mblocks = static_cast<int>(cdiv(m, side_m));
+  g.kblocks = static_cast<int>(cdiv(k, side_k));
   g.stride = m * k + m;
   g.pcoef = static_cast<const double*>(prologue_coef);
   const int64_t blocks = n * g.splits * g.mblocks * static_cast<int64_t>(g.kblocks);
   MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
   const auto s = static_cast<hipStream_t>(stream);
   auto* part = static_cast<float*>(workspace);
-  hipLaunchKernelGGL(pick_wgrad(tm, tk, prologue), dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), 0, s,
-                     static_cast<const bf16_t*>(grad_output), static_cast<const bf16_t*>(x), part, g);
+  if (wide) {
+    const size_t lds = static_cast<size_t>(2 * kWgWideRows) * kWgPitch * 2 +
+                       (prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? 2 * kWgWideRows * sizeof(float) : 0);
+    WgradKernel fn = prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? pw_wgrad_wide_kernel<2>
+                     : prologue == MEDNEXT_PW_PROLOGUE_GELU ? pw_wgrad_wide_kernel<1>
+                                                            : pw_wgrad_wide_kernel<0>;
+    hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds, s,
+                       static_cast<const bf16_t*>(grad_output), static_cast<const bf16_t*>(x), part, g);
+  } else {
+    hipLaunchKernelGGL(pick_wgrad(tm, tk, prologue), dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), 0, s,
+                       static_cast<const bf16_t*>(grad_output), static_cast<const bf16_t*>(x), part, g);
+  }
   MEDNEXT_CHECK_LAUNCH();
   const int64_t total = m * k + m;
   auto* sums = reinterpret_cast<double*>(static_cast<unsigned char*>(workspace) +

@@ -172,3 +172,34 @@ def test_tiled_is_deterministic_and_matches_streaming_closely():
     P.set_pointwise_kernels(P.PW_KERNELS_STREAMING)
     ys = P.pointwise_conv(x, w, b)
     assert rel_l2(y1.float(), ys.float()) <= 4e-3
+
+
+@pytest.mark.parametrize("n,k,m,spatial", [(1, 128, 128, (8, 8, 16)), (2, 160, 272, (5, 7, 9)), (1, 64, 96, (4, 4, 33)),
+                                            (2, 256, 1024, (4, 8, 8))])
+@pytest.mark.parametrize("prologue", ["none", "gelu", "affine"])
+def test_weight_grad_tiles(n, k, m, spatial, prologue):
+    """dW = dY . prologue(X)^T and dB = sum dY with 64 x 64 workgroup tiles
+    (streaming) and 128 x 128 ones (tiled): ragged sides (M = 96, 272; K = 64,
+    160), V % 8 != 0, several splits and samples."""
+    print(f"[pw wgrad tiles] n={n} k={k} m={m} spatial={spatial} prologue={prologue}", flush=True)
+    g = torch.Generator().manual_seed(5 * k + m + len(prologue))
+    x = torch.randn(n, k, *spatial, generator=g).bfloat16()
+    dy = torch.randn(n, m, *spatial, generator=g).bfloat16()
+    coef = torch.randn(n, k, 4, generator=g, dtype=torch.float64)
+    coef[..., 0] = 1 + 0.3 * coef[..., 0]
+    pro = {"none": P.PW_PROLOGUE_NONE, "gelu": P.PW_PROLOGUE_GELU, "affine": P.PW_PROLOGUE_AFFINE}[prologue]
+    xd, dyd, cd = x.to(DEV), dy.to(DEV), coef.to(DEV)
+    outs = run_both(lambda: P.pointwise_weight_grad(dyd, xd, prologue=pro,
+                                                    prologue_coef=cd if prologue == "affine" else None))
+    xf = x.double().flatten(2)
+    if prologue == "gelu":
+        xf = F.gelu(xf)
+    elif prologue == "affine":
+        xf = (xf * coef[..., :1] + coef[..., 1:2]).bfloat16().double()  # rounded per element, as the kernels do
+    dyf = dy.double().flatten(2)
+    want_dw = torch.einsum("nmv,nkv->mk", dyf, xf)
+    want_db = dyf.sum(dim=(0, 2))
+    for dw, db in outs:
+        assert dw.shape == (m, k, 1, 1, 1)
+        assert rel_l2(dw.cpu().view(m, k), want_dw) <= TOL
+        assert rel_l2(db.cpu(), want_db) <= TOL
