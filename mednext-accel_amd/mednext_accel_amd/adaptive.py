@@ -35,6 +35,7 @@ from torch.nn import functional as F
 
 from .optimization.descriptors import ExecutionContext, OperatorDescriptor
 from .optimization.policy_resolver import PolicyDecision, PolicyResolver
+from .precast import cast_param
 
 
 @dataclass(frozen=True, slots=True)
@@ -290,15 +291,16 @@ class AdaptivePointwise3d(_AdaptiveModule):
         strided = self.stride != (1, 1, 1)
         if decision.implementation == "hip_pointwise_gemm" and _gemm_guards(x, self.in_channels, self.out_channels):
             dt = torch.bfloat16
-            bias = self.bias.to(dt) if self.bias is not None else None
+            bias = cast_param(self.bias, dt) if self.bias is not None else None
+            weight = cast_param(self.weight, dt)
             ops = _hip_ops()
             if not strided:
                 op = ops.pointwise_conv_transpose3d if self.transposed else ops.pointwise_conv3d
-                return op(x.to(dt), self.weight.to(dt), bias)
+                return op(x.to(dt), weight, bias)
             if not self.transposed:
                 # Every second voxel, gathered once (autograd scatters its gradient back).
-                return ops.pointwise_conv3d(x[:, :, ::2, ::2, ::2].to(dt).contiguous(), self.weight.to(dt), bias)
-            y = ops.pointwise_conv_transpose3d(x.to(dt), self.weight.to(dt), bias)
+                return ops.pointwise_conv3d(x[:, :, ::2, ::2, ::2].to(dt).contiguous(), weight, bias)
+            y = ops.pointwise_conv_transpose3d(x.to(dt), weight, bias)
             full = tuple(2 * s - 1 for s in x.shape[2:])
             if bias is None:
                 out = y.new_zeros((x.shape[0], self.out_channels, *full))
@@ -361,8 +363,8 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
         hip_ops = _hip_ops()
         dtype = getattr(torch, context.dtype)
         x = x.to(dtype)
-        weight = self.weight.to(dtype)
-        bias = self.bias.to(dtype) if self.bias is not None else None
+        weight = cast_param(self.weight, dtype)
+        bias = cast_param(self.bias, dtype) if self.bias is not None else None
         op = hip_ops.depthwise_conv_transpose3d_stride2 if self.transpose else hip_ops.depthwise_conv3d_stride2
         return op(x, weight, bias, self.kernel_size[0])
 
@@ -391,8 +393,8 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
         hip_ops = _hip_ops()
         dtype = getattr(torch, context.dtype)
         x = x.to(dtype)
-        weight = self.weight.to(dtype)
-        bias = self.bias.to(dtype) if self.bias is not None else None
+        weight = cast_param(self.weight, dtype)
+        bias = cast_param(self.bias, dtype) if self.bias is not None else None
 
         def recipe(decision: PolicyDecision) -> list[int]:
             p = decision.parameters
@@ -515,9 +517,9 @@ class AdaptiveExpansion:
     def __call__(self, h: Tensor, residual: Tensor | None) -> Tensor:
         b = self.block
         dt = torch.bfloat16
-        w1, w2 = b.expand.weight.to(dt), b.project.weight.to(dt)
-        b1 = b.expand.bias.to(dt) if b.expand.bias is not None else None
-        b2 = b.project.bias.to(dt) if b.project.bias is not None else None
+        w1, w2 = cast_param(b.expand.weight, dt), cast_param(b.project.weight, dt)
+        b1 = cast_param(b.expand.bias, dt) if b.expand.bias is not None else None
+        b2 = cast_param(b.project.bias, dt) if b.project.bias is not None else None
         fuse_residual = residual is not None and residual.dtype == dt and residual.is_contiguous()
         res = residual if fuse_residual else None
         if b.expand.out_channels >= self.stored_gelu_from:

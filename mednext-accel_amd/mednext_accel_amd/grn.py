@@ -24,6 +24,7 @@ from torch import Tensor, nn
 from .adaptive import ModelOptimizationContext, _context_from_tensor, _hip_ops, device_facts
 from .optimization.descriptors import OperatorDescriptor
 from .optimization.policy_resolver import PolicyResolver
+from .precast import cast_param
 
 
 def global_response_norm3d_reference(x: Tensor, gamma: Tensor, beta: Tensor, eps: float = 1e-6) -> Tensor:
@@ -165,9 +166,9 @@ class AdaptiveGRNExpansion:
     def __call__(self, h: Tensor, residual: Tensor | None) -> Tensor:
         b = self.block
         dt = torch.bfloat16
-        w1, w2 = b.expand.weight.to(dt), b.project.weight.to(dt)
-        b1 = b.expand.bias.to(dt) if b.expand.bias is not None else None
-        b2 = b.project.bias.to(dt) if b.project.bias is not None else None
+        w1, w2 = cast_param(b.expand.weight, dt), cast_param(b.project.weight, dt)
+        b1 = cast_param(b.expand.bias, dt) if b.expand.bias is not None else None
+        b2 = cast_param(b.project.bias, dt) if b.project.bias is not None else None
         fuse_residual = residual is not None and residual.dtype == dt and residual.is_contiguous()
         out, _a, _dgelu, _coef = _hip_ops().grn_expansion(
             h.to(dt), w1, b1, w2, b2, b.grn.gamma, b.grn.beta, residual if fuse_residual else None, float(b.grn.eps)

@@ -42,6 +42,7 @@ from .config import MedNeXtV1Config, get_mednext_v1_config
 from .optimization.policies import PolicyRegistry
 from .optimization.policy_resolver import PolicyDecision
 from .optimization.report import OptimizationReport
+from .precast import install_weight_precast
 
 DeepSupervisionOutput = Literal["tuple", "list", "stacked"]
 OptimizationSource: TypeAlias = Literal["auto", "reference"] | str | PathLike[str] | Mapping[str, object]
@@ -273,6 +274,7 @@ def configure_optimization(model: MedNeXtV1, optimization: OptimizationSource) -
         "mednext_v1", model.config.variant, checkpoint_name(model.checkpointing), model.approximate_gelu_eval
     )
     install_adaptive_operators(model, resolver=resolver, model_context=model_context)
+    install_weight_precast(model)
     model.__dict__["_optimization_resolver"] = resolver
     model.__dict__["_optimization_model_context"] = model_context
     return model

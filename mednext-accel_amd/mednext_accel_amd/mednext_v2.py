@@ -48,6 +48,7 @@ from .grn import (
     install_fused_grn_expansions,
 )
 from .mednext_v1 import DeepSupervisionOutput, OptimizationSource, checkpoint_name, spatial_shape_for_role
+from .precast import install_weight_precast
 from .optimization.descriptors import OperatorDescriptor
 from .optimization.policies import PolicyRegistry
 from .optimization.policy_resolver import PolicyDecision
@@ -259,6 +260,7 @@ def configure_optimization(model: MedNeXtV2, optimization: OptimizationSource) -
     install_adaptive_operators(model, resolver=resolver, model_context=model_context)
     install_adaptive_grn(model, resolver=resolver, model_context=model_context)
     install_fused_grn_expansions(model, resolver=resolver, model_context=model_context)
+    install_weight_precast(model)
     model.__dict__["_optimization_resolver"] = resolver
     model.__dict__["_optimization_model_context"] = model_context
     return model

@@ -1,0 +1,65 @@
+"""The per-forward parameter pre-cast (precast.py) on the CPU: the batched cast
+is the per-tensor casts (values, gradients, unused outputs), and a model with
+the pre-cast installed trains exactly like one without."""
+
+from __future__ import annotations
+
+import copy
+from dataclasses import replace
+
+import torch
+
+from mednext_accel_amd import MedNeXtV1
+from mednext_accel_amd.config import get_mednext_v1_config
+from mednext_accel_amd.mednext_v1 import configure_optimization
+from mednext_accel_amd.precast import _CastMany, cast_param, precast_parameters
+
+
+def test_cast_many_is_the_per_tensor_casts():
+    gen = torch.Generator().manual_seed(3)
+    params = [torch.randn(shape, generator=gen, requires_grad=True) for shape in ((3, 4), (5,), (2, 1, 3, 3, 3))]
+    outs = _CastMany.apply(torch.bfloat16, *params)
+    for o, p in zip(outs, params, strict=True):
+        assert o.dtype == torch.bfloat16 and o.shape == p.shape
+        assert torch.equal(o, p.detach().to(torch.bfloat16))
+    grads = [torch.randn(o.shape, generator=gen).bfloat16() for o in outs]
+    torch.autograd.backward([outs[0], outs[2]], [grads[0], grads[2]])  # the second copy is unused
+    assert torch.equal(params[0].grad, grads[0].float())
+    assert params[1].grad is None
+    assert torch.equal(params[2].grad, grads[2].float())
+
+
+def test_cast_param_outside_a_forward_is_a_plain_cast():
+    p = torch.randn(4, 3)
+    assert torch.equal(cast_param(p, torch.bfloat16), p.to(torch.bfloat16))
+    assert cast_param(p, torch.float32) is p
+
+
+def test_model_with_precast_trains_like_one_without():
+    cfg = replace(get_mednext_v1_config("base", in_channels=1, out_channels=2, kernel_size=3, deep_supervision=False),
+                  base_channels=4, block_counts=(1,) * 9)
+    torch.manual_seed(0)
+    model = configure_optimization(MedNeXtV1(cfg), "auto").train()
+    assert len(precast_parameters(model)) == len(model.__dict__["_mednext_precast_params"]) > 0
+    plain = copy.deepcopy(model)
+    plain.__dict__["_mednext_precast_params"] = []  # hooks stay, but cast nothing
+    x = torch.randn(1, 1, 32, 32, 32)
+    for m in (model, plain):
+        with torch.autocast("cpu", dtype=torch.bfloat16):
+            m(x).float().square().mean().backward()
+    for (name, p), q in zip(model.named_parameters(), plain.parameters(), strict=True):
+        assert (p.grad is None) == (q.grad is None), name
+        if p.grad is not None:
+            assert torch.equal(p.grad, q.grad), name
+
+
+def test_copies_start_on_16_byte_boundaries():
+    params = [torch.randn(n, requires_grad=True) for n in (3, 8, 13, 1, 27)]
+    outs = _CastMany.apply(torch.bfloat16, *params)
+    base = outs[0].data_ptr()
+    for o, p in zip(outs, params, strict=True):
+        assert (o.data_ptr() - base) % 16 == 0
+        assert torch.equal(o, p.detach().bfloat16())
+    sum(o.float().sum() for o in outs).backward()
+    for p in params:
+        assert torch.equal(p.grad, torch.ones_like(p))
