@@ -255,7 +255,8 @@ int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* 
 enum mednext_pw_kernels {
   MEDNEXT_PW_KERNELS_AUTO = 0,
   MEDNEXT_PW_KERNELS_STREAMING = 1,
-  MEDNEXT_PW_KERNELS_TILED = 2
+  MEDNEXT_PW_KERNELS_TILED = 2,
+  MEDNEXT_PW_KERNELS_TILED_64 = 3 /* TILED with 64-row workgroups; 64 x 64 weight-gradient tiles */
 };
 int32_t mednext_pointwise_set_kernels(int32_t choice);
 /* 1 if a launch of this shape and mode (blocks_per_sample 0) runs the tiled

@@ -758,13 +758,17 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
   constexpr int F16 = 4 * MT;  // 16-row fragments per workgroup
   constexpr int XS = 8 * 64;   // uint4 per X slice: eight B operands x 64 lanes
   constexpr int WS = F16 * 64; // uint4 per weight slice
-  constexpr int STAGE = kTileSlices * (XS + WS);
+  constexpr int SLICE = XS + WS;  // one slice's B operands followed by its A fragments
   constexpr bool kAux = epi_has_aux(EPI);
   constexpr bool kAux2 = EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE;
   constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_AFFINE;
   extern __shared__ __align__(16) uint16_t pw_lds[];
   uint4* const stages = reinterpret_cast<uint4*>(pw_lds);
-  float* const bias_lds = reinterpret_cast<float*>(stages + 2 * STAGE);
+  // LDS holds only the slices used: min(2, ks) per stage, and a second stage
+  // only when K takes more than one step.
+  const int sps = min(kTileSlices, g.ks);
+  const int nstages = g.ks > kTileSlices ? 2 : 1;
+  float* const bias_lds = reinterpret_cast<float*>(stages + nstages * sps * SLICE);
   float* const c0_lds = bias_lds + BM;
   float* const c1_lds = c0_lds + BM;
   float* const kcoef = c1_lds + BM;  // AFFINE: (s, t) per input channel
@@ -848,11 +852,11 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
       }
       uint4 bv[8];
       transpose8x8(cur, bv);
-      uint4* dst = stage + wave * XS + lane;
+      uint4* dst = stage + wave * SLICE + lane;
 #pragma unroll
       for (int j = 0; j < 8; ++j) dst[j * 64] = bv[j];
     } else {
-      uint4* dst = stage + kTileSlices * XS + wslot * WS;
+      uint4* dst = stage + wslot * SLICE + XS;
       if (!g.wt) {
 #pragma unroll
         for (int f = 0; f < F16; ++f) dst[f * 64 + lane] = rg[f];
@@ -895,7 +899,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
   if (my_slice < g.ks) load_slice(my_slice);
   __syncthreads();  // row vectors and AFFINE coefficients
   for (int s = 0; s < steps; ++s) {
-    uint4* const stage = stages + (s & 1) * STAGE;
+    uint4* const stage = stages + (s & 1) * sps * SLICE;
     const int slice = kTileSlices * s + my_slice;
     if (slice < g.ks) store_slice(slice, stage);
     if (slice + kTileSlices < g.ks) load_slice(slice + kTileSlices);
@@ -904,8 +908,8 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
 #pragma unroll
       for (int sl = 0; sl < kTileSlices; ++sl) {
         if (kTileSlices * s + sl < g.ks) {
-          const uint4* xs = stage + sl * XS + lane;
-          const uint4* ws = stage + kTileSlices * XS + sl * WS + (MT * wave) * 64 + lane;
+          const uint4* xs = stage + sl * SLICE + lane;
+          const uint4* ws = stage + sl * SLICE + XS + (MT * wave) * 64 + lane;
           uint4 a[MT];
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) a[mt] = ws[mt * 64];
@@ -1416,7 +1420,9 @@ int pick_mt(int64_t k, int64_t m, int epi) {
   const bool aux = epi_has_aux(epi);
   auto fits = [&](int mt) { return static_cast<size_t>(16 * mt) * ks * 32 * 2 <= kMaxWeightLds; };
   if (ks >= kSplitKSlices) return m > 16 && fits(2) ? 2 : 1;
-  if (epi == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) return 1;  // two aux rows per output row
+  // Two aux rows per output row: two m-tiles fit the register budget only with
+  // the single-slice loop unrolled (K <= 32).
+  if (epi == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) return ks == 1 && m > 16 && fits(2) ? 2 : 1;
   if (!aux && ks == 1 && m > 32 && fits(4)) return 4;
   if (m > 16 && fits(2)) return 2;
   return 1;
@@ -1553,7 +1559,7 @@ bool tiled_pays(const FwdPlan& p, int64_t n, int64_t m, int64_t v) {
 int32_t launch_tiled(const void* x, const void* weight, const void* bias, const void* aux, void* y, const PwExtra& ex,
                      int64_t n, int64_t k, int64_t m, int64_t v, int32_t weight_layout, int32_t prologue,
                      int32_t epilogue, void* stream) {
-  const int mt = tiled_mt(n, m, v);
+  const int mt = g_product_kernels.load(std::memory_order_relaxed) == MEDNEXT_PW_KERNELS_TILED_64 ? 1 : tiled_mt(n, m, v);
   PwGeom g{};
   g.K = static_cast<int>(k);
   g.M = static_cast<int>(m);
@@ -1565,8 +1571,10 @@ int32_t launch_tiled(const void* x, const void* weight, const void* bias, const 
   g.wt = weight_layout;
   const int64_t blocks = n * g.mgroups * g.chunks;
   MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
-  const size_t stage = static_cast<size_t>(kTileSlices) * (8 * 64 + 4 * mt * 64) * 16;
-  const size_t lds = 2 * stage + 3 * 64 * mt * sizeof(float) +
+  const int64_t sps = std::min<int64_t>(kTileSlices, g.ks);
+  const int64_t nstages = g.ks > kTileSlices ? 2 : 1;
+  const size_t slice = static_cast<size_t>(8 * 64 + 4 * mt * 64) * 16;
+  const size_t lds = static_cast<size_t>(nstages * sps) * slice + 3 * 64 * mt * sizeof(float) +
                      (prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? 2 * static_cast<size_t>(k) * sizeof(float) : 0);
   FwdKernel fn = mt == 1 ? tiled_instance<1>(prologue, epilogue) : tiled_instance<2>(prologue, epilogue);
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds, static_cast<hipStream_t>(stream),
@@ -1579,8 +1587,8 @@ int32_t launch_tiled(const void* x, const void* weight, const void* bias, const 
 }  // namespace
 
 extern "C" int32_t mednext_pointwise_set_kernels(int32_t choice) {
-  MEDNEXT_CHECK_ARG(choice >= MEDNEXT_PW_KERNELS_AUTO && choice <= MEDNEXT_PW_KERNELS_TILED,
-                    "choice must be MEDNEXT_PW_KERNELS_AUTO, _STREAMING or _TILED");
+  MEDNEXT_CHECK_ARG(choice >= MEDNEXT_PW_KERNELS_AUTO && choice <= MEDNEXT_PW_KERNELS_TILED_64,
+                    "choice must be MEDNEXT_PW_KERNELS_AUTO, _STREAMING, _TILED or _TILED_64");
   g_product_kernels.store(choice, std::memory_order_relaxed);
   return MEDNEXT_STATUS_OK;
 }
@@ -1590,7 +1598,8 @@ extern "C" int32_t mednext_pointwise_uses_tiled(int64_t n, int64_t k, int64_t m,
   if (n < 1 || k < 1 || k > kMaxK || m < 1 || v < 1 || !pro_epi_supported(prologue, epilogue)) return 0;
   const int choice = g_product_kernels.load(std::memory_order_relaxed);
   if (choice == MEDNEXT_PW_KERNELS_STREAMING || !tiled_eligible(k, m, prologue, epilogue)) return 0;
-  return choice == MEDNEXT_PW_KERNELS_TILED || tiled_pays(plan_fwd(n, k, m, v, epilogue, 0), n, m, v) ? 1 : 0;
+  if (choice == MEDNEXT_PW_KERNELS_TILED || choice == MEDNEXT_PW_KERNELS_TILED_64) return 1;
+  return tiled_pays(plan_fwd(n, k, m, v, epilogue, 0), n, m, v) ? 1 : 0;
 }
 
 extern "C" int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, int64_t v,
@@ -1711,10 +1720,10 @@ extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const voi
   // kTiledMinBlocks workgroups (any 64 x 64 shape under TILED).
   const int choice = g_product_kernels.load(std::memory_order_relaxed);
   const int64_t wide_blocks = n * g.splits * cdiv(m, kWgWideRows) * cdiv(k, kWgWideRows);
-  const bool wide = choice != MEDNEXT_PW_KERNELS_STREAMING &&
-                    (choice == MEDNEXT_PW_KERNELS_TILED
-                         ? tm == 4 && tk == 4
-                         : m >= kWgWideRows && k >= kWgWideRows && wide_blocks >= kTiledMinBlocks);
+  const bool wide = choice == MEDNEXT_PW_KERNELS_TILED
+                        ? tm == 4 && tk == 4
+                        : choice == MEDNEXT_PW_KERNELS_AUTO && m >= kWgWideRows && k >= kWgWideRows &&
+                              wide_blocks >= kTiledMinBlocks;
   const int side_m = wide ? kWgWideRows : 16 * tm, side_k = wide ? kWgWideRows : 16 * tk;
   g.mblocks = static_cast<int>(cdiv(m, side_m));
   g.kblocks = static_cast<int>(cdiv(k, side_k));

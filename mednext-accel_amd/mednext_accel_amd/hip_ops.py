@@ -281,7 +281,7 @@ PW_EPILOGUE_ROW_REDUCE, PW_EPILOGUE_AFFINE_SCALE, PW_EPILOGUE_BIAS_GELU_PAIR, PW
 #: Forward kernel family (include/mednext_hip.h ``mednext_pw_kernels``): the
 #: library's automatic choice, the streaming kernels only, or the LDS-tiled
 #: kernel wherever it applies.
-PW_KERNELS_AUTO, PW_KERNELS_STREAMING, PW_KERNELS_TILED = 0, 1, 2
+PW_KERNELS_AUTO, PW_KERNELS_STREAMING, PW_KERNELS_TILED, PW_KERNELS_TILED_64 = 0, 1, 2, 3
 
 
 def set_pointwise_kernels(choice: int) -> None:

@@ -87,7 +87,9 @@ def test_pointwise_kernel_choice_is_host_logic():
         assert not uses(2, 1024, 120, 32768)
         P.set_pointwise_kernels(P.PW_KERNELS_STREAMING)
         assert not uses(2, 1024, 128, 32768)
+        P.set_pointwise_kernels(P.PW_KERNELS_TILED_64)
+        assert uses(2, 32, 96, 128**3) and not uses(2, 1024, 120, 32768)
         with pytest.raises(_hip.HipLibraryError):
-            P.set_pointwise_kernels(3)
+            P.set_pointwise_kernels(4)
     finally:
         P.set_pointwise_kernels(P.PW_KERNELS_AUTO)

@@ -31,8 +31,10 @@ def _restore_choice():
 
 
 def run_both(fn):
+    """fn() with the streaming kernels, the tiled kernel (64- or 128-row
+    workgroups by the library's choice) and the tiled kernel at 64 rows."""
     outs = []
-    for choice in (P.PW_KERNELS_STREAMING, P.PW_KERNELS_TILED):
+    for choice in (P.PW_KERNELS_STREAMING, P.PW_KERNELS_TILED, P.PW_KERNELS_TILED_64):
         P.set_pointwise_kernels(choice)
         outs.append(fn())
     P.set_pointwise_kernels(P.PW_KERNELS_AUTO)
