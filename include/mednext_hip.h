@@ -339,6 +339,27 @@ int32_t mednext_grn_bwd(const void* grad_output, int32_t dy_dtype, const void* x
                         int64_t spatial, double eps, int32_t splits, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------ up-block join
+ * The tail of a MedNeXt up block, bf16: out [N][C][D][H][W] (D, H even, W a
+ * multiple of 8) = pad(main) + pad(residual), where main is the block's
+ * [N][C][D-1][H-1][W-1] output, the residual is the stride-2 transposed
+ * 1x1x1 conv with bias b [C] (nullable) whose GEMM output y = W^T x + b at
+ * the even grid points is small [N][C][D/2][H/2][W/2], and the pad is one
+ * voxel per dimension at the start (lead 1, MedNeXt v1) or at the end (lead
+ * 0, v2). Replaces the F.pad / conv_transpose3d / add sequence of the
+ * reference's up blocks (models/blocks.py:176-181, models/blocks_v2.py:128-133).
+ * The backward writes grad_main (on the grid), grad_small (the even grid
+ * points) and, when grad_bias != NULL, grad_bias = the sum of grad_out over
+ * the other grid points (fixed-order fp64 reduction of per-plane fp32
+ * partials in the caller's workspace). */
+int32_t mednext_up_join_fwd(const void* main_in, const void* small, const void* bias, void* out, int64_t n,
+                            int64_t c, int64_t d, int64_t h, int64_t w, int32_t lead, int32_t dtype,
+                            void* stream);
+size_t mednext_up_join_bwd_workspace_bytes(int64_t n, int64_t c, int64_t d);
+int32_t mednext_up_join_bwd(const void* grad_out, void* grad_main, void* grad_small, void* grad_bias,
+                            void* workspace, size_t workspace_bytes, int64_t n, int64_t c, int64_t d,
+                            int64_t h, int64_t w, int32_t lead, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

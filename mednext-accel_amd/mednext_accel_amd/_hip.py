@@ -92,6 +92,12 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _i64, _p, _p, _i32, _p, _p, _p, _i64, _i64, c_double, _p, c_size_t, _p),
     ),
+    "mednext_up_join_fwd": (_i32, (_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p)),
+    "mednext_up_join_bwd_workspace_bytes": (c_size_t, (_i64, _i64, _i64)),
+    "mednext_up_join_bwd": (
+        _i32,
+        (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p),
+    ),
     "mednext_depthwise3d_s2_gather": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
     "mednext_depthwise3d_s2_scatter": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
     "mednext_depthwise3d_s2_wgrad_workspace_bytes": (c_size_t, (*(_i64,) * 8, _i32, _i32)),
@@ -101,7 +107,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

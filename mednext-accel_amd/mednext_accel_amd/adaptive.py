@@ -285,6 +285,22 @@ class AdaptivePointwise3d(_AdaptiveModule):
         out = torch.stack(rows).reshape(x.shape[0], self.out_channels, *spatial)
         return out.squeeze(0) if squeeze else out
 
+    def join_parts(self, x: Tensor) -> tuple[Tensor, Tensor | None] | None:
+        """For a stride-2 transposed 1x1x1 conv on the matrix-core route: the
+        GEMM output at the input's voxels (bias included) and the bf16 bias,
+        which an up block turns into its padded residual sum in one pass
+        (``hip_ops.up_block_join``); None when this module would not take the
+        HIP route for ``x``."""
+        if not (self.transposed and self.stride == (2, 2, 2)):
+            return None
+        context = _context_from_tensor(x, self.model_context, training=self.training)
+        decision = self.resolver.resolve(self.descriptor, context, context.phase)
+        if decision.implementation != "hip_pointwise_gemm" or not _gemm_guards(x, self.in_channels, self.out_channels):
+            return None
+        dt = torch.bfloat16
+        bias = cast_param(self.bias, dt) if self.bias is not None else None
+        return _hip_ops().pointwise_conv_transpose3d(x.to(dt), cast_param(self.weight, dt), bias), bias
+
     def forward(self, x: Tensor) -> Tensor:
         context = _context_from_tensor(x, self.model_context, training=self.training)
         decision = self.resolver.resolve(self.descriptor, context, context.phase)

@@ -161,8 +161,40 @@ class MedNeXtUpBlock(MedNeXtBlock):
         self._pad = (1, 0) * spatial_dims  # one leading voxel per dim: 2s-1 -> 2s
 
     def forward(self, x: Tensor) -> Tensor:
-        out = F.pad(super().forward(x), self._pad)
+        main = super().forward(x)
+        if self.residual is not None:
+            joined = join_up_residual(self.residual, x, main, lead=1)
+            if joined is not None:
+                return joined
+        out = F.pad(main, self._pad)
         return out if self.residual is None else out + F.pad(self.residual(x), self._pad)
+
+
+def join_up_residual(residual: nn.Module, x: Tensor, main: Tensor, *, lead: int) -> Tensor | None:
+    """``pad(main) + pad(residual(x))`` of an up block in one HIP pass
+    (``hip_ops.up_block_join``) when the residual's stride-2 transposed 1x1x1
+    conv takes the matrix-core route and the shapes fit (bf16, main
+    contiguous at 2s - 1 per dimension, the padded width a multiple of 8);
+    None otherwise, and the caller pads and adds as usual. ``lead`` 1 pads at
+    the start (v1), 0 at the end (v2)."""
+    parts_of = getattr(residual, "join_parts", None)
+    if (
+        parts_of is None
+        or not main.is_cuda
+        or main.dtype != torch.bfloat16
+        or main.ndim != 5
+        or not main.is_contiguous()
+        or tuple(main.shape[2:]) != tuple(2 * s - 1 for s in x.shape[2:])
+        or (main.shape[-1] + 1) % 8 != 0
+    ):
+        return None
+    parts = parts_of(x)
+    if parts is None:
+        return None
+    from . import hip_ops
+
+    small, bias = parts
+    return hip_ops.up_block_join(main, small, bias, lead)
 
 
 class OutputHead(nn.Module):

@@ -20,7 +20,7 @@ from torch import Tensor, nn
 from torch.nn import functional as F
 from torch.utils.checkpoint import checkpoint
 
-from .blocks import EvalModeGELU
+from .blocks import EvalModeGELU, join_up_residual
 from .grn import GlobalResponseNorm3d
 
 
@@ -121,7 +121,12 @@ class MedNeXtV2UpBlock(MedNeXtV2Block):
         self._pad = (0, 1) * 3  # one trailing voxel per dim: 2s-1 -> 2s
 
     def forward(self, x: Tensor) -> Tensor:
-        out = F.pad(super().forward(x), self._pad)
+        main = super().forward(x)
+        if self.residual is not None:
+            joined = join_up_residual(self.residual, x, main, lead=0)
+            if joined is not None:
+                return joined
+        out = F.pad(main, self._pad)
         return out if self.residual is None else out + F.pad(self.residual(x), self._pad)
 
 

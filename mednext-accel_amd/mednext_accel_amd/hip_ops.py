@@ -1043,6 +1043,104 @@ def _t2_backward(ctx, grad_output):
 depthwise_conv_transpose3d_stride2.register_autograd(_t2_backward, setup_context=_setup_s2)
 
 
+# ---------------------------------------------------------------- up-block join
+
+
+def _check_join(main: Tensor, small: Tensor, bias: Tensor | None) -> tuple[int, ...]:
+    _check_device(main, small)
+    for t, name in ((main, "main"), (small, "small")):
+        if t.dtype != torch.bfloat16 or not t.is_contiguous() or t.ndim != 5:
+            raise ValueError(f"{name} must be a contiguous bfloat16 NCDHW tensor")
+    n, c = main.shape[:2]
+    d, h, w = (int(s) + 1 for s in main.shape[2:])
+    if tuple(small.shape) != (n, c, d // 2, h // 2, w // 2) or d % 2 or h % 2 or w % 8:
+        raise ValueError("main must be [N, C, 2a-1, 2b-1, 2c-1] with 2c % 8 == 0 and small [N, C, a, b, c]")
+    if bias is not None and (bias.shape != (c,) or bias.dtype != torch.bfloat16):
+        raise ValueError("bias must be a bfloat16 [C] tensor")
+    return n, c, d, h, w
+
+
+def up_join(main: Tensor, small: Tensor, bias: Tensor | None, lead: int) -> Tensor:
+    """``pad(main) + pad(residual)`` of a MedNeXt up block in one pass: the
+    residual is the stride-2 transposed 1x1x1 conv whose GEMM output (bias
+    included) at the even grid points is ``small`` and whose value elsewhere
+    is ``bias``; the one-voxel pad is at the start (``lead=1``, v1) or the end
+    (``lead=0``, v2)."""
+    n, c, d, h, w = _check_join(main, small, bias)
+    out = main.new_empty((n, c, d, h, w))
+    _hip.check(
+        _hip.load().mednext_up_join_fwd(
+            main.data_ptr(), small.data_ptr(), _hip.ptr(bias), out.data_ptr(), n, c, d, h, w, int(lead),
+            _hip.DTYPE_CODES[torch.bfloat16], _hip.stream_of(main),
+        ),
+        "mednext_up_join_fwd",
+    )
+    return out
+
+
+def up_join_backward(grad_out: Tensor, lead: int, with_bias: bool) -> tuple[Tensor, Tensor, Tensor | None]:
+    """(grad_main, grad_small, grad_bias or None) of ``up_join``."""
+    _check_device(grad_out)
+    if grad_out.dtype != torch.bfloat16 or not grad_out.is_contiguous() or grad_out.ndim != 5:
+        raise ValueError("grad_out must be a contiguous bfloat16 NCDHW tensor")
+    n, c, d, h, w = (int(s) for s in grad_out.shape)
+    gmain = grad_out.new_empty((n, c, d - 1, h - 1, w - 1))
+    gsmall = grad_out.new_empty((n, c, d // 2, h // 2, w // 2))
+    gbias = grad_out.new_empty((c,)) if with_bias else None
+    lib = _hip.load()
+    nbytes = lib.mednext_up_join_bwd_workspace_bytes(n, c, d)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=grad_out.device)
+    _hip.check(
+        lib.mednext_up_join_bwd(
+            grad_out.data_ptr(), gmain.data_ptr(), gsmall.data_ptr(), _hip.ptr(gbias), ws.data_ptr(), nbytes,
+            n, c, d, h, w, int(lead), _hip.DTYPE_CODES[torch.bfloat16], _hip.stream_of(grad_out),
+        ),
+        "mednext_up_join_bwd",
+    )
+    return gmain, gsmall, gbias
+
+
+@torch.library.custom_op("mednext_accel_amd::up_block_join", mutates_args=())
+def up_block_join(main: Tensor, small: Tensor, bias: Tensor | None, lead: int) -> Tensor:
+    """Custom-op form of ``up_join`` (reference models/blocks.py:179-181,
+    models/blocks_v2.py:131-133)."""
+    return up_join(main, small, bias, lead)
+
+
+@up_block_join.register_fake
+def _(main, small, bias, lead):
+    return main.new_empty((main.shape[0], main.shape[1], *(s + 1 for s in main.shape[2:])))
+
+
+@torch.library.custom_op("mednext_accel_amd::up_block_join_backward", mutates_args=())
+def up_block_join_backward_op(grad_out: Tensor, lead: int, with_bias: bool) -> tuple[Tensor, Tensor, Tensor]:
+    gmain, gsmall, gbias = up_join_backward(grad_out.contiguous(), lead, with_bias)
+    return gmain, gsmall, gbias if gbias is not None else grad_out.new_empty((0,))
+
+
+@up_block_join_backward_op.register_fake
+def _(grad_out, lead, with_bias):
+    n, c, d, h, w = grad_out.shape
+    return (grad_out.new_empty((n, c, d - 1, h - 1, w - 1)), grad_out.new_empty((n, c, d // 2, h // 2, w // 2)),
+            grad_out.new_empty((c,) if with_bias else (0,)))
+
+
+def _setup_join(ctx, inputs, output):
+    _main, _small, bias, lead = inputs
+    ctx.lead = lead
+    ctx.has_bias = bias is not None
+
+
+def _join_backward(ctx, grad_out):
+    need_main, need_small, need_bias = ctx.needs_input_grad[:3]
+    with_bias = ctx.has_bias and need_bias
+    gmain, gsmall, gbias = up_block_join_backward_op(grad_out.contiguous(), ctx.lead, with_bias)
+    return (gmain if need_main else None, gsmall if need_small else None, gbias if with_bias else None, None)
+
+
+up_block_join.register_autograd(_join_backward, setup_context=_setup_join)
+
+
 # ------------------------------------------------------------------------ GRN
 
 
