@@ -1035,8 +1035,12 @@ def _t2_backward(ctx, grad_output):
     dw = depthwise_s2_wgrad_op(grad_output, x, ctx.kernel_size)[0] if need_w else None
     db = None
     if need_b and ctx.has_bias:
-        db = grad_output.sum(dim=(0, 2, 3, 4), dtype=torch.float64 if x.dtype == torch.float64 else torch.float32)
-        db = db.to(x.dtype)
+        # Per-(n, c) sums over the contiguous voxels first: a last-dimension
+        # reduction runs at memory speed, a reduction over dims (0, 2, 3, 4)
+        # of an NCDHW tensor at about a quarter of it.
+        acc = torch.float64 if x.dtype == torch.float64 else torch.float32
+        db = grad_output.reshape(grad_output.shape[0], grad_output.shape[1], -1).sum(dim=2, dtype=acc)
+        db = db.sum(dim=0).to(x.dtype)
     return dx, dw, db, None
 
 
