@@ -35,7 +35,7 @@ from torch.nn import functional as F
 
 from .optimization.descriptors import ExecutionContext, OperatorDescriptor
 from .optimization.policy_resolver import PolicyDecision, PolicyResolver
-from .precast import cast_param
+from .precast import cast_param, precast_or_param
 
 
 @dataclass(frozen=True, slots=True)
@@ -325,7 +325,7 @@ class AdaptivePointwise3d(_AdaptiveModule):
             out[:, :, ::2, ::2, ::2] = y
             return out
         if self.transposed:
-            return F.conv_transpose3d(x, self.weight, self.bias, stride=self.stride)
+            return F.conv_transpose3d(x, precast_or_param(self.weight), precast_or_param(self.bias), stride=self.stride)
         if (
             decision.implementation == "pointwise_gemm_per_sample"
             and not strided
@@ -334,7 +334,7 @@ class AdaptivePointwise3d(_AdaptiveModule):
             and x.is_contiguous()
         ):
             return self._gemm(x)
-        return F.conv3d(x, self.weight, self.bias, stride=self.stride)
+        return F.conv3d(x, precast_or_param(self.weight), precast_or_param(self.bias), stride=self.stride)
 
 
 class AdaptiveDepthwise3d(_AdaptiveModule):
@@ -364,9 +364,11 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
     def _reference(self, x: Tensor) -> Tensor:
         if self.transpose:
             return F.conv_transpose3d(
-                x, self.weight, self.bias, self.stride, self.padding, self.output_padding, self.groups, self.dilation
+                x, precast_or_param(self.weight), precast_or_param(self.bias), self.stride, self.padding,
+                self.output_padding, self.groups, self.dilation,
             )
-        return F.conv3d(x, self.weight, self.bias, self.stride, self.padding, self.dilation, self.groups)
+        return F.conv3d(x, precast_or_param(self.weight), precast_or_param(self.bias), self.stride, self.padding,
+                        self.dilation, self.groups)
 
     def _forward_stride2(self, x: Tensor, context: ExecutionContext) -> Tensor:
         """Down-block (stride 2) and up-block (transposed, stride 2) routes: the

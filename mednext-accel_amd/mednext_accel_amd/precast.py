@@ -64,6 +64,16 @@ def _unpacked(flat: Tensor, meta) -> list[Tensor]:
     return views
 
 
+def precast_or_param(p: Tensor | None) -> Tensor | None:
+    """The current forward's pre-cast copy of ``p`` if there is one, else ``p``
+    itself: for operators that leave the casting to autocast (a native
+    convolution then finds its weight already in the autocast dtype and casts
+    nothing)."""
+    if p is None or _ACTIVE is None:
+        return p
+    return _ACTIVE.get(id(p), p)
+
+
 class _CastMany(torch.autograd.Function):
     """``tuple(p.to(dtype) for p in params)`` with one concatenation and one
     cast kernel each way. The copies are views of one buffer, each starting on
@@ -147,4 +157,4 @@ def install_weight_precast(model: nn.Module, dtype: torch.dtype = torch.bfloat16
     return len(params)
 
 
-__all__ = ["cast_param", "install_weight_precast", "precast_parameters"]
+__all__ = ["cast_param", "install_weight_precast", "precast_or_param", "precast_parameters"]
