@@ -62,10 +62,14 @@ def make_training_step(
     autocast_dtype: torch.dtype | None = torch.bfloat16,
     device: torch.device | str | None = None,
     capturable: bool = False,
+    fused_optimizer: bool | None = None,
 ) -> TrainingStep:
     """Synthetic inputs (seeded on the CPU generator, then moved) and AdamW
     (``capturable=True``: its step counters live on the device, as a captured
-    step needs)."""
+    step needs). ``fused_optimizer`` (default: on for GPU parameters) selects
+    PyTorch's single-pass AdamW kernel over its multi-tensor form: the same
+    update, one read and write of parameters, gradients and moments instead
+    of one per elementwise stage."""
     device = torch.device(device) if device is not None else next(model.parameters()).device
     gen = torch.Generator().manual_seed(seed)
     sample = torch.randn(batch, in_channels, size, size, size, generator=gen).to(device)
@@ -81,7 +85,9 @@ def make_training_step(
         if s % 2:
             break
         s //= 2
-    optimizer = torch.optim.AdamW(model.parameters(), lr=lr, capturable=capturable)
+    if fused_optimizer is None:
+        fused_optimizer = device.type == "cuda"
+    optimizer = torch.optim.AdamW(model.parameters(), lr=lr, capturable=capturable, fused=fused_optimizer or None)
     return TrainingStep(model, optimizer, sample, targets, autocast_dtype)
 
 
