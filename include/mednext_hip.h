@@ -77,6 +77,17 @@ int32_t mednext_depthwise3d_dgrad(const void* grad_output, const void* weight, v
                                   int32_t kernel_size, int32_t dtype, int32_t engine,
                                   int32_t tile_w, int32_t depth_chunk, void* stream);
 
+/* grad_input = the k = 3 input gradient above + accumulate (a bf16 tensor
+ * shaped like grad_input), in one pass: MFMA engine, bf16, k = 3 only. The
+ * MedNeXt block's input receives the depthwise input gradient and the
+ * gradient of its residual; the reference's autograd adds the two
+ * (models/blocks.py:82-91 uses x twice), here the add rides on the
+ * depthwise kernel's store. */
+int32_t mednext_depthwise3d_dgrad_acc(const void* grad_output, const void* weight, const void* accumulate,
+                                      void* grad_input, int64_t n, int64_t c, int64_t d, int64_t h, int64_t w,
+                                      int32_t kernel_size, int32_t dtype, int32_t engine, int32_t tile_w,
+                                      int32_t depth_chunk, void* stream);
+
 /* Bytes of fp32 (fp64 for MEDNEXT_DTYPE_F64) partials the wgrad launch needs
  * (0 if the shape / recipe is unsupported). The MFMA engine additionally needs
  * W % 32 == 0. */

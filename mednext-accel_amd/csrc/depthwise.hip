@@ -1039,6 +1039,25 @@ extern "C" int32_t mednext_depthwise3d_dgrad(const void* grad_output, const void
                              dtype, engine, tile_w, depth_chunk, stream);
 }
 
+extern "C" int32_t mednext_depthwise3d_dgrad_acc(const void* grad_output, const void* weight,
+                                                 const void* accumulate, void* grad_input, int64_t n, int64_t c,
+                                                 int64_t d, int64_t h, int64_t w, int32_t kernel_size,
+                                                 int32_t dtype, int32_t engine, int32_t tile_w,
+                                                 int32_t depth_chunk, void* stream) {
+  MEDNEXT_CHECK_ARG(grad_output != nullptr && weight != nullptr && accumulate != nullptr && grad_input != nullptr,
+                    "null tensor pointer");
+  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_MFMA && dtype == MEDNEXT_DTYPE_BF16 && kernel_size == 3,
+                    "the accumulating input gradient runs the bf16 k = 3 matrix-core kernel");
+  MEDNEXT_CHECK_ARG((reinterpret_cast<uintptr_t>(weight) & 3u) == 0, "weight must be 4-byte aligned");
+  MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && d >= 1 && h < (int64_t(1) << 31) && c < (int64_t(1) << 31) &&
+                        d < (int64_t(1) << 31),
+                    "shape out of range");
+  MEDNEXT_CHECK_ARG(aligned16(grad_output) && aligned16(grad_input) && aligned16(accumulate),
+                    "MFMA engine needs 16-byte aligned tensors");
+  return dw_mfma_stencil(grad_output, weight, nullptr, grad_input, n, c, d, h, w, kernel_size, true, tile_w,
+                         depth_chunk, static_cast<hipStream_t>(stream), accumulate);
+}
+
 extern "C" size_t mednext_depthwise3d_wgrad_workspace_bytes(int64_t n, int64_t c, int64_t d,
                                                             int64_t h, int64_t w,
                                                             int32_t kernel_size, int32_t dtype,

@@ -67,12 +67,17 @@ __device__ inline uint4 lds_read16(const uint16_t* p) { return *reinterpret_cast
 
 // ------------------------------------------------------------------ stencil
 
-template <int K, bool FLIP, bool BIAS, int CT, int PD>
+// ACC (input gradient with k = 3 only): y = stencil + acc, acc a tensor shaped
+// like y (the gradient that reaches the same input through the block's
+// residual), added to the bf16-rounded stencil value in fp32 and rounded
+// again, exactly as a separate bf16 add would.
+template <int K, bool FLIP, bool BIAS, int CT, int PD, bool ACC = false>
 __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t* __restrict__ x,
                                                                    const bf16_t* __restrict__ wt,
                                                                    const bf16_t* __restrict__ bias,
                                                                    bf16_t* __restrict__ y,
-                                                                   MGeom g) {
+                                                                   MGeom g,
+                                                                   const bf16_t* __restrict__ acc_in = nullptr) {
   constexpr int P = K / 2;
   constexpr int K3 = K * K * K;
   constexpr int TH = 16 * kRT, TW = 16 * CT;
@@ -138,6 +143,9 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   // Threads without a chunk write a dummy LDS slot past the two buffers.
   const __amdgpu_buffer_rsrc_t xr = slab_rsrc(xnc, static_cast<uint32_t>(g.D * plane * 2));
   const __amdgpu_buffer_rsrc_t yr = slab_rsrc(ync, static_cast<uint32_t>(g.D * plane * 2));
+  const __amdgpu_buffer_rsrc_t ar =
+      slab_rsrc(ACC ? reinterpret_cast<const uint16_t*>(acc_in) + bp.nc * g.D * plane : ync,
+                ACC ? static_cast<uint32_t>(g.D * plane * 2) : 0u);
   int ch_off[NCH];  // byte offset inside a plane, or -1 outside the plane
   int ch_lds[NCH];  // LDS element offset
 #pragma unroll
@@ -243,7 +251,15 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
               const int r = e / (TW / 8), ch = e - r * (TW / 8);
               const int h = th0 + r, w = tw0 + 8 * ch;
               const uint32_t off = (h < g.H && w < g.W) ? obase + static_cast<uint32_t>(2 * (h * g.W + w)) : kOob;
-              buf_store16(yr, off, *reinterpret_cast<const uint4*>(obuf + r * OC + 8 * ch));
+              uint4 v = *reinterpret_cast<const uint4*>(obuf + r * OC + 8 * ch);
+              if constexpr (ACC) {
+                const uint4 a = buf_load16(ar, off);  // zeros at the out-of-range offset
+                v = make_uint4(pack_bf16x2(bf16_lo(v.x) + bf16_lo(a.x), bf16_hi(v.x) + bf16_hi(a.x)),
+                               pack_bf16x2(bf16_lo(v.y) + bf16_lo(a.y), bf16_hi(v.y) + bf16_hi(a.y)),
+                               pack_bf16x2(bf16_lo(v.z) + bf16_lo(a.z), bf16_hi(v.z) + bf16_hi(a.z)),
+                               pack_bf16x2(bf16_lo(v.w) + bf16_lo(a.w), bf16_hi(v.w) + bf16_hi(a.w)));
+              }
+              buf_store16(yr, off, v);
             }
           }
         }
@@ -537,7 +553,7 @@ int make_geom(int64_t c, int64_t d, int64_t h, int64_t w, int tile_cols, int dep
 
 template <int K, bool FLIP, int CT, int PD>
 int launch_stencil(const void* x, const void* wt, const void* bias, void* y, const MGeom& g,
-                   int64_t blocks, hipStream_t st) {
+                   int64_t blocks, hipStream_t st, const void* acc = nullptr) {
   constexpr int P = K / 2;
   // two plane buffers + one dummy 16-byte slot for threads without a fill chunk
   constexpr size_t stage = stencil_stages_output(K) ? static_cast<size_t>(2) * (16 * kRT) * (16 * CT + 8) : 0;
@@ -547,6 +563,14 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
   auto pb = static_cast<const bf16_t*>(bias);
   auto py = static_cast<bf16_t*>(y);
   const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+  if constexpr (FLIP && stencil_stages_output(K)) {
+    if (acc != nullptr) {
+      hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, false, CT, PD, true>), grid, block, lds, st, px, pw,
+                         pb, py, g, static_cast<const bf16_t*>(acc));
+      MEDNEXT_CHECK_LAUNCH();
+      return MEDNEXT_STATUS_OK;
+    }
+  }
   if (bias)
     hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, true, CT, PD>), grid, block, lds, st, px,
                        pw, pb, py, g);
@@ -559,12 +583,12 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
 
 template <int K, bool FLIP>
 int launch_stencil_ct(const void* x, const void* wt, const void* bias, void* y, const MGeom& g,
-                      int tile_cols, int64_t blocks, hipStream_t st) {
+                      int tile_cols, int64_t blocks, hipStream_t st, const void* acc) {
   constexpr int PD = K == 3 ? 4 : 2;
   switch (tile_cols) {
-    case 32: return launch_stencil<K, FLIP, 2, PD>(x, wt, bias, y, g, blocks, st);
-    case 64: return launch_stencil<K, FLIP, 4, PD>(x, wt, bias, y, g, blocks, st);
-    default: return launch_stencil<K, FLIP, 8, PD>(x, wt, bias, y, g, blocks, st);
+    case 32: return launch_stencil<K, FLIP, 2, PD>(x, wt, bias, y, g, blocks, st, acc);
+    case 64: return launch_stencil<K, FLIP, 4, PD>(x, wt, bias, y, g, blocks, st, acc);
+    default: return launch_stencil<K, FLIP, 8, PD>(x, wt, bias, y, g, blocks, st, acc);
   }
 }
 
@@ -617,7 +641,8 @@ bool dw_mfma_supported(int64_t d, int64_t h, int64_t w, int k) {
 
 int dw_mfma_stencil(const void* x, const void* weight, const void* bias, void* y, int64_t n,
                     int64_t c, int64_t d, int64_t h, int64_t w, int k, bool flip, int tile_cols,
-                    int depth_chunk, hipStream_t st) {
+                    int depth_chunk, hipStream_t st, const void* acc) {
+  MEDNEXT_CHECK_ARG(acc == nullptr || (flip && k == 3), "accumulation is for the k = 3 input gradient");
   MEDNEXT_CHECK_ARG(dw_mfma_supported(d, h, w, k),
                     "MFMA stencil needs k in {3,5}, W % 8 == 0, W >= 32, H >= 32 and a slab < 2 GiB");
   MEDNEXT_CHECK_ARG(tile_cols == 32 || tile_cols == 64 || tile_cols == 128,
@@ -628,11 +653,11 @@ int dw_mfma_stencil(const void* x, const void* weight, const void* bias, void* y
   const int64_t blocks = n * c * g.nDc * g.nHt * g.nWt;
   MEDNEXT_CHECK_ARG(blocks < (int64_t(1) << 31), "grid too large");
   if (k == 3) {
-    return flip ? launch_stencil_ct<3, true>(x, weight, bias, y, g, tile_cols, blocks, st)
-                : launch_stencil_ct<3, false>(x, weight, bias, y, g, tile_cols, blocks, st);
+    return flip ? launch_stencil_ct<3, true>(x, weight, bias, y, g, tile_cols, blocks, st, acc)
+                : launch_stencil_ct<3, false>(x, weight, bias, y, g, tile_cols, blocks, st, nullptr);
   }
-  return flip ? launch_stencil_ct<5, true>(x, weight, bias, y, g, tile_cols, blocks, st)
-              : launch_stencil_ct<5, false>(x, weight, bias, y, g, tile_cols, blocks, st);
+  return flip ? launch_stencil_ct<5, true>(x, weight, bias, y, g, tile_cols, blocks, st, nullptr)
+              : launch_stencil_ct<5, false>(x, weight, bias, y, g, tile_cols, blocks, st, nullptr);
 }
 
 

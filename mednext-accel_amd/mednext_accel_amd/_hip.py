@@ -38,6 +38,10 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
     ),
+    "mednext_depthwise3d_dgrad_acc": (
+        _i32,
+        (_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
+    ),
     "mednext_depthwise3d_wgrad_workspace_bytes": (
         c_size_t,
         (_i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32),
@@ -107,7 +111,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -36,6 +36,7 @@ from torch.nn import functional as F
 from .optimization.descriptors import ExecutionContext, OperatorDescriptor
 from .optimization.policy_resolver import PolicyDecision, PolicyResolver
 from .precast import cast_param, precast_or_param
+from .tiles import ENGINE_MFMA
 
 
 @dataclass(frozen=True, slots=True)
@@ -421,6 +422,43 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
         return hip_ops.depthwise_conv3d_regular(
             x, weight, bias, self.kernel_size[0], recipe(fwd), recipe(dx), recipe(dw), *custom
         )
+
+    def forward_tap(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        """``(self(x), residual)`` for a block that adds x back at its end: the
+        residual is x itself, as a second output of ``DepthwiseResidualTap``
+        when every phase takes the HIP route with the matrix-core k = 3 input
+        gradient on bf16 x (its gradient is then added inside that kernel),
+        x otherwise."""
+        context = _context_from_tensor(x, self.model_context, training=self.training)
+        if (
+            context.phase != "training"
+            or context.device_type != "cuda"
+            or not torch.is_grad_enabled()
+            or x.ndim != 5
+            or x.dtype != torch.bfloat16
+            or not x.is_contiguous()
+            or self.transpose
+            or self.stride != (1, 1, 1)
+            or self.output_padding != (0, 0, 0)
+            or self.kernel_size[0] != 3
+            or getattr(torch, context.dtype) != torch.bfloat16
+        ):
+            return self(x), x
+        fwd, dx, dw = self.phase_decisions(context)
+        if any(d.implementation == "reference" for d in (fwd, dx, dw)):
+            return self(x), x
+
+        def recipe(decision: PolicyDecision) -> list[int]:
+            p = decision.parameters
+            return [int(p.get("engine", 0)), int(p.get("tile_w", 0)), int(p.get("depth_chunk", 0))] if p else []
+
+        hip_ops = _hip_ops()
+        rdx = recipe(dx)
+        if hip_ops._recipe_for(x, 3, rdx or None, "input_grad")[0] != ENGINE_MFMA:
+            return self(x), x
+        weight = cast_param(self.weight, torch.bfloat16)
+        bias = cast_param(self.bias, torch.bfloat16) if self.bias is not None else None
+        return hip_ops.DepthwiseResidualTap.apply(x, weight, bias, 3, recipe(fwd), rdx, recipe(dw))
 
 
 class AdaptiveGroupNorm3d(_AdaptiveModule):

@@ -54,15 +54,25 @@ class MedNeXtV2Block(nn.Module):
         # and the residual add with matrix-core kernels when it applies.
         fused = self.__dict__.get("fused_expansion")
         if fused is not None and fused.applies(x):
-            d = self.depthwise(x)
+            d, res = self._depthwise_and_residual(x)
             if fused.supports(d):
                 h = self.norm(d, out_dtype=torch.bfloat16)
-                residual = x if self.use_residual else None
+                residual = res if self.use_residual else None
                 if self.checkpoint_expansion and self.training and torch.is_grad_enabled():
                     return checkpoint(fused, h, residual, use_reentrant=False, preserve_rng_state=False)
                 return fused(h, residual)
-            return self._finish(self.norm(d), x)
-        return self._finish(self.norm(self.depthwise(x)), x)
+            return self._finish(self.norm(d), res)
+        d, res = self._depthwise_and_residual(x)
+        return self._finish(self.norm(d), res)
+
+    def _depthwise_and_residual(self, x: Tensor) -> tuple[Tensor, Tensor]:
+        """The depthwise output and the tensor the residual add uses (x; from
+        an adaptive depthwise its tap, so the two gradients of x are summed in
+        the depthwise input-gradient kernel)."""
+        tap = getattr(self.depthwise, "forward_tap", None)
+        if self.use_residual and tap is not None:
+            return tap(x)
+        return self.depthwise(x), x
 
     def _finish(self, h: Tensor, x: Tensor) -> Tensor:
         if self.checkpoint_expansion and self.training and torch.is_grad_enabled():

@@ -182,6 +182,65 @@ def depthwise_weight_grad(
     return grad_weight, grad_bias
 
 
+def depthwise_input_grad_acc(grad_output: Tensor, weight: Tensor, accumulate: Tensor, recipe) -> Tensor:
+    """``depthwise_input_grad(grad_output, weight) + accumulate`` in one pass
+    (bf16, k = 3, matrix-core recipe): the add rides on the kernel's store."""
+    k = _check_depthwise(grad_output, weight)
+    if k != 3 or grad_output.dtype != torch.bfloat16:
+        raise ValueError("the accumulating input gradient takes bf16 k = 3")
+    if accumulate.shape != grad_output.shape or accumulate.dtype != torch.bfloat16 or not accumulate.is_contiguous():
+        raise ValueError("accumulate must be a contiguous bf16 tensor shaped like grad_output")
+    engine, tile_w, depth_chunk = _recipe_for(grad_output, k, recipe, "input_grad")
+    if engine != ENGINE_MFMA:
+        raise ValueError("the accumulating input gradient runs the matrix-core engine")
+    n, c, d, h, w = (int(s) for s in grad_output.shape)
+    dx = torch.empty_like(grad_output)
+    _hip.check(
+        _hip.load().mednext_depthwise3d_dgrad_acc(
+            grad_output.data_ptr(), weight.data_ptr(), accumulate.data_ptr(), dx.data_ptr(), n, c, d, h, w, k,
+            _hip.dtype_code(grad_output.dtype), engine, tile_w, depth_chunk, _hip.stream_of(grad_output),
+        ),
+        "mednext_depthwise3d_dgrad_acc",
+    )
+    return dx
+
+
+class DepthwiseResidualTap(torch.autograd.Function):
+    """``(depthwise(x), x)`` for a block whose input also feeds its residual
+    add (reference models/blocks.py:82-91): the residual branch takes the
+    second output, so both gradients of x arrive in this function's backward
+    and are summed by the input-gradient kernel's store
+    (``depthwise_input_grad_acc``) instead of by a separate autograd add.
+    HIP recipes for all three phases (bf16, k = 3, matrix-core input
+    gradient)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, kernel_size, fwd_recipe, dx_recipe, dw_recipe):
+        ctx.save_for_backward(x, weight)
+        ctx.kernel_size, ctx.dx_recipe, ctx.dw_recipe = kernel_size, dx_recipe or None, dw_recipe or None
+        ctx.has_bias = bias is not None
+        return depthwise_forward(x, weight, bias, fwd_recipe or None), x
+
+    @staticmethod
+    def backward(ctx, grad_d, grad_x):
+        x, weight = ctx.saved_tensors
+        need_x, need_w, need_b = ctx.needs_input_grad[:3]
+        dx = dw = db = None
+        if grad_d is None:
+            return grad_x, None, None, None, None, None, None
+        grad_d = grad_d.contiguous()
+        if need_x:
+            if grad_x is not None and grad_x.dtype == grad_d.dtype:
+                dx = depthwise_input_grad_acc(grad_d, weight, grad_x.contiguous(), ctx.dx_recipe)
+            else:
+                dx = depthwise_input_grad(grad_d, weight, ctx.dx_recipe)
+                if grad_x is not None:
+                    dx = dx + grad_x
+        if need_w or (need_b and ctx.has_bias):
+            dw, db = depthwise_weight_grad(x, grad_d, ctx.kernel_size, ctx.dw_recipe)
+        return dx, dw if need_w else None, db if (need_b and ctx.has_bias) else None, None, None, None, None
+
+
 @functools.lru_cache(maxsize=4096)
 def _wgrad_workspace_bytes(*args: int) -> int:
     return int(_hip.load().mednext_depthwise3d_wgrad_workspace_bytes(*args))
