@@ -77,8 +77,8 @@ int32_t mednext_depthwise3d_dgrad(const void* grad_output, const void* weight, v
                                   int32_t kernel_size, int32_t dtype, int32_t engine,
                                   int32_t tile_w, int32_t depth_chunk, void* stream);
 
-/* grad_input = the k = 3 input gradient above + accumulate (a bf16 tensor
- * shaped like grad_input), in one pass: MFMA engine, bf16, k = 3 only. The
+/* grad_input = the input gradient above + accumulate (a bf16 tensor shaped
+ * like grad_input), in one pass: MFMA engine, bf16, k in {3, 5}. The
  * MedNeXt block's input receives the depthwise input gradient and the
  * gradient of its residual; the reference's autograd adds the two
  * (models/blocks.py:82-91 uses x twice), here the add rides on the

@@ -1046,8 +1046,9 @@ extern "C" int32_t mednext_depthwise3d_dgrad_acc(const void* grad_output, const 
                                                  int32_t depth_chunk, void* stream) {
   MEDNEXT_CHECK_ARG(grad_output != nullptr && weight != nullptr && accumulate != nullptr && grad_input != nullptr,
                     "null tensor pointer");
-  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_MFMA && dtype == MEDNEXT_DTYPE_BF16 && kernel_size == 3,
-                    "the accumulating input gradient runs the bf16 k = 3 matrix-core kernel");
+  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_MFMA && dtype == MEDNEXT_DTYPE_BF16 &&
+                        (kernel_size == 3 || kernel_size == 5),
+                    "the accumulating input gradient runs the bf16 k = 3 / 5 matrix-core kernels");
   MEDNEXT_CHECK_ARG((reinterpret_cast<uintptr_t>(weight) & 3u) == 0, "weight must be 4-byte aligned");
   MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && d >= 1 && h < (int64_t(1) << 31) && c < (int64_t(1) << 31) &&
                         d < (int64_t(1) << 31),

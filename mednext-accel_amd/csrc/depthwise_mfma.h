@@ -13,7 +13,7 @@ bool dw_mfma_supported(int64_t d, int64_t h, int64_t w, int k);
 
 // bf16 depthwise stencil on MFMA: forward (flip = false, bias nullable) or
 // input gradient (flip = true, bias = nullptr). tile_cols in {32, 64, 128}.
-// With acc != nullptr (input gradient, k = 3 only): y = stencil + acc.
+// With acc != nullptr (input gradient): y = stencil + acc.
 int dw_mfma_stencil(const void* x, const void* weight, const void* bias, void* y, int64_t n,
                     int64_t c, int64_t d, int64_t h, int64_t w, int k, bool flip, int tile_cols,
                     int depth_chunk, hipStream_t st, const void* acc = nullptr);

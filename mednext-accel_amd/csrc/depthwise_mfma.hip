@@ -67,7 +67,7 @@ __device__ inline uint4 lds_read16(const uint16_t* p) { return *reinterpret_cast
 
 // ------------------------------------------------------------------ stencil
 
-// ACC (input gradient with k = 3 only): y = stencil + acc, acc a tensor shaped
+// ACC (input gradient): y = stencil + acc, acc a tensor shaped
 // like y (the gradient that reaches the same input through the block's
 // residual), added to the bf16-rounded stencil value in fp32 and rounded
 // again, exactly as a separate bf16 add would.
@@ -232,7 +232,12 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
             const int w = tw0 + 16 * tx + 4 * q;
             const bool ok = write_o && h < g.H && w < g.W;
             const uint32_t off = ok ? obase + static_cast<uint32_t>(2 * (h * g.W + w)) : kOob;
-            const u32x2_t words = __builtin_bit_cast(u32x2_t, packed);
+            u32x2_t words = __builtin_bit_cast(u32x2_t, packed);
+            if constexpr (ACC) {
+              const u32x2_t a = buf_load8(ar, off);  // zeros at the out-of-range offset
+              words = u32x2_t{pack_bf16x2(bf16_lo(words[0]) + bf16_lo(a[0]), bf16_hi(words[0]) + bf16_hi(a[0])),
+                              pack_bf16x2(bf16_lo(words[1]) + bf16_lo(a[1]), bf16_hi(words[1]) + bf16_hi(a[1]))};
+            }
             buf_store8(yr, off, words[0], words[1]);
           }
         }
@@ -563,7 +568,7 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
   auto pb = static_cast<const bf16_t*>(bias);
   auto py = static_cast<bf16_t*>(y);
   const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
-  if constexpr (FLIP && stencil_stages_output(K)) {
+  if constexpr (FLIP) {
     if (acc != nullptr) {
       hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, false, CT, PD, true>), grid, block, lds, st, px, pw,
                          pb, py, g, static_cast<const bf16_t*>(acc));
@@ -642,7 +647,7 @@ bool dw_mfma_supported(int64_t d, int64_t h, int64_t w, int k) {
 int dw_mfma_stencil(const void* x, const void* weight, const void* bias, void* y, int64_t n,
                     int64_t c, int64_t d, int64_t h, int64_t w, int k, bool flip, int tile_cols,
                     int depth_chunk, hipStream_t st, const void* acc) {
-  MEDNEXT_CHECK_ARG(acc == nullptr || (flip && k == 3), "accumulation is for the k = 3 input gradient");
+  MEDNEXT_CHECK_ARG(acc == nullptr || flip, "accumulation is for the input gradient");
   MEDNEXT_CHECK_ARG(dw_mfma_supported(d, h, w, k),
                     "MFMA stencil needs k in {3,5}, W % 8 == 0, W >= 32, H >= 32 and a slab < 2 GiB");
   MEDNEXT_CHECK_ARG(tile_cols == 32 || tile_cols == 64 || tile_cols == 128,
@@ -656,7 +661,7 @@ int dw_mfma_stencil(const void* x, const void* weight, const void* bias, void* y
     return flip ? launch_stencil_ct<3, true>(x, weight, bias, y, g, tile_cols, blocks, st, acc)
                 : launch_stencil_ct<3, false>(x, weight, bias, y, g, tile_cols, blocks, st, nullptr);
   }
-  return flip ? launch_stencil_ct<5, true>(x, weight, bias, y, g, tile_cols, blocks, st, nullptr)
+  return flip ? launch_stencil_ct<5, true>(x, weight, bias, y, g, tile_cols, blocks, st, acc)
               : launch_stencil_ct<5, false>(x, weight, bias, y, g, tile_cols, blocks, st, nullptr);
 }
 

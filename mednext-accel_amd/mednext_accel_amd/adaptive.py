@@ -428,7 +428,9 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
         residual is x itself, as a second output of ``DepthwiseResidualTap``
         when every phase takes the HIP route with the matrix-core k = 3 input
         gradient on bf16 x (its gradient is then added inside that kernel),
-        x otherwise."""
+        x otherwise. The k = 5 kernel supports the same accumulation, but on
+        MedNeXt-Large it measured no faster than the separate add (55.96 vs
+        55.63 ms per step, alternating steps), so k = 5 blocks keep the add."""
         context = _context_from_tensor(x, self.model_context, training=self.training)
         if (
             context.phase != "training"
@@ -454,11 +456,12 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
 
         hip_ops = _hip_ops()
         rdx = recipe(dx)
-        if hip_ops._recipe_for(x, 3, rdx or None, "input_grad")[0] != ENGINE_MFMA:
+        k = self.kernel_size[0]
+        if hip_ops._recipe_for(x, k, rdx or None, "input_grad")[0] != ENGINE_MFMA:
             return self(x), x
         weight = cast_param(self.weight, torch.bfloat16)
         bias = cast_param(self.bias, torch.bfloat16) if self.bias is not None else None
-        return hip_ops.DepthwiseResidualTap.apply(x, weight, bias, 3, recipe(fwd), rdx, recipe(dw))
+        return hip_ops.DepthwiseResidualTap.apply(x, weight, bias, k, recipe(fwd), rdx, recipe(dw))
 
 
 class AdaptiveGroupNorm3d(_AdaptiveModule):

@@ -184,10 +184,10 @@ def depthwise_weight_grad(
 
 def depthwise_input_grad_acc(grad_output: Tensor, weight: Tensor, accumulate: Tensor, recipe) -> Tensor:
     """``depthwise_input_grad(grad_output, weight) + accumulate`` in one pass
-    (bf16, k = 3, matrix-core recipe): the add rides on the kernel's store."""
+    (bf16, k in {3, 5}, matrix-core recipe): the add rides on the kernel's store."""
     k = _check_depthwise(grad_output, weight)
-    if k != 3 or grad_output.dtype != torch.bfloat16:
-        raise ValueError("the accumulating input gradient takes bf16 k = 3")
+    if k not in (3, 5) or grad_output.dtype != torch.bfloat16:
+        raise ValueError("the accumulating input gradient takes bf16 k = 3 or 5")
     if accumulate.shape != grad_output.shape or accumulate.dtype != torch.bfloat16 or not accumulate.is_contiguous():
         raise ValueError("accumulate must be a contiguous bf16 tensor shaped like grad_output")
     engine, tile_w, depth_chunk = _recipe_for(grad_output, k, recipe, "input_grad")
@@ -211,7 +211,7 @@ class DepthwiseResidualTap(torch.autograd.Function):
     second output, so both gradients of x arrive in this function's backward
     and are summed by the input-gradient kernel's store
     (``depthwise_input_grad_acc``) instead of by a separate autograd add.
-    HIP recipes for all three phases (bf16, k = 3, matrix-core input
+    HIP recipes for all three phases (bf16, k = 3 or 5, matrix-core input
     gradient)."""
 
     @staticmethod

@@ -238,23 +238,24 @@ def test_launcher_argument_errors():
         hip_ops.depthwise_forward(x, torch.randn(2, 1, 7, 7, 7, device=DEV))  # k=7 unsupported
 
 
+@pytest.mark.parametrize("k", [3, 5])
 @pytest.mark.parametrize("shape,recipe", [((1, 16, 12, 64, 64), [1, 64, 4]), ((2, 8, 9, 33, 96), [1, 32, 3])])
-def test_residual_tap_sums_both_gradients_in_the_kernel(shape, recipe):
+def test_residual_tap_sums_both_gradients_in_the_kernel(shape, recipe, k):
     """DepthwiseResidualTap: (depthwise(x), x) whose backward adds the residual
     branch's gradient inside the matrix-core input-gradient kernel; the result
     is the separate kernel + bf16 add, bit for bit."""
-    print(f"[depthwise residual tap] shape={shape} recipe={recipe}", flush=True)
+    print(f"[depthwise residual tap] shape={shape} recipe={recipe} k={k}", flush=True)
     gen = torch.Generator(device=DEV).manual_seed(21)
     x = torch.randn(shape, generator=gen, device=DEV).bfloat16().requires_grad_()
-    w = (torch.randn(shape[1], 1, 3, 3, 3, generator=gen, device=DEV) / 3).bfloat16().requires_grad_()
+    w = (torch.randn(shape[1], 1, k, k, k, generator=gen, device=DEV) / k).bfloat16().requires_grad_()
     b = torch.randn(shape[1], generator=gen, device=DEV).bfloat16().requires_grad_()
-    d, xr = hip_ops.DepthwiseResidualTap.apply(x, w, b, 3, recipe, recipe, recipe)
+    d, xr = hip_ops.DepthwiseResidualTap.apply(x, w, b, k, recipe, recipe, recipe)
     assert torch.equal(d, hip_ops.depthwise_forward(x.detach(), w.detach(), b.detach(), recipe))
     assert torch.equal(xr, x)
     gd = torch.randn(shape, generator=gen, device=DEV).bfloat16()
     gr = torch.randn(shape, generator=gen, device=DEV).bfloat16()
     dx, dw, db = torch.autograd.grad((d, xr), (x, w, b), (gd, gr))
     want_dx = hip_ops.depthwise_input_grad(gd, w.detach(), recipe) + gr
-    want_dw, want_db = hip_ops.depthwise_weight_grad(x.detach(), gd, 3, recipe)
+    want_dw, want_db = hip_ops.depthwise_weight_grad(x.detach(), gd, k, recipe)
     assert torch.equal(dx, want_dx)
     assert torch.equal(dw, want_dw) and torch.equal(db, want_db)
