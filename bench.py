@@ -472,7 +472,8 @@ def main() -> int:
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU only (got --gpus {args.gpus}): this operator path has no "
-            "multi-GPU mode; see DESIGN.md for how it would shard.",
+            "multi-GPU mode (it would shard by data parallelism: one process per GPU, each running "
+            "these kernels on its own batch share, gradients all-reduced in buckets over RCCL).",
             file=sys.stderr,
         )
         return 2
