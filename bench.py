@@ -32,6 +32,8 @@ ROOT = Path(__file__).resolve().parent
 for _path in (ROOT / "mednext-accel_amd", ROOT):
     if str(_path) not in sys.path:
         sys.path.insert(0, str(_path))
+# A HIP selection must never run PyTorch's operators in its place here.
+os.environ.setdefault("MEDNEXT_ACCEL_AMD_REQUIRE_HIP", "1")
 
 METRIC = "depthwise Conv3d fwd+bwd GB/s (% of HBM peak); MedNeXt-B 128³ train step ms"
 HBM_PEAK_GBS = 8000.0

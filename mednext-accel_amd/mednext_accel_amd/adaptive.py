@@ -20,13 +20,15 @@ Routes:
     float32 like autocast's float32 ``group_norm``.
 
 Unsupported inputs (CPU tensors, evaluation, non-contiguous, ...) take the
-native PyTorch route, as in the reference. A HIP selection on a GPU never falls
-back: if the HIP library is missing the call raises.
+native PyTorch route, as in the reference; so does every HIP selection when
+``libmednext_hip.so`` cannot be loaded (``_hip_ops``), with one warning.
 """
 
 from __future__ import annotations
 
 import functools
+import os
+import warnings
 from dataclasses import dataclass
 
 import torch
@@ -187,9 +189,48 @@ def _gemm_guards(x: Tensor, cin: int, cout: int) -> bool:
     )
 
 
-def _hip_ops():
-    from . import hip_ops  # loads libmednext_hip.so; raises if it is missing
+#: Set to 1 to make a HIP selection raise when libmednext_hip.so cannot be
+#: loaded, instead of running PyTorch's native operator (the test suites and
+#: the benchmark set it, so a result can never come from the fallback).
+REQUIRE_HIP_ENV = "MEDNEXT_ACCEL_AMD_REQUIRE_HIP"
 
+_backend_state: list = []  # [hip_ops module] once loaded, [None] once the load failed
+
+
+def _hip_ops():
+    """The HIP operator module, or None when ``libmednext_hip.so`` cannot be
+    loaded (not built, stale ABI, no HIP runtime).
+
+    None sends the adaptive modules to PyTorch's native operators, as the
+    reference's wrapper does when its kernel backend fails to import (reference
+    ``ops/adaptive.py:273-276``): a model built with ``optimization="auto"``
+    keeps training, on the GPU, without the custom kernels. The first failure
+    is reported once with a ``RuntimeWarning`` naming the cause; with
+    ``MEDNEXT_ACCEL_AMD_REQUIRE_HIP=1`` it raises instead. Direct calls of the
+    ``hip_ops`` launchers and ops always raise on a missing library.
+    """
+    if torch.compiler.is_compiling():
+        from . import hip_ops
+
+        return hip_ops
+    if _backend_state:
+        return _backend_state[0]
+    from . import _hip
+
+    try:
+        _hip.load()
+        from . import hip_ops
+    except (_hip.HipLibraryError, OSError, ImportError) as error:
+        if os.environ.get(REQUIRE_HIP_ENV, "0") not in ("", "0"):
+            raise
+        warnings.warn(
+            f"mednext_accel_amd: the HIP kernels are unavailable ({error}); the adaptive "
+            "modules run PyTorch's native operators",
+            RuntimeWarning,
+            stacklevel=3,
+        )
+        hip_ops = None
+    _backend_state.append(hip_ops)
     return hip_ops
 
 
@@ -298,19 +339,24 @@ class AdaptivePointwise3d(_AdaptiveModule):
         decision = self.resolver.resolve(self.descriptor, context, context.phase)
         if decision.implementation != "hip_pointwise_gemm" or not _gemm_guards(x, self.in_channels, self.out_channels):
             return None
+        ops = _hip_ops()
+        if ops is None:
+            return None
         dt = torch.bfloat16
         bias = cast_param(self.bias, dt) if self.bias is not None else None
-        return _hip_ops().pointwise_conv_transpose3d(x.to(dt), cast_param(self.weight, dt), bias), bias
+        return ops.pointwise_conv_transpose3d(x.to(dt), cast_param(self.weight, dt), bias), bias
 
     def forward(self, x: Tensor) -> Tensor:
         context = _context_from_tensor(x, self.model_context, training=self.training)
         decision = self.resolver.resolve(self.descriptor, context, context.phase)
         strided = self.stride != (1, 1, 1)
+        ops = None
         if decision.implementation == "hip_pointwise_gemm" and _gemm_guards(x, self.in_channels, self.out_channels):
+            ops = _hip_ops()
+        if ops is not None:
             dt = torch.bfloat16
             bias = cast_param(self.bias, dt) if self.bias is not None else None
             weight = cast_param(self.weight, dt)
-            ops = _hip_ops()
             if not strided:
                 op = ops.pointwise_conv_transpose3d if self.transposed else ops.pointwise_conv3d
                 return op(x.to(dt), weight, bias)
@@ -380,6 +426,8 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
         if not any(d.implementation == impl for d in self.phase_decisions(context)):
             return self._reference(x)
         hip_ops = _hip_ops()
+        if hip_ops is None:
+            return self._reference(x)
         dtype = getattr(torch, context.dtype)
         x = x.to(dtype)
         weight = cast_param(self.weight, dtype)
@@ -410,6 +458,8 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
         if not any(custom):
             return self._reference(x)
         hip_ops = _hip_ops()
+        if hip_ops is None:
+            return self._reference(x)
         dtype = getattr(torch, context.dtype)
         x = x.to(dtype)
         weight = cast_param(self.weight, dtype)
@@ -455,6 +505,8 @@ class AdaptiveDepthwise3d(_AdaptiveModule):
             return [int(p.get("engine", 0)), int(p.get("tile_w", 0)), int(p.get("depth_chunk", 0))] if p else []
 
         hip_ops = _hip_ops()
+        if hip_ops is None:
+            return self(x), x
         rdx = recipe(dx)
         k = self.kernel_size[0]
         if hip_ops._recipe_for(x, k, rdx or None, "input_grad")[0] != ENGINE_MFMA:
@@ -502,10 +554,10 @@ class AdaptiveGroupNorm3d(_AdaptiveModule):
             return y if out_dtype is None else y.to(out_dtype)
         context = _context_from_tensor(x, self.model_context, training=self.training)
         decision = self.resolver.resolve(self.descriptor, context, context.phase)
-        if decision.implementation != "hip_group_norm":
+        hip_ops = _hip_ops() if decision.implementation == "hip_group_norm" else None
+        if hip_ops is None:
             y = self._reference(x)
             return y if out_dtype is None else y.to(out_dtype)
-        hip_ops = _hip_ops()
         autocast = torch.is_autocast_enabled(x.device.type) and x.dtype != torch.float64
         # Autocast runs group_norm in float32 (input cast up, float32 result);
         # the kernel reads the low-precision input directly, which is exact.
@@ -558,7 +610,9 @@ class AdaptiveExpansion:
         context = _context_from_tensor(x, self.model_context, training=True)
         if context.dtype != "bfloat16":
             return False
-        return self.resolver.resolve(self.descriptor, context, "training").implementation == "hip_fused_expansion"
+        if self.resolver.resolve(self.descriptor, context, "training").implementation != "hip_fused_expansion":
+            return False
+        return _hip_ops() is not None
 
     def supports(self, h: Tensor) -> bool:
         """Shape check on the expansion's input (the depthwise output: halved

@@ -103,9 +103,10 @@ class AdaptiveGlobalResponseNorm3d(nn.Module):
         # GRN is not an autocast op: the decision keys on the tensor's own dtype.
         context = replace(context, dtype=str(x.dtype).removeprefix("torch."))
         decision = self.resolver.resolve(self.descriptor, context, "training")
-        if decision.implementation != "hip_fused_grn" or not x.is_contiguous():
+        ops = _hip_ops() if decision.implementation == "hip_fused_grn" and x.is_contiguous() else None
+        if ops is None:
             return self._reference(x)
-        return _hip_ops().fused_global_response_norm3d(x, self.gamma, self.beta, self.eps)
+        return ops.fused_global_response_norm3d(x, self.gamma, self.beta, self.eps)
 
     def extra_repr(self) -> str:
         return f"{self.gamma.shape[1]}, eps={self.eps}"
@@ -147,7 +148,9 @@ class AdaptiveGRNExpansion:
         context = _context_from_tensor(x, self.model_context, training=True)
         if context.dtype != "bfloat16":
             return False
-        return self.resolver.resolve(self.descriptor, context, "training").implementation == "hip_fused_grn_expansion"
+        if self.resolver.resolve(self.descriptor, context, "training").implementation != "hip_fused_grn_expansion":
+            return False
+        return _hip_ops() is not None
 
     def supports(self, h: Tensor) -> bool:
         """Shape check on the expansion's input (the depthwise output)."""

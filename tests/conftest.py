@@ -2,6 +2,7 @@
 
 from __future__ import annotations
 
+import os
 import sys
 from pathlib import Path
 
@@ -11,6 +12,11 @@ ROOT = Path(__file__).resolve().parents[1]
 for path in (ROOT / "mednext-accel_amd", ROOT):
     if str(path) not in sys.path:
         sys.path.insert(0, str(path))
+
+
+# A HIP selection whose library cannot be loaded must fail the test, never run
+# PyTorch's operators in its place (the adaptive wrappers' fallback).
+os.environ.setdefault("MEDNEXT_ACCEL_AMD_REQUIRE_HIP", "1")
 
 
 def pytest_configure(config):

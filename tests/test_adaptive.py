@@ -329,3 +329,48 @@ def test_decision_for_shape_without_a_gpu():
     assert [d.parameters[k] for k in ("engine", "tile_w", "depth_chunk")] == tiles.depthwise_recipe(
         2, 64, (64,) * 3, 3, "bfloat16", "weight_grad"
     )
+
+
+def test_missing_library_falls_back_to_native_with_one_warning(monkeypatch):
+    """The reference's wrapper runs the native op when its kernel backend
+    cannot be imported (reference ops/adaptive.py:273-276). Here: a HIP
+    selection on a (simulated) gfx950 device with ``libmednext_hip.so``
+    unloadable runs PyTorch's operators, forward and backward, and warns once;
+    with MEDNEXT_ACCEL_AMD_REQUIRE_HIP=1 the same call raises."""
+    from mednext_accel_amd import _hip, adaptive
+
+    def unloadable():
+        raise _hip.HipLibraryError("libmednext_hip.so is not built")
+
+    gfx950 = lambda x, mc, training: ctx(tuple(x.shape[2:]), dtype="float64", batch=x.shape[0])  # noqa: E731
+    monkeypatch.setattr(_hip, "load", unloadable)
+    monkeypatch.setattr(adaptive, "_context_from_tensor", gfx950)
+    monkeypatch.setattr(adaptive, "_backend_state", [])
+    monkeypatch.delenv(adaptive.REQUIRE_HIP_ENV, raising=False)
+
+    torch.manual_seed(5)
+    ref = nn.Sequential(nn.Conv3d(3, 3, 3, padding=1, groups=3), nn.GroupNorm(3, 3), nn.Conv3d(3, 7, 1)).double()
+    cand = copy.deepcopy(ref)
+    install_adaptive_operators(cand, resolver=PolicyRegistry().resolver(), model_context=MC)
+    decisions = cand[0].phase_decisions(gfx950(torch.empty(2, 3, 4, 5, 6), MC, True))
+    assert all(d.implementation != "reference" for d in decisions), decisions
+    x = torch.randn(2, 3, 4, 5, 6, dtype=torch.double, requires_grad=True)
+    y = x.detach().clone().requires_grad_()
+    with pytest.warns(RuntimeWarning, match="HIP kernels are unavailable"):
+        b = cand(y)
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # reported once only
+        b2 = cand(y)
+    a = ref(x)
+    torch.testing.assert_close(b, a)
+    torch.testing.assert_close(b2, a)
+    g = torch.randn_like(a)
+    for got, want in zip(
+        torch.autograd.grad(b, (y, *cand.parameters()), g), torch.autograd.grad(a, (x, *ref.parameters()), g), strict=True
+    ):
+        torch.testing.assert_close(got, want)
+
+    monkeypatch.setattr(adaptive, "_backend_state", [])
+    monkeypatch.setenv(adaptive.REQUIRE_HIP_ENV, "1")
+    with pytest.raises(_hip.HipLibraryError):
+        cand(y)
