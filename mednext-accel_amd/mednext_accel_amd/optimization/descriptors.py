@@ -1,34 +1,57 @@
-"""Operator identities and execution facts the policy layer resolves against.
+"""What the policy layer resolves against: an operator and an execution context.
 
-Field names and meanings follow the reference's ``OperatorDescriptor`` /
-``ExecutionContext`` (optimization/descriptors.py:22-156) so that policies and
-reports written for it read the same here. One fact is added: ``arch``, the
-GPU's ISA name (``gcnArchName`` without feature suffixes, e.g. ``"gfx950"``),
-which is what the AMD policy layer keys on; ``sm`` keeps the value
+``OperatorDescriptor`` is the shape-independent identity of one wrapped
+module; ``ExecutionContext`` the facts of one call (device, dtype, batch,
+spatial shape, model). Their field names are the reference's
+(``optimization/descriptors.py``), because policy documents and optimization
+reports name them. This build adds ``ExecutionContext.arch``: the GPU's ISA
+name (``gcnArchName`` without feature flags, e.g. ``"gfx950"``), on which the
+AMD policy layers are keyed. ``sm`` keeps what
 ``torch.cuda.get_device_capability`` reports.
+
+Both are frozen and hashable (the resolver memoises on them) and both
+normalise their geometry tuples on construction.
 """
 
 from __future__ import annotations
 
-from dataclasses import asdict, dataclass
+from dataclasses import dataclass, fields
 from math import prod
 from typing import Literal
 
 ExecutionPhase = Literal["training", "inference", "export"]
+_PHASES = ("training", "inference", "export")
+# Geometry fields of a convolution descriptor and the least value each allows.
+_GEOMETRY = (("kernel_size", 1), ("stride", 1), ("padding", 0), ("dilation", 1))
 
 
-def _dims(value, name: str, *, minimum: int = 1) -> tuple[int, ...]:
-    out = tuple(value)
-    if len(out) not in (2, 3) or not all(isinstance(v, int) for v in out):
+def _spatial(value, name: str, least: int) -> tuple[int, ...]:
+    """A 2-D or 3-D integer tuple with every entry >= least."""
+    items = tuple(value)
+    if len(items) not in (2, 3) or any(not isinstance(v, int) for v in items):
         raise ValueError(f"{name} must contain two or three integers")
-    if any(v < minimum for v in out):
-        raise ValueError(f"{name} values must be >= {minimum}")
+    if min(items) < least:
+        raise ValueError(f"{name} values must be >= {least}")
+    return items
+
+
+def _primitive(instance) -> dict[str, object]:
+    """Field values as JSON-ready primitives (tuples become lists)."""
+    out = {}
+    for f in fields(instance):
+        value = getattr(instance, f.name)
+        out[f.name] = list(value) if isinstance(value, tuple) else value
     return out
 
 
 @dataclass(frozen=True, slots=True)
 class OperatorDescriptor:
-    """Shape-independent identity of one optimizable operator (a module instance)."""
+    """One optimizable operator (a module instance), independent of input shape.
+
+    ``family`` (e.g. ``depthwise_conv3d``, ``pointwise_conv3d``,
+    ``group_norm3d``) and ``direction`` (``regular``, ``downsample``,
+    ``transpose``) name the operator; convolutions also carry their geometry,
+    all of it or none; ``role`` is the module's path in the model."""
 
     family: str
     direction: str
@@ -42,22 +65,19 @@ class OperatorDescriptor:
     role: str | None = None
 
     def __post_init__(self) -> None:
-        if not self.family or not self.direction:
+        if not (self.family and self.direction):
             raise ValueError("family and direction must be non-empty")
-        if self.in_channels <= 0 or self.out_channels <= 0:
+        if min(self.in_channels, self.out_channels) <= 0:
             raise ValueError("in_channels and out_channels must be positive")
-        geometry = (self.kernel_size, self.stride, self.padding, self.dilation, self.groups)
-        given = [g is not None for g in geometry]
-        if any(given) and not all(given):
-            raise ValueError("convolution geometry fields must be supplied together")
-        if not any(given):
+        present = [getattr(self, name) is not None for name, _ in _GEOMETRY] + [self.groups is not None]
+        if not any(present):
             return
+        if not all(present):
+            raise ValueError("convolution geometry fields must be supplied together")
         if self.groups <= 0:
             raise ValueError("groups must be positive")
-        object.__setattr__(self, "kernel_size", _dims(self.kernel_size, "kernel_size"))
-        object.__setattr__(self, "stride", _dims(self.stride, "stride"))
-        object.__setattr__(self, "padding", _dims(self.padding, "padding", minimum=0))
-        object.__setattr__(self, "dilation", _dims(self.dilation, "dilation"))
+        for name, least in _GEOMETRY:
+            object.__setattr__(self, name, _spatial(getattr(self, name), name, least))
 
     @classmethod
     def normalization(cls, *, family: str, channels: int, role: str | None = None) -> OperatorDescriptor:
@@ -82,21 +102,19 @@ class OperatorDescriptor:
 
     @property
     def signature(self) -> tuple[object, ...]:
+        """What identifies the operator's kernel, without its role."""
         return (self.family, self.direction, self.in_channels, self.out_channels, self.kernel_size, self.stride)
 
     def to_primitive(self) -> dict[str, object]:
-        data = asdict(self)
-        for key in ("kernel_size", "stride", "padding", "dilation"):
-            if data[key] is not None:
-                data[key] = list(data[key])
-        if self.kernel_size is None:
-            data = {k: v for k, v in data.items() if v is not None}
+        data = _primitive(self)
+        if self.kernel_size is None:  # not a convolution: drop the empty fields
+            data = {key: value for key, value in data.items() if value is not None}
         return data
 
 
 @dataclass(frozen=True, slots=True)
 class ExecutionContext:
-    """Runtime facts one resolution is made for."""
+    """The runtime facts of one call that a policy rule may condition on."""
 
     phase: ExecutionPhase
     device_type: str
@@ -113,27 +131,30 @@ class ExecutionContext:
     arch: str | None = None
 
     def __post_init__(self) -> None:
-        if self.phase not in ("training", "inference", "export"):
-            raise ValueError(f"unknown phase {self.phase!r}")
-        if self.batch_size <= 0:
-            raise ValueError("batch_size must be positive")
-        if self.total_vram_bytes < 0:
-            raise ValueError("total_vram_bytes must be nonnegative")
-        object.__setattr__(self, "spatial_shape", _dims(self.spatial_shape, "spatial_shape"))
+        problems = (
+            (self.phase not in _PHASES, f"unknown phase {self.phase!r}"),
+            (self.batch_size <= 0, "batch_size must be positive"),
+            (self.total_vram_bytes < 0, "total_vram_bytes must be nonnegative"),
+        )
+        for failed, message in problems:
+            if failed:
+                raise ValueError(message)
+        object.__setattr__(self, "spatial_shape", _spatial(self.spatial_shape, "spatial_shape", 1))
         if self.sm is not None:
             sm = tuple(self.sm)
-            if len(sm) != 2 or any(v < 0 for v in sm):
+            if len(sm) != 2 or min(sm) < 0:
                 raise ValueError("sm must contain two nonnegative integers")
             object.__setattr__(self, "sm", sm)
 
     @property
     def vendor(self) -> str | None:
-        """``"amd"`` when an ISA name is known, ``"nvidia"`` for an SM-only context."""
+        """``"amd"`` when the ISA name is known, ``"nvidia"`` for an SM-only GPU
+        context, None off the GPU."""
         if self.device_type != "cuda":
             return None
         if self.arch is not None:
             return "amd"
-        return "nvidia" if self.sm is not None else None
+        return None if self.sm is None else "nvidia"
 
     @property
     def spatial_volume(self) -> int:
@@ -144,7 +165,4 @@ class ExecutionContext:
         return self.total_vram_bytes / 2**30
 
     def to_primitive(self) -> dict[str, object]:
-        data = asdict(self)
-        data["spatial_shape"] = list(self.spatial_shape)
-        data["sm"] = None if self.sm is None else list(self.sm)
-        return data
+        return _primitive(self)

@@ -174,3 +174,36 @@ def test_explain_optimization_on_cpu_is_reference():
     assert report.decisions and all(d.implementation == "reference" for d in report.decisions)
     with pytest.raises(ValueError):
         model.explain_optimization(input_shape=(1, 64, 64, 64), dtype="float32", device="cpu")
+
+
+def test_report_helpers_and_json_form():
+    import json
+
+    model = mednext_small(in_channels=1, out_channels=2, base_channels=4)
+    report = model.explain_optimization(input_shape=(1, 1, 32, 32, 32), dtype=torch.bfloat16, device="cpu")
+    counts = report.implementations()
+    assert counts == {"reference": len(report.decisions)}
+    assert report.custom() == ()
+    data = json.loads(json.dumps(report.to_primitive()))
+    assert data["policies"] == ["reference"] and len(data["decisions"]) == len(report.decisions)
+    assert data["context"]["spatial_shape"] == [32, 32, 32]
+
+
+def test_load_policy_sources(tmp_path):
+    import json
+
+    import yaml
+
+    from mednext_accel_amd.optimization import load_bundled_policy, load_policy, policy_to_primitive
+
+    bundled = load_bundled_policy("gfx950")
+    assert load_policy(bundled) is bundled
+    doc = policy_to_primitive(bundled)
+    (tmp_path / "p.yaml").write_text(yaml.safe_dump(doc))
+    (tmp_path / "p.json").write_text(json.dumps(doc))
+    assert load_policy(tmp_path / "p.yaml") == bundled == load_policy(str(tmp_path / "p.json"))
+    assert load_policy(doc) == bundled
+    with pytest.raises(ValueError, match="suffix"):
+        load_policy(tmp_path / "p.txt")
+    with pytest.raises(ValueError, match="factory mode"):
+        load_policy("auto")
