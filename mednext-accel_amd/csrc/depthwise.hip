@@ -444,9 +444,10 @@ int make_plan(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int 
   const int p = k / 2;
   out->lds_bytes = static_cast<size_t>(kRH * g.THt + 2 * p) * (4 * g.TWt + 8) * acc_bytes;
   MEDNEXT_CHECK_ARG(out->lds_bytes <= 64 * 1024, "tile needs more than 64 KiB of LDS");
-  out->splits = static_cast<int>(n) * g.nDc * g.nHt * g.nWt;
-  out->blocks = n * c * g.nDc * g.nHt * g.nWt;
+  const int64_t splits = n * g.nDc * g.nHt * g.nWt;
+  out->blocks = splits * c;
   MEDNEXT_CHECK_ARG(out->blocks < (int64_t(1) << 31), "grid too large");
+  out->splits = static_cast<int>(splits);
   out->g = g;
   return MEDNEXT_STATUS_OK;
 }
