@@ -18,8 +18,9 @@ the same thing here; the vendor/arch layering is this build's.
 
 Mechanics: the layers for one (vendor, target, phase) are compiled once into
 ``_Candidate`` lists whose rule conditions are predicates over the operator's
-facts; the facts of one (operator, context) are computed on first use; and
-decisions are memoised, because every wrapper resolves on every forward.
+facts, and decisions are memoised, because every wrapper resolves on every
+forward. Under ``torch.compile`` nothing is cached: the resolution is traced
+into the graph once.
 """
 
 from __future__ import annotations
@@ -64,7 +65,7 @@ class PolicyDecision:
 
 
 # Every fact a rule condition may name, read off the operator and the context.
-_FACT_SOURCES: Mapping[str, Callable[[OperatorDescriptor, ExecutionContext], object]] = MappingProxyType(
+_FACT_SOURCES: dict[str, Callable[[OperatorDescriptor, ExecutionContext], object]] = dict(
     {
         "family": lambda d, c: d.family,
         "direction": lambda d, c: d.direction,
@@ -89,22 +90,13 @@ _FACT_SOURCES: Mapping[str, Callable[[OperatorDescriptor, ExecutionContext], obj
 )
 
 
-class _Facts:
-    """Facts of one (operator, context), computed when a condition asks."""
-
-    __slots__ = ("descriptor", "context", "known")
-
-    def __init__(self, descriptor: OperatorDescriptor, context: ExecutionContext) -> None:
-        self.descriptor, self.context, self.known = descriptor, context, {}
-
-    def __getitem__(self, name: str) -> object:
-        if name not in self.known:
-            source = _FACT_SOURCES.get(name)
-            self.known[name] = None if source is None else source(self.descriptor, self.context)
-        return self.known[name]
+def _facts(descriptor: OperatorDescriptor, context: ExecutionContext) -> dict[str, object]:
+    """All facts of one (operator, context), built in one expression (no dict
+    is mutated, so the resolution also traces under ``torch.compile``)."""
+    return {name: source(descriptor, context) for name, source in _FACT_SOURCES.items()}
 
 
-def _predicate(rule: PolicyRule) -> Callable[[_Facts], bool]:
+def _predicate(rule: PolicyRule) -> Callable[[Mapping[str, object]], bool]:
     """The rule's effective condition as one test over the facts; a fact that
     is unknown (None) fails every condition on it."""
     checks = []
@@ -112,9 +104,9 @@ def _predicate(rule: PolicyRule) -> Callable[[_Facts], bool]:
         test = expected.contains if isinstance(expected, NumericRange) else partial(operator.eq, expected)
         checks.append((name, test))
 
-    def matches(facts: _Facts) -> bool:
+    def matches(facts: Mapping[str, object]) -> bool:
         for name, test in checks:
-            value = facts[name]
+            value = facts.get(name)
             if value is None or not test(value):
                 return False
         return True
@@ -127,7 +119,7 @@ class _Candidate:
     policy: OptimizationPolicy
     rule: PolicyRule
     selection: PolicySelection
-    matches: Callable[[_Facts], bool]
+    matches: Callable[[Mapping[str, object]], bool]
 
 
 def _policy_target(policy: OptimizationPolicy) -> object:
@@ -180,7 +172,7 @@ class PolicyResolver:
 
     def _layers_for(self, context: ExecutionContext, phase: str) -> tuple[tuple[_Candidate, ...], ...]:
         key = (context.vendor, _device_target(context), phase)
-        layers = self._compiled.get(key)
+        layers = None if torch.compiler.is_compiling() else self._compiled.get(key)
         if layers is None:
             layers = tuple(
                 tuple(
@@ -190,7 +182,8 @@ class PolicyResolver:
                 )
                 for policy in self.context_layers(context)
             )
-            self._compiled[key] = layers
+            if not torch.compiler.is_compiling():
+                self._compiled[key] = layers
         return layers
 
     # ------------------------------------------------------------ warnings
@@ -237,7 +230,7 @@ class PolicyResolver:
             return self._reference(descriptor, phase, "reference", "context-guard", None,
                                    "requires a GPU with a known architecture")
         warning = self.warn_for_target(context.vendor, _device_target(context))
-        facts = _Facts(descriptor, context)
+        facts = _facts(descriptor, context)
         fallback: PolicyDecision | None = None
         for layer in self._layers_for(context, phase):
             hit = next((c for c in layer if c.matches(facts)), None)

@@ -374,3 +374,22 @@ def test_missing_library_falls_back_to_native_with_one_warning(monkeypatch):
     monkeypatch.setenv(adaptive.REQUIRE_HIP_ENV, "1")
     with pytest.raises(_hip.HipLibraryError):
         cand(y)
+
+
+def test_resolution_traces_under_torch_compile_fullgraph():
+    """The resolver runs inside the adaptive wrappers' forward, which
+    torch.compile(fullgraph=True) traces: a resolution must trace without a
+    graph break (reference tests/ops/test_phase_routing.py:142-158 compiles
+    the wrapped model the same way)."""
+    resolver = PolicyRegistry().resolver()
+    desc = _conv_descriptor(nn.Conv3d(32, 32, 3, padding=1, groups=32), role="encoder_stages.0.0.depthwise")
+    context = ctx((128,) * 3)
+
+    def pick(x):
+        d = resolver.resolve(desc, context, "backward_weight")
+        return x + 1 if d.implementation == "hip_split_dw" else x - 1
+
+    torch._dynamo.reset()
+    compiled = torch.compile(pick, fullgraph=True, backend="eager")
+    x = torch.zeros(3)
+    assert torch.equal(compiled(x), pick(x)) and torch.equal(pick(x), x + 1)
