@@ -118,6 +118,9 @@ def precast_parameters(model: nn.Module) -> list[nn.Parameter]:
 
 def _precast_before(module: nn.Module, args) -> None:
     global _ACTIVE
+    # Copies of an earlier forward that did not return (an exception skips the
+    # post hook's normal path) must never serve this one.
+    _ACTIVE = None
     params = module.__dict__.get("_mednext_precast_params")
     dtype = module.__dict__.get("_mednext_precast_dtype")
     if not params:
@@ -153,7 +156,7 @@ def install_weight_precast(model: nn.Module, dtype: torch.dtype = torch.bfloat16
     model.__dict__["_mednext_precast_dtype"] = dtype
     if first:
         model.register_forward_pre_hook(_precast_before)
-        model.register_forward_hook(_precast_after)
+        model.register_forward_hook(_precast_after, always_call=True)
     return len(params)
 
 

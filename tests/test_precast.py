@@ -63,3 +63,29 @@ def test_copies_start_on_16_byte_boundaries():
     sum(o.float().sum() for o in outs).backward()
     for p in params:
         assert torch.equal(p.grad, torch.ones_like(p))
+
+
+def test_failed_forward_leaves_no_stale_copies():
+    """A forward that raises (e.g. a caught out-of-memory error) must not leave
+    its bf16 copies active: the next forward (here an evaluation pass without
+    autocast) reads the fp32 parameters."""
+    from mednext_accel_amd import precast
+
+    cfg = replace(get_mednext_v1_config("base", in_channels=1, out_channels=2, kernel_size=3, deep_supervision=False),
+                  base_channels=4, block_counts=(1,) * 9)
+    torch.manual_seed(0)
+    model = configure_optimization(MedNeXtV1(cfg), "auto").train()
+    reference = copy.deepcopy(model)
+    boom = model.stem.register_forward_hook(lambda *a: (_ for _ in ()).throw(RuntimeError("boom")))
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        try:
+            model(torch.randn(1, 1, 32, 32, 32))
+        except RuntimeError as error:
+            assert "boom" in str(error)
+    boom.remove()
+    assert precast._ACTIVE is None
+    model.eval()
+    reference.eval()
+    x = torch.randn(1, 1, 32, 32, 32)
+    with torch.no_grad():
+        assert torch.equal(model(x), reference(x))
