@@ -108,6 +108,25 @@ int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_output, void* 
                                   int32_t kernel_size, int32_t dtype, int32_t engine,
                                   int32_t tile_w, int32_t depth_chunk, void* stream);
 
+/* Allocation-free variant of mednext_depthwise3d_wgrad (same kernels, same
+ * results bit for bit). No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). The fp32 / fp64 partials
+ * live in a library-owned device array of
+ * mednext_depthwise3d_wgrad_noalloc_max_bytes() bytes (16 MiB) per GPU, held
+ * from the first call on that GPU until the process ends; shapes whose
+ * partials need more (see mednext_depthwise3d_wgrad_workspace_bytes) are
+ * rejected with MEDNEXT_STATUS_INVALID_ARGUMENT. The call allocates nothing.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other host threads) race and must be serialised by the
+ * caller. `stream` must belong to the current device. */
+size_t mednext_depthwise3d_wgrad_noalloc_max_bytes(void);
+
+int32_t mednext_depthwise3d_wgrad_noalloc(const void* x, const void* grad_output, void* grad_weight,
+                                          void* grad_bias, int64_t n, int64_t c, int64_t d, int64_t h,
+                                          int64_t w, int32_t kernel_size, int32_t dtype, int32_t engine,
+                                          int32_t tile_w, int32_t depth_chunk, void* stream);
+
 /* ---------------------------------------------------------------- group norm
  * GroupNorm with groups == channels on [N, C, V] (V = spatial volume), biased
  * variance, rstd = 1/sqrt(var + eps). Replaces the reference's

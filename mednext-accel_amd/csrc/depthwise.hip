@@ -18,6 +18,7 @@
 #include "depthwise_mfma.h"
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 namespace mednext {
@@ -1132,6 +1133,79 @@ extern "C" int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_out
       return launch_wgrad<bf16_t>(x, grad_output, grad_weight, grad_bias, workspace, pl,
                                   kernel_size, vec, s);
   }
+}
+
+// ------------------------------------------- allocation-free weight gradient
+//
+// mednext_depthwise3d_wgrad_noalloc keeps the fp32 / fp64 partials in this
+// library-owned device array instead of a caller workspace. Each GPU holds its
+// own copy (at its own address) from the first call on it until the process
+// ends; its contents carry over between calls, and every launch overwrites all
+// the partial slots it reads, so nothing needs clearing.
+constexpr size_t kWgradScratchBytes = size_t(16) << 20;
+static __device__ __align__(256) unsigned char scratch[kWgradScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per
+// device (the host-side name is only a stand-in for the symbol).
+int32_t scratch_on_current_device(void* stream, void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) {
+    mednext::set_error(std::string("hipGetDevice failed: ") + hipGetErrorString(err));
+    return MEDNEXT_STATUS_LAUNCH_ERROR;
+  }
+  if (stream != nullptr) {
+    hipDevice_t sdev = -1;
+    err = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (err != hipSuccess) {
+      mednext::set_error(std::string("hipStreamGetDevice failed: ") + hipGetErrorString(err));
+      return MEDNEXT_STATUS_LAUNCH_ERROR;
+    }
+    MEDNEXT_CHECK_ARG(sdev == dev, "the stream belongs to device " + std::to_string(sdev) +
+                                       " but device " + std::to_string(dev) + " is current");
+  }
+  MEDNEXT_CHECK_ARG(dev >= 0 && dev < kMaxScratchDevices, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      mednext::set_error(std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(err));
+      return MEDNEXT_STATUS_LAUNCH_ERROR;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MEDNEXT_STATUS_OK;
+}
+}  // namespace
+
+extern "C" size_t mednext_depthwise3d_wgrad_noalloc_max_bytes(void) { return kWgradScratchBytes; }
+
+extern "C" int32_t mednext_depthwise3d_wgrad_noalloc(const void* x, const void* grad_output, void* grad_weight,
+                                                     void* grad_bias, int64_t n, int64_t c, int64_t d, int64_t h,
+                                                     int64_t w, int32_t kernel_size, int32_t dtype, int32_t engine,
+                                                     int32_t tile_w, int32_t depth_chunk, void* stream) {
+  const size_t need = mednext_depthwise3d_wgrad_workspace_bytes(n, c, d, h, w, kernel_size, dtype, engine, tile_w,
+                                                                depth_chunk);
+  if (need == 0) {
+    // Unsupported shape or recipe: the allocating entry point names the reason.
+    return mednext_depthwise3d_wgrad(x, grad_output, grad_weight, grad_bias, nullptr, 0, n, c, d, h, w, kernel_size,
+                                     dtype, engine, tile_w, depth_chunk, stream);
+  }
+  MEDNEXT_CHECK_ARG(need <= kWgradScratchBytes,
+                    "this shape needs " + std::to_string(need) + " bytes of partials, more than the " +
+                        std::to_string(kWgradScratchBytes) + "-byte scratch array of the allocation-free entry point");
+  void* ptr = nullptr;
+  const int32_t st = scratch_on_current_device(stream, &ptr);
+  if (st != MEDNEXT_STATUS_OK) return st;
+  return mednext_depthwise3d_wgrad(x, grad_output, grad_weight, grad_bias, ptr, kWgradScratchBytes, n, c, d, h, w,
+                                   kernel_size, dtype, engine, tile_w, depth_chunk, stream);
 }
 
 extern "C" int32_t mednext_depthwise3d_s2_gather(const void* big, const void* weight, const void* bias,

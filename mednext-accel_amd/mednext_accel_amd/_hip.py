@@ -50,6 +50,11 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
     ),
+    "mednext_depthwise3d_wgrad_noalloc_max_bytes": (c_size_t, ()),
+    "mednext_depthwise3d_wgrad_noalloc": (
+        _i32,
+        (_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _p),
+    ),
     "mednext_group_norm_workspace_bytes": (c_size_t, (_i64, _i64, _i64, _i32)),
     "mednext_group_norm_fwd": (
         _i32,
@@ -111,7 +116,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
