@@ -49,6 +49,7 @@ def parse_args() -> argparse.Namespace:
     ap.add_argument("--size", type=int, default=128)
     ap.add_argument("--kernel-size", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-block", action="store_true", help="skip the configs[2] block timing")
     ap.add_argument("--no-train-step", action="store_true", help="skip the MedNeXt-Base training-step timing")
     ap.add_argument("--train-steps", type=int, default=50)
     ap.add_argument("--train-warmup", type=int, default=20)
@@ -74,6 +75,7 @@ def parse_args() -> argparse.Namespace:
         help="instead of the headline line, print one JSON line per kernel phase of the configs[1] stage sweep "
         "(depthwise k3/k5 fwd, dX, dW; stride-2 maps; GroupNorm; pointwise GEMMs) and exit",
     )
+    ap.add_argument("--sweep-reps", type=int, default=40, help="timed launches per op in --sweep")
     ap.add_argument(
         "--copy-calibration",
         action="store_true",
@@ -168,6 +170,96 @@ def time_depthwise(args, torch, hip_ops, lead: GpuLead):
     }
 
 
+def time_cfg0_gpu(args, torch, hip_ops, lead: GpuLead) -> dict:
+    """configs[0] on the GPU: fp32 1x32x64^3 k3 forward + input grad + weight
+    grad (+ bias grad) through the HIP kernels, the like-for-like counterpart of
+    ``cpu_baseline`` (same shape, dtype and 24*E byte count). Inputs rotate over
+    six resident sets (402 MB > 256 MB Infinity Cache)."""
+    dev = torch.device("cuda:0")
+    c, s, k = 32, 64, 3
+    gen = torch.Generator(device=dev).manual_seed(1)
+    w = (torch.rand(c, 1, k, k, k, generator=gen, device=dev) * 2 - 1) / (k**3) ** 0.5
+    b = torch.zeros(c, device=dev)
+    sets = [(torch.randn(1, c, s, s, s, generator=gen, device=dev), torch.randn(1, c, s, s, s, generator=gen, device=dev))
+            for _ in range(6)]
+    phases = {
+        "forward": lambda i: hip_ops.depthwise_forward(sets[i % 6][0], w, b),
+        "input_grad": lambda i: hip_ops.depthwise_input_grad(sets[i % 6][1], w),
+        "weight_grad": lambda i: hip_ops.depthwise_weight_grad(sets[i % 6][0], sets[i % 6][1], k),
+    }
+    us = {name: _timed_launches(torch, lead, fn, 6, max(10, args.steps)) for name, fn in phases.items()}
+    elements = c * s**3
+    total_us = sum(us.values())
+    return {
+        "value": round(3 * 2 * elements * 4 / (total_us * 1e-6) / 1e9, 1),
+        "unit": "GB/s",
+        "phase_us": {k_: round(v, 2) for k_, v in us.items()},
+        "sample": f"HIP kernels (VALU engine, fp32) on cfg0 fp32 1x{c}x{s}^3 k{k}, fwd + dX + dW(+dB), "
+                  "mean per launch over back-to-back launches; 24*E algorithmic bytes as cpu_baseline",
+    }
+
+
+def block_reference_op_bytes(channels: int, size: int, ratio: int) -> int:
+    """Algorithmic HBM bytes of one MedNeXt block's forward as the reference
+    runs it, one operator at a time under bf16 autocast (E = C * S^3 elements,
+    hidden R*E): depthwise 4E (bf16 read + write), GroupNorm 6E (bf16 read,
+    fp32 write), expand 2E + 2RE, GELU 4RE, project 2RE + 2E, residual add
+    6E. Forward + backward counts the forward three times (backward ~ 2x)."""
+    e = channels * size**3
+    forward = 4 * e + 6 * e + (2 * e + 2 * ratio * e) + 4 * ratio * e + (2 * ratio * e + 2 * e) + 6 * e
+    return 3 * forward
+
+
+def time_block(args, torch, channels: int, size: int, ratio: int, reps: int = 20) -> dict:
+    """one MedNeXt block (dw k3 -> GroupNorm -> expand -> GELU ->
+    project -> + residual), bf16 autocast, forward + backward, this package's
+    block vs the same block as plain PyTorch modules, on the same GPU."""
+    import copy
+
+    from mednext_accel_amd import MedNeXtBlock
+    from mednext_accel_amd.adaptive import ModelOptimizationContext, install_adaptive_operators
+    from mednext_accel_amd.optimization import PolicyRegistry
+
+    torch.manual_seed(11)
+    ref = MedNeXtBlock(spatial_dims=3, in_channels=channels, out_channels=channels, expansion_ratio=ratio,
+                       kernel_size=3).cuda().train()
+    hip = copy.deepcopy(ref)
+    install_adaptive_operators(hip, resolver=PolicyRegistry().resolver(),
+                               model_context=ModelOptimizationContext("mednext_v1", "base", "none"))
+    xs = [torch.randn(1, channels, size, size, size, device="cuda", requires_grad=True) for _ in range(3)]
+    g = torch.randn(1, channels, size, size, size, device="cuda").bfloat16()
+    out = {}
+    for name, block in (("hip", hip), ("reference_eager", ref)):
+        def step(i, block=block):
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                y = block(xs[i % 3])
+            y.backward(g)
+
+        for i in range(3):
+            step(i)
+        torch.cuda.synchronize()
+        times = []
+        for i in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            step(i)
+            end.record()
+            torch.cuda.synchronize()
+            times.append(start.elapsed_time(end))
+        out[name] = round(1000.0 * statistics.median(times), 1)
+    nbytes = block_reference_op_bytes(channels, size, ratio)
+    return {
+        "block": f"C={channels} {size}^3 R={ratio} k3",
+        "hip_us": out["hip"],
+        "reference_eager_us": out["reference_eager"],
+        "speedup": round(out["reference_eager"] / out["hip"], 2),
+        "reference_op_bytes": nbytes,
+        "hip_gbs_at_reference_op_bytes": round(nbytes / (out["hip"] * 1e-6) / 1e9, 1),
+        "note": "fwd + bwd, event median of single synchronised steps (host launch time included); "
+                "reference_op_bytes = the reference's per-operator HBM traffic (forward x3)",
+    }
+
+
 # Kernel-name prefixes (rocprofv3 short names) launched by each phase at k=3 bf16.
 PHASE_KERNELS = {
     "forward": ("dw_mfma_stencil_kernel<3, false",),
@@ -250,6 +342,7 @@ def time_train_step(args, torch, optimization: str, variant: str = "base", steps
         "mean_wall_step_ms": round(1000.0 * wall / max(1, steps), 3),
         "peak_allocated_mib": round(torch.cuda.max_memory_allocated() / 2**20, 1),
         "final_loss": round(float(step.last_loss.detach()), 5),
+        "steps_run": warmup + steps,
     }
     if graph:
         result["captured"] = "hip_graph"
@@ -322,7 +415,11 @@ ROTATE_BYTES = 768 << 20  # rotate inputs over > 3x the 256 MiB Infinity Cache
 
 def _timed_launches(torch, lead: GpuLead, launch, sets: int, reps: int) -> float:
     """Mean microseconds per launch of ``launch(i)`` over ``reps`` launches
-    bracketed by two events, inputs rotated over ``sets`` resident copies."""
+    bracketed by two events, inputs rotated over ``sets`` resident copies.
+    The warm-up launches and the timed launches each follow a GPU spin
+    kernel, so a kernel trace splits into (warm-up, timed) segments per op in
+    sweep order (what the rocprofv3 counter summaries attribute by)."""
+    lead(0.01)
     for i in range(min(reps, 3)):
         launch(i % sets)
     torch.cuda.synchronize()
@@ -350,7 +447,7 @@ def sweep(args, torch, hip_ops, lead: GpuLead) -> None:
     host), algorithmic bytes, GB/s and, for the GEMMs, TFLOP/s."""
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev).manual_seed(1234)
-    reps = 40
+    reps = args.sweep_reps
 
     def randn(*shape):
         return torch.randn(shape, generator=gen, device=dev).bfloat16()
@@ -363,6 +460,15 @@ def sweep(args, torch, hip_ops, lead: GpuLead) -> None:
             rec.update(tflops=round(tf, 2), mfma_frac=round(tf / MFMA_BF16_PEAK_TFLOPS, 4))
         rec.update(extra)
         _emit(rec)
+
+    # A plain copy of known size first: the counter summaries scale rocprofv3's
+    # FETCH_SIZE / WRITE_SIZE by what they read for it.
+    src = randn(2**27)
+    dsts = [torch.empty_like(src) for _ in range(2)]
+    us = _timed_launches(torch, lead, lambda i: torch.neg(src, out=dsts[i]), 2, reps)
+    record("copy_calibration", "2^27 bf16 (torch.neg)", us, 2 * src.numel() * 2)
+    del src, dsts
+    torch.cuda.empty_cache()
 
     for (c, s), ratio in zip(STAGE_SHAPES, V2_RATIOS):
         # GRN of a MedNeXt v2 expansion (C * ratio channels) at this stage, bf16
@@ -580,8 +686,10 @@ def main() -> int:
             big = time_train_step(args, torch, "auto", "large", args.large_steps, args.large_warmup)
             big_graph = None if args.no_graph_step else time_train_step(
                 args, torch, "auto", "large", args.large_steps, args.large_warmup, graph=True)
+            # Same warm-up and timed step counts as the HIP legs, so the final
+            # losses are taken after the same number of AdamW steps.
             big_eager = None if args.no_eager_step else time_train_step(
-                args, torch, "reference", "large", max(3, args.large_steps // 2), 2)
+                args, torch, "reference", "large", args.large_steps, args.large_warmup)
             result["train_step_large"] = {
                 "model": (
                     f"MedNeXt-Large k5, 1x1x{args.train_size}^3, 5-head deep supervision, expansion-branch "
@@ -600,7 +708,7 @@ def main() -> int:
         v2_graph = None if args.no_graph_step else time_train_step(
             args, torch, "auto", "v2", args.v2_steps, args.v2_warmup, graph=True)
         v2_eager = None if args.no_eager_step else time_train_step(
-            args, torch, "reference", "v2", max(3, args.v2_steps // 2), 2)
+            args, torch, "reference", "v2", args.v2_steps, args.v2_warmup)
         result["train_step_v2"] = {
             "model": (
                 f"MedNeXt v2 Base (GRN), 1x1x{args.train_size}^3, 5-head deep supervision, no checkpointing, "
@@ -614,6 +722,9 @@ def main() -> int:
             "graph_speedup_vs_reference_eager": round(v2_eager["median_step_ms"] / v2_graph["median_step_ms"], 3)
             if v2_eager and v2_graph else None,
         }
+    if not args.no_block:
+        result["block_cfg2"] = [time_block(args, torch, 32, 128, 2), time_block(args, torch, 128, 32, 4)]
+    result["cfg0_gpu_fp32"] = time_cfg0_gpu(args, torch, hip_ops, lead)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(args, torch)
     print(json.dumps(result))

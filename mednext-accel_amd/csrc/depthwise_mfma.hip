@@ -190,7 +190,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   load_plane(0, pre[0]);
   store_plane(lds, pre[0]);
 #pragma unroll
-  for (int j = 1; j <= PD; ++j) load_plane(j, pre[(j - 1) % PD]);
+  for (int j = 1; j < PD; ++j) load_plane(j, pre[(j - 1) % PD]);
   __syncthreads();
 
   for (int q0 = 0; q0 < nplanes; q0 += U) {
@@ -454,7 +454,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
     store(0, first);
   }
 #pragma unroll
-  for (int j = 1; j <= PD; ++j) load(j, pre[(j - 1) % PD]);
+  for (int j = 1; j < PD; ++j) load(j, pre[(j - 1) % PD]);
   __syncthreads();
 
   for (int s0 = 0; s0 < nsteps; s0 += PD) {
