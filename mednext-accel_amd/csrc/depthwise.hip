@@ -16,6 +16,7 @@
 #include "cdna4.h"
 #include "common.h"
 #include "depthwise_mfma.h"
+#include "depthwise_volume.h"
 
 #include <algorithm>
 #include <mutex>
@@ -509,9 +510,12 @@ int stencil_entry(const void* x, const void* weight, const void* bias, void* y, 
   MEDNEXT_CHECK_ARG(dtype_ok(dtype), "unsupported dtype");
   MEDNEXT_CHECK_ARG((reinterpret_cast<uintptr_t>(weight) & 3u) == 0,
                     "weight must be 4-byte aligned");
-  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_VALU || engine == MEDNEXT_ENGINE_MFMA,
-                    "engine must be MEDNEXT_ENGINE_VALU or MEDNEXT_ENGINE_MFMA");
+  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_VALU || engine == MEDNEXT_ENGINE_MFMA || engine == MEDNEXT_ENGINE_VOLUME,
+                    "engine must be MEDNEXT_ENGINE_VALU, MEDNEXT_ENGINE_MFMA or MEDNEXT_ENGINE_VOLUME");
   auto s = static_cast<hipStream_t>(stream);
+  if (engine == MEDNEXT_ENGINE_VOLUME) {
+    return dw_volume_stencil(x, weight, bias, y, n, c, d, h, w, k, dtype, FLIP, tile_w, depth_chunk, s);
+  }
   if (engine == MEDNEXT_ENGINE_MFMA) {
     MEDNEXT_CHECK_ARG(dtype == MEDNEXT_DTYPE_BF16, "the MFMA engine is bf16 only");
     MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && d >= 1 && h < (int64_t(1) << 31) &&
@@ -1074,6 +1078,11 @@ extern "C" size_t mednext_depthwise3d_wgrad_workspace_bytes(int64_t n, int64_t c
     if (splits <= 0) return 0;
     return static_cast<size_t>(c * splits * (k3 + 1) * 4);
   }
+  if (engine == MEDNEXT_ENGINE_VOLUME) {
+    const int splits = dw_volume_wgrad_splits(n, c, d, h, w, kernel_size, dtype, tile_w, depth_chunk);
+    if (splits <= 0) return 0;
+    return static_cast<size_t>(c * splits * (k3 + 1) * acc_bytes_of(dtype));
+  }
   if (engine != MEDNEXT_ENGINE_VALU) return 0;
   Plan pl;
   if (make_plan(n, c, d, h, w, kernel_size, acc_bytes_of(dtype), tile_w, depth_chunk, &pl) !=
@@ -1091,10 +1100,35 @@ extern "C" int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_out
   MEDNEXT_CHECK_ARG(x != nullptr && grad_output != nullptr && grad_weight != nullptr,
                     "null tensor pointer");
   MEDNEXT_CHECK_ARG(dtype_ok(dtype), "unsupported dtype");
-  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_VALU || engine == MEDNEXT_ENGINE_MFMA,
-                    "engine must be MEDNEXT_ENGINE_VALU or MEDNEXT_ENGINE_MFMA");
+  MEDNEXT_CHECK_ARG(engine == MEDNEXT_ENGINE_VALU || engine == MEDNEXT_ENGINE_MFMA || engine == MEDNEXT_ENGINE_VOLUME,
+                    "engine must be MEDNEXT_ENGINE_VALU, MEDNEXT_ENGINE_MFMA or MEDNEXT_ENGINE_VOLUME");
   const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
   auto s = static_cast<hipStream_t>(stream);
+  if (engine == MEDNEXT_ENGINE_VOLUME) {
+    const int splits = dw_volume_wgrad_splits(n, c, d, h, w, kernel_size, dtype, tile_w, depth_chunk);
+    if (splits <= 0) {
+      // The planner names the reason.
+      return dw_volume_wgrad(x, grad_output, nullptr, n, c, d, h, w, kernel_size, dtype, tile_w, depth_chunk, s);
+    }
+    const size_t need = static_cast<size_t>(c * splits * (k3 + 1) * acc_bytes_of(dtype));
+    MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
+    int st = dw_volume_wgrad(x, grad_output, workspace, n, c, d, h, w, kernel_size, dtype, tile_w, depth_chunk, s);
+    if (st != MEDNEXT_STATUS_OK) return st;
+    switch (dtype) {
+      case MEDNEXT_DTYPE_F32:
+        return launch_finish<float, float>(static_cast<const float*>(workspace), grad_weight, grad_bias, c, splits,
+                                           static_cast<int>(k3), s);
+      case MEDNEXT_DTYPE_F64:
+        return launch_finish<double, double>(static_cast<const double*>(workspace), grad_weight, grad_bias, c, splits,
+                                             static_cast<int>(k3), s);
+      case MEDNEXT_DTYPE_F16:
+        return launch_finish<f16_t, float>(static_cast<const float*>(workspace), grad_weight, grad_bias, c, splits,
+                                           static_cast<int>(k3), s);
+      default:
+        return launch_finish<bf16_t, float>(static_cast<const float*>(workspace), grad_weight, grad_bias, c, splits,
+                                            static_cast<int>(k3), s);
+    }
+  }
   if (engine == MEDNEXT_ENGINE_MFMA) {
     MEDNEXT_CHECK_ARG(dtype == MEDNEXT_DTYPE_BF16, "the MFMA engine is bf16 only");
     MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && d >= 1 && c < (int64_t(1) << 31) &&

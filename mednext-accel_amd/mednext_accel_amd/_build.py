@@ -24,7 +24,10 @@ LIB_NAME = "libmednext_hip.so"
 LIB_PATH = LIB_DIR / LIB_NAME
 
 ARCH = "gfx950"
-SOURCES = ("capi.hip", "depthwise.hip", "depthwise_mfma.hip", "groupnorm.hip", "grn.hip", "pointwise.hip", "upjoin.hip")
+SOURCES = (
+    "capi.hip", "depthwise.hip", "depthwise_mfma.hip", "depthwise_volume.hip", "groupnorm.hip", "grn.hip",
+    "pointwise.hip", "upjoin.hip",
+)
 
 # Packed FP32 VALU instructions are disabled for all device code: some of
 # their forms have produced silent wrong results on the target machines.

@@ -27,6 +27,8 @@ from . import _hip
 from .tiles import (
     ENGINE_MFMA,
     ENGINE_VALU,
+    ENGINE_VOLUME,
+    VOLUME_SEG,
     depthwise_recipe,
     group_norm_splits,
     pointwise_blocks,
@@ -61,8 +63,11 @@ def _checked_recipe(recipe: tuple[int, int, int]) -> tuple[int, int, int]:
     elif engine == ENGINE_MFMA:
         if tile_w not in (32, 64, 128):
             raise ValueError("MFMA tile_w must be 32, 64 or 128")
+    elif engine == ENGINE_VOLUME:
+        if tile_w != VOLUME_SEG:
+            raise ValueError(f"volume-engine tile_w must be {VOLUME_SEG}")
     else:
-        raise ValueError("engine must be 0 (VALU) or 1 (MFMA)")
+        raise ValueError("engine must be 0 (VALU), 1 (MFMA) or 2 (VOLUME)")
     if depth_chunk < 1:
         raise ValueError("depth_chunk must be >= 1")
     return engine, tile_w, depth_chunk

@@ -8,7 +8,8 @@ are this package's gfx950 recipes (``tiles.py``).
 
 Recipe fields:
   hip_depthwise_fwd / hip_depthwise_dx / hip_split_dw:
-      engine (0 = VALU stencil, 1 = bf16 matrix cores), tile_w, depth_chunk
+      engine (0 = VALU stencil, 1 = bf16 matrix cores, 2 = small-plane volume
+      kernels), tile_w, depth_chunk
   hip_group_norm: splits (chunks per (n, c) row)
 """
 
@@ -82,11 +83,13 @@ def validate_parameters(implementation: str, parameters: Mapping[str, object]) -
             raise ValueError(f"parameters.splits must be <= {tiles.MAX_GN_SPLITS}")
         return
     engine = parameters.get("engine", tiles.ENGINE_VALU)
-    if engine not in (tiles.ENGINE_VALU, tiles.ENGINE_MFMA) or type(engine) is not int:
-        raise ValueError("parameters.engine must be 0 (VALU) or 1 (MFMA)")
+    if engine not in (tiles.ENGINE_VALU, tiles.ENGINE_MFMA, tiles.ENGINE_VOLUME) or type(engine) is not int:
+        raise ValueError("parameters.engine must be 0 (VALU), 1 (MFMA) or 2 (VOLUME)")
     if "tile_w" in parameters:
         tile_w = _positive_int("tile_w", parameters["tile_w"])
-        widths = (32, 64, 128) if engine == tiles.ENGINE_MFMA else tiles.TILE_WIDTHS
+        widths = {tiles.ENGINE_MFMA: (32, 64, 128), tiles.ENGINE_VOLUME: (tiles.VOLUME_SEG,)}.get(
+            engine, tiles.TILE_WIDTHS
+        )
         if tile_w not in widths:
             raise ValueError(f"parameters.tile_w must be one of {widths} for engine {engine}")
     if "depth_chunk" in parameters and _positive_int("depth_chunk", parameters["depth_chunk"]) > MAX_DEPTH_CHUNK:
@@ -134,6 +137,16 @@ def resolve_parameters(
 
 
 def _check_engine_fits(implementation, params, descriptor, context) -> None:
+    if params["engine"] == tiles.ENGINE_VOLUME:
+        spatial = tuple(context.spatial_shape)
+        if not tiles.volume_supported(spatial):
+            raise ValueError("engine 2 (VOLUME) needs planes of at most 256 elements")
+        plan = tiles.volume_plan(context.batch_size, descriptor.in_channels, spatial, descriptor.kernel_size[0],
+                                 params["depth_chunk"], acc_bytes=8 if context.dtype == "float64" else 4,
+                                 wgrad=implementation == "hip_split_dw")
+        if plan.lds_bytes > tiles.LDS_LIMIT:
+            raise ValueError("engine 2 (VOLUME): depth_chunk too long for the LDS limit")
+        return
     if params["engine"] != tiles.ENGINE_MFMA:
         return
     phase = _DEPTHWISE_PHASE[implementation]

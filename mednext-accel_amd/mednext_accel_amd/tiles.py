@@ -86,6 +86,7 @@ def depthwise_plan(
 
 ENGINE_VALU = 0
 ENGINE_MFMA = 1
+ENGINE_VOLUME = 2
 MFMA_TILE_ROWS = 32  # two 16-row MFMA tiles per workgroup
 PHASES = ("forward", "input_grad", "weight_grad")
 
@@ -135,6 +136,76 @@ def mfma_wgrad_rows(kernel_size: int, tile_w: int) -> int:
     return (16 - (kernel_size - 1)) * (4 // (tile_w // 32))
 
 
+# ----------------------------------------------------------- small planes
+
+VOLUME_SEG = 4  # output planes per lane of the volume kernels (their tile_w)
+VOLUME_MAX_PLANE = MAX_THREADS  # H * W the volume kernels take
+VOLUME_TARGET_WORKGROUPS = 2 * CU_COUNT
+# Phases whose default recipe is the volume engine on small planes (the weight
+# gradient keeps the VALU stencil until its volume kernel is faster there).
+VOLUME_PHASES = ("forward", "input_grad")
+LDS_LIMIT = 64 * 1024  # per-workgroup LDS the kernels request at most
+
+
+def volume_supported(spatial: tuple[int, int, int]) -> bool:
+    """Planes the volume kernels take (mirrors dw_volume_supported)."""
+    _d, h, w = spatial
+    return 1 <= h * w <= VOLUME_MAX_PLANE
+
+
+@dataclass(frozen=True, slots=True)
+class VolumePlan:
+    """Launch shape of the volume kernels (mirrors volume_plan in depthwise_volume.hip)."""
+
+    slabs_per_workgroup: int
+    depth_chunk: int
+    chunks_d: int
+    workgroups: int
+    lds_bytes: int
+
+
+def volume_lds_bytes(cpw: int, depth_chunk: int, spatial, kernel_size: int, acc_bytes: int, wgrad: bool) -> int:
+    _d, h, w = spatial
+    p = kernel_size // 2
+    tdp = _cdiv(depth_chunk, VOLUME_SEG) * VOLUME_SEG
+    staged = cpw * (tdp + 2 * p) * (h + 2 * p) * (w + 2 * p)
+    if not wgrad:
+        return (staged + cpw * (kernel_size**3 + 1)) * acc_bytes
+    taps = 8 if acc_bytes == 8 else 16  # lane values reduced per LDS round
+    red = taps * MAX_THREADS + taps * (MAX_THREADS // 16)
+    return (staged + cpw * tdp * h * w + red) * acc_bytes
+
+
+def volume_plan(batch: int, channels: int, spatial, kernel_size: int, depth_chunk: int, *, acc_bytes: int = 4,
+                wgrad: bool = False) -> VolumePlan:
+    d, h, w = spatial
+    td = min(depth_chunk, d)
+    slabs = batch * channels
+    cpw = max(1, min(MAX_THREADS // (h * w), slabs))
+    while cpw > 1 and volume_lds_bytes(cpw, td, spatial, kernel_size, acc_bytes, wgrad) > LDS_LIMIT:
+        cpw -= 1
+    chunks = _cdiv(d, td)
+    return VolumePlan(cpw, td, chunks, _cdiv(slabs, cpw) * chunks,
+                      volume_lds_bytes(cpw, td, spatial, kernel_size, acc_bytes, wgrad))
+
+
+def volume_depth_chunk(batch: int, channels: int, spatial, kernel_size: int, acc_bytes: int) -> int:
+    """The longest D-run (a multiple of VOLUME_SEG, or D) whose grid still has
+    VOLUME_TARGET_WORKGROUPS workgroups and whose staged planes (weight
+    gradient, the larger footprint) fit the LDS limit."""
+    d = spatial[0]
+    td = d
+
+    def fits(td: int) -> bool:
+        return volume_plan(batch, channels, spatial, kernel_size, td, acc_bytes=acc_bytes, wgrad=True).lds_bytes <= LDS_LIMIT
+
+    while td > VOLUME_SEG and (
+        volume_plan(batch, channels, spatial, kernel_size, td).workgroups < VOLUME_TARGET_WORKGROUPS or not fits(td)
+    ):
+        td = max(VOLUME_SEG, _cdiv(td // 2, VOLUME_SEG) * VOLUME_SEG)
+    return td
+
+
 @functools.lru_cache(maxsize=4096)
 def depthwise_recipe(
     batch: int,
@@ -150,6 +221,9 @@ def depthwise_recipe(
     W)`` columns per workgroup: forward / input-grad tiles are 32 rows high,
     weight-grad tiles ``mfma_wgrad_rows(k, tile_w)``. The D-run per workgroup is
     the longest that still yields ``MFMA_TARGET_WORKGROUPS``.
+    Small planes (H * W <= 256: the 16^3 and 8^3 stages) run the volume
+    kernels, which stage whole planes in LDS, with ``tile_w = VOLUME_SEG`` and
+    the D-run of ``volume_depth_chunk``, in the phases of ``VOLUME_PHASES``.
     Everything else runs the VALU stencil with the widest tile the plane allows
     (up to 64 columns) and a D-run that yields TARGET_WORKGROUPS workgroups. In
     both cases at least k - 1 planes per workgroup (``depth_chunk_floor``).
@@ -168,6 +242,9 @@ def depthwise_recipe(
         slabs = batch * channels * _cdiv(h, rows) * _cdiv(w, tile_w)
         target = MFMA_TARGET_WORKGROUPS[(kind, kernel_size)]
         return [ENGINE_MFMA, tile_w, _depth_chunk(d, slabs, kernel_size, target)]
+    if volume_supported(spatial) and phase in VOLUME_PHASES:
+        acc_bytes = 8 if dtype == "float64" else 4
+        return [ENGINE_VOLUME, VOLUME_SEG, volume_depth_chunk(batch, channels, spatial, kernel_size, acc_bytes)]
     tile_w = 4
     while tile_w < 64 and tile_w < w:
         tile_w *= 2

@@ -289,7 +289,8 @@ def test_policy_schema_rejects_malformed_documents(mutate, message):
 def test_depthwise_parameter_validation():
     base = {"version": 2, "kind": "mednext-accel-policy", "name": "p", "target": {"vendor": "amd"}}
     for params, message in (
-        ({"engine": 2}, "engine"),
+        ({"engine": 3}, "engine"),
+        ({"engine": 2, "tile_w": 8}, "tile_w"),
         ({"engine": 1, "tile_w": 16}, "tile_w"),
         ({"engine": 0, "tile_w": 128}, "tile_w"),
         ({"depth_chunk": 0}, "positive"),

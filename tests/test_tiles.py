@@ -24,6 +24,15 @@ def test_depthwise_recipe_invariants(channels, size, k, dtype, phase):
         wgs = channels * -(-size // rows) * -(-size // tile_w) * -(-size // depth_chunk)
         kind = "weight_grad" if phase == "weight_grad" else "stencil"
         target = tiles.MFMA_TARGET_WORKGROUPS[(kind, k)]
+    elif engine == tiles.ENGINE_VOLUME:
+        assert tiles.volume_supported((size,) * 3) and tile_w == tiles.VOLUME_SEG
+        acc = 8 if dtype == "float64" else 4
+        plan = tiles.volume_plan(1, channels, (size,) * 3, k, depth_chunk, acc_bytes=acc, wgrad=phase == "weight_grad")
+        assert plan.lds_bytes <= tiles.LDS_LIMIT
+        wgs = plan.workgroups
+        # Fill the chip unless the shortest D-run (one lane's planes) forbids it.
+        assert wgs >= tiles.VOLUME_TARGET_WORKGROUPS or depth_chunk == tiles.VOLUME_SEG
+        return
     else:
         plan = tiles.depthwise_plan(1, channels, (size,) * 3, k, tile_w, depth_chunk)
         assert plan.lds_bytes <= 64 * 1024
@@ -62,3 +71,22 @@ def test_mfma_stage0_recipes_match_measured_best():
     assert r(1, 64, (64,) * 3, 3, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 64, 16]
     assert r(1, 32, (128,) * 3, 5, "bfloat16", "forward") == [tiles.ENGINE_MFMA, 128, 64]
     assert r(1, 64, (64,) * 3, 3, "bfloat16", "input_grad") == [tiles.ENGINE_MFMA, 64, 16]
+
+
+def test_small_planes_use_the_volume_engine():
+    """16^3 and 8^3 (H * W <= 256) take the volume kernels in every dtype in
+    the volume phases; the staged planes fit the LDS limit even in fp64."""
+    for channels, size in ((256, 16), (512, 8)):
+        for k in (3, 5):
+            for dtype in ("bfloat16", "float32", "float64"):
+                for phase in tiles.PHASES:
+                    engine, tile_w, depth_chunk = tiles.depthwise_recipe(1, channels, (size,) * 3, k, dtype, phase)
+                    if phase not in tiles.VOLUME_PHASES:
+                        assert engine == tiles.ENGINE_VALU
+                        continue
+                    assert (engine, tile_w) == (tiles.ENGINE_VOLUME, tiles.VOLUME_SEG)
+                    acc = 8 if dtype == "float64" else 4
+                    for wgrad in (False, True):
+                        plan = tiles.volume_plan(1, channels, (size,) * 3, k, depth_chunk, acc_bytes=acc, wgrad=wgrad)
+                        assert plan.lds_bytes <= tiles.LDS_LIMIT
+    assert not tiles.volume_supported((32, 32, 32)) and tiles.volume_supported((4, 16, 16))
