@@ -37,9 +37,11 @@ enum mednext_status {
  * W >= 32, H >= 32, one (n, c) slab < 2 GiB; weight-grad also W % 32 == 0);
  * tile_w is then the columns per workgroup (32, 64 or 128).
  * VOLUME: small planes (H * W <= 256, e.g. the 16^3 and 8^3 MedNeXt stages),
- * every dtype: whole zero-padded planes of one or more (n, c) slabs staged in
- * LDS; tile_w must be 4 (output planes per lane) and depth_chunk is the D-run
- * of one workgroup (its staged planes must fit 64 KiB of LDS). */
+ * every dtype: one workgroup of k waves (one per kernel row) per (n, c) slab,
+ * band of 64 consecutive plane positions and D-run, its zero-padded input rows
+ * staged in LDS; tile_w must be 64 (plane positions per workgroup) and
+ * depth_chunk is the D-run of one workgroup (its staged planes must fit
+ * 64 KiB of LDS). */
 enum mednext_engine { MEDNEXT_ENGINE_VALU = 0, MEDNEXT_ENGINE_MFMA = 1, MEDNEXT_ENGINE_VOLUME = 2 };
 
 enum mednext_dtype {

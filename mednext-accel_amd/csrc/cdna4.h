@@ -16,6 +16,8 @@
 
 #include <cstdint>
 
+#include "common.h"
+
 namespace mednext {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -30,6 +32,53 @@ __device__ inline __amdgpu_buffer_rsrc_t slab_rsrc(const void* base, uint32_t by
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), bytes,
                                            0x00020000);
 }
+// One element through a raw buffer resource; `ok == false` reads the
+// out-of-range offset, which returns zero. Keeping every load unconditional
+// lets a task issue all of its loads back to back.
+template <typename T>
+struct BufIo;
+template <>
+struct BufIo<float> {
+  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  }
+  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+  }
+};
+template <>
+struct BufIo<double> {
+  __device__ static double ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+  }
+  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, double v) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, off, 0, 0);
+  }
+};
+template <>
+struct BufIo<f16_t> {
+  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return static_cast<float>(__builtin_bit_cast(f16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
+  }
+  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<f16_t>(v)), r, off, 0, 0);
+  }
+};
+template <>
+struct BufIo<bf16_t> {
+  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+  }
+  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), r, off, 0, 0);
+  }
+};
+
+template <typename T>
+__device__ inline uint32_t boff(bool ok, int elem) {
+  return ok ? static_cast<uint32_t>(elem) * static_cast<uint32_t>(sizeof(T)) : kOob;
+}
+
 __device__ inline uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
   return make_uint4(v[0], v[1], v[2], v[3]);

@@ -395,10 +395,40 @@ __global__ __launch_bounds__(256) void dw_wgrad_finish_kernel(const Acc* __restr
   }
 }
 
+// The same sums for few partials per tap: one thread per (channel, tap), the
+// partials added in index order in fp64.
+template <typename T, typename Acc>
+__global__ __launch_bounds__(256) void dw_wgrad_finish_few_kernel(const Acc* __restrict__ partial,
+                                                                  T* __restrict__ dw, T* __restrict__ db,
+                                                                  int channels, int splits, int k3) {
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (item >= static_cast<int64_t>(channels) * (k3 + 1)) return;
+  const Acc* p = partial + item * splits;
+  double s = 0.0;
+  for (int j = 0; j < splits; ++j) s += static_cast<double>(p[j]);
+  const int64_t c = item / (k3 + 1);
+  const int t = static_cast<int>(item - c * (k3 + 1));
+  if (t < k3) {
+    dw[c * k3 + t] = Cvt<T, Acc>::store(static_cast<Acc>(s));
+  } else if (db != nullptr) {
+    db[c] = Cvt<T, Acc>::store(static_cast<Acc>(s));
+  }
+}
+
+// Partials per tap up to which one thread sums a tap (above it, a wave per tap).
+constexpr int kFinishFewSplits = 16;
+
 template <typename T, typename Acc>
 int launch_finish(const Acc* part, void* dw, void* db, int64_t c, int splits, int k3,
                   hipStream_t st) {
   const int64_t items = c * (k3 + 1);
+  if (splits <= kFinishFewSplits) {
+    hipLaunchKernelGGL((dw_wgrad_finish_few_kernel<T, Acc>), dim3(static_cast<unsigned>(cdiv(items, 256))),
+                       dim3(256), 0, st, part, static_cast<T*>(dw), static_cast<T*>(db), static_cast<int>(c),
+                       splits, k3);
+    MEDNEXT_CHECK_LAUNCH();
+    return MEDNEXT_STATUS_OK;
+  }
   hipLaunchKernelGGL((dw_wgrad_finish_kernel<T, Acc>), dim3(static_cast<unsigned>(cdiv(items, 4))),
                      dim3(256), 0, st, part, static_cast<T*>(dw), static_cast<T*>(db),
                      static_cast<int>(c), splits, k3);
@@ -650,53 +680,6 @@ __device__ inline void load_taps(const T* __restrict__ w, int c, Acc (&wv)[K * K
   const T* wc = w + static_cast<int64_t>(c) * K * K * K;
 #pragma unroll
   for (int t = 0; t < K * K * K; ++t) wv[t] = Cvt<T, Acc>::load(wc[t]);
-}
-
-// One element through a raw buffer resource; `ok == false` reads the
-// out-of-range offset, which returns zero. Keeping every load unconditional
-// lets a task issue all of its loads back to back.
-template <typename T>
-struct BufIo;
-template <>
-struct BufIo<float> {
-  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
-  }
-  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
-  }
-};
-template <>
-struct BufIo<double> {
-  __device__ static double ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
-  }
-  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, double v) {
-    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2_t, v), r, off, 0, 0);
-  }
-};
-template <>
-struct BufIo<f16_t> {
-  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return static_cast<float>(__builtin_bit_cast(f16_t, __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0)));
-  }
-  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
-    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, static_cast<f16_t>(v)), r, off, 0, 0);
-  }
-};
-template <>
-struct BufIo<bf16_t> {
-  __device__ static float ld(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
-  }
-  __device__ static void st(__amdgpu_buffer_rsrc_t r, uint32_t off, float v) {
-    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), r, off, 0, 0);
-  }
-};
-
-template <typename T>
-__device__ inline uint32_t boff(bool ok, int elem) {
-  return ok ? static_cast<uint32_t>(elem) * static_cast<uint32_t>(sizeof(T)) : kOob;
 }
 
 template <typename T>

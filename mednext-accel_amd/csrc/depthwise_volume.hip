@@ -3,26 +3,37 @@
 // dtype; fp32 accumulation (fp64 for fp64).
 //
 // At these sizes the tiled kernels leave most lanes idle (a 16 x 16 plane is
-// one or two 4-column tiles) and run long serial per-thread chains, so they
-// are latency-bound at 30-60 us for 1-4 MB of data. Here one workgroup holds
-// whole planes: the zero-padded block of input planes a D-chunk needs, for one
-// or several (n, c) slabs (`cpw` of them), is staged in LDS (converted to the
-// accumulation type), and the lanes map to consecutive (h, w) positions of a
-// plane, so every LDS read of a wave touches consecutive addresses and every
-// store is one contiguous run of the output.
+// one or two column tiles) and run long serial per-thread chains, so they are
+// latency-bound at 30-60 us for 1-4 MB of data. Here the work is cut so that
+// every lane runs a short chain of useful FMAs:
 //
-// Forward / input gradient: a lane owns one (h, w) position and kSeg
-// consecutive output planes; per (kh, kw) it reads the kSeg + k - 1 input
-// values of its column once and applies all k taps along D to them.
+// A workgroup owns one (n, c) slab, one band of kBand = 64 consecutive plane
+// positions (row-major (h, w): a 16 x 16 plane has four bands of four rows,
+// an 8 x 8 plane one) and one D-run of TD output planes. It has k waves:
+// wave kh takes kernel row kh, lane l the band's position l. The zero-padded
+// input rows the band needs (its rows plus P above and below, W + 2P columns)
+// of the TD + 2P planes the D-run reaches are staged once in LDS, converted
+// to the accumulation type.
 //
-// Weight gradient: a lane owns one (h, w) position of one slab and walks its
-// column of input planes once; each plane's k * k values meet the k most
-// recent grad_output values (a register ring), so all k^3 taps and the bias
-// sum accumulate in registers in one pass. The lane sums are reduced per
-// slab in a fixed order through LDS (segments of 16 lanes, then segments in
-// order) into the same [C][k^3 + 1][splits] partial layout as the other
-// weight-gradient kernels, and the shared fixed-order finish kernel sums the
-// splits (one per (n, D-chunk)).
+// Each lane walks the staged planes front to back. Per input plane it reads
+// the k values of its kernel row (x[pd][h + kh][w .. w + k - 1]) and applies
+// them to every tap along D, k * k FMAs:
+//   forward / input gradient: into a register ring of the k output planes the
+//     input plane reaches, with this kernel row's k * k weights in registers.
+//     An output plane leaves the ring complete for the row and goes to LDS;
+//     the k rows' sums (+ bias) are then added in a fixed order and stored,
+//     one contiguous 64-position run per plane;
+//   weight gradient: against a register ring of the k most recent
+//     grad_output values (staged in LDS with the input), into the row's k * k
+//     tap sums and the bias sum. The lane sums are reduced per wave in a
+//     fixed order through LDS (16-lane segments, then the four segments) into
+//     the same [C][k^3 + 1][splits] partial layout as the other
+//     weight-gradient kernels; the shared fixed-order finish kernel sums the
+//     splits (one per (n, band, D-run)).
+// The first and last k - 1 planes of the walk are unrolled with only the taps
+// whose output (forward) or grad_output (weight gradient) plane exists in the
+// D-run, so no FMA is spent on the zero padding along D.
+#include "cdna4.h"
 #include "common.h"
 #include "depthwise_volume.h"
 
@@ -31,411 +42,630 @@
 namespace mednext {
 namespace {
 
-constexpr int kVolThreads = 256;
-constexpr int kSeg = 4;  // output planes per lane (forward / input gradient)
+constexpr int kBand = 64;  // plane positions per workgroup: one wave's lanes
+constexpr int kFillBatch = 8;  // loads in flight per thread while staging
 
-struct VolGeom {
+struct BandGeom {
   int C, D, H, W;
-  int TD;      // output planes per workgroup (D-chunk)
-  int TDp;     // TD rounded up to a multiple of kSeg
-  int nDc;     // D-chunks per slab
-  int cpw;     // slabs per workgroup
+  int TD;        // output planes per D-run
+  int TDk;       // planes the lanes walk: max(TD, k - 1); planes past the D-run are zero / not stored
+  int nDc;       // D-runs per slab
+  int nbands;    // bands per plane
+  int SR;        // staged rows per band: the most rows a band spans + 2P
+  uint32_t wp_magic;     // ceil(2^31 / (W + 2P))
+  uint32_t plane_magic;  // ceil(2^31 / (SR * (W + 2P)))
+  uint32_t w4_magic;     // ceil(2^31 / (W / 4)) (W % 4 == 0 only)
+  uint32_t sr_magic;     // ceil(2^31 / SR)
   int64_t slabs;
 };
+
+// n / d for n * d < 2^31 with magic = ceil(2^31 / d): n * magic / 2^31 exceeds
+// n / d by less than n / 2^31 < 1 / d, which never reaches the next integer.
+__device__ inline int div_magic(int n, uint32_t magic) {
+  return static_cast<int>(__umulhi(static_cast<uint32_t>(n) << 1, magic));
+}
 
 template <typename T, typename Acc>
 __device__ inline Acc load_acc(const T* p, int64_t i) {
   return Cvt<T, Acc>::load(p[i]);
 }
 
-// Stage the zero-padded input planes [d0 - P, d0 + TDp + P) of `cpw` slabs
-// starting at slab0 into lds[s][pd][ph][pw] (pitches (H + 2P) x (W + 2P)).
-// A lane owns padded plane positions (consecutive lanes: consecutive
-// positions, so the loads of a wave are contiguous runs of a row) and loads
-// kFillBatch planes of one position before storing any of them, so a
-// workgroup waits for a few memory round trips instead of one per element.
-constexpr int kFillBatch = 8;
+// Stage rows [hb0 - P, hb0 - P + SR) x columns [-P, W + P) of the planes
+// [d0 - P, d0 + TDk + P) of one slab into lds[pd][row][col], zero outside the
+// tensor. Consecutive threads take consecutive columns of a row. Loads go
+// through a raw buffer resource over the slab, out-of-tensor elements read the
+// out-of-range offset (zero), so each thread issues kFillBatch loads back to
+// back with no branches before its first store.
+template <typename T, typename Acc, int P>
+__device__ inline void fill_band(Acc* __restrict__ lds, const T* __restrict__ x, const BandGeom& g, int64_t slab,
+                                 int d0, int hb0, int nthreads) {
+  const int Wp = g.W + 2 * P;
+  const int per_plane = g.SR * Wp;
+  const int total = (g.TDk + 2 * P) * per_plane;
+  const int plane = g.H * g.W;
+  const __amdgpu_buffer_rsrc_t src =
+      slab_rsrc(x + slab * g.D * plane, static_cast<uint32_t>(g.D * plane * static_cast<int>(sizeof(T))));
+  for (int base = 0; base < total; base += nthreads * kFillBatch) {
+    Acc v[kFillBatch];
+#pragma unroll
+    for (int b = 0; b < kFillBatch; ++b) {
+      v[b] = Acc(0);
+      if (base + b * nthreads >= total) break;  // uniform: no load for slots past the staged block
+      const int e = base + b * nthreads + static_cast<int>(threadIdx.x);
+      const int pd = div_magic(e, g.plane_magic);
+      const int r = e - pd * per_plane;
+      const int sr = div_magic(r, g.wp_magic);
+      const int gw = r - sr * Wp - P;
+      const int gh = hb0 + sr - P;
+      const int gd = d0 + pd - P;
+      const bool ok = e < total && gd >= 0 && gd < g.D && gh >= 0 && gh < g.H && gw >= 0 && gw < g.W;
+      v[b] = BufIo<T>::ld(src, boff<T>(ok, gd * plane + gh * g.W + gw));
+    }
+#pragma unroll
+    for (int b = 0; b < kFillBatch; ++b) {
+      const int e = base + b * nthreads + static_cast<int>(threadIdx.x);
+      if (e < total) lds[e] = v[b];
+    }
+  }
+}
+
+// Four consecutive elements through a raw buffer resource (one 8-byte load
+// for 16-bit types), converted to the accumulation type; the out-of-range
+// offset reads zeros.
+template <typename T>
+struct BufIo4;
+template <>
+struct BufIo4<bf16_t> {
+  __device__ static void ld(__amdgpu_buffer_rsrc_t r, uint32_t off, float (&v)[4]) {
+    const u32x2_t q = buf_load8(r, off);
+    v[0] = bf16_to_f32(static_cast<uint16_t>(q[0]));
+    v[1] = bf16_to_f32(static_cast<uint16_t>(q[0] >> 16));
+    v[2] = bf16_to_f32(static_cast<uint16_t>(q[1]));
+    v[3] = bf16_to_f32(static_cast<uint16_t>(q[1] >> 16));
+  }
+};
+template <>
+struct BufIo4<f16_t> {
+  __device__ static void ld(__amdgpu_buffer_rsrc_t r, uint32_t off, float (&v)[4]) {
+    const u32x2_t q = buf_load8(r, off);
+    v[0] = static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>(q[0])));
+    v[1] = static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>(q[0] >> 16)));
+    v[2] = static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>(q[1])));
+    v[3] = static_cast<float>(__builtin_bit_cast(f16_t, static_cast<uint16_t>(q[1] >> 16)));
+  }
+};
+template <>
+struct BufIo4<float> {
+  __device__ static void ld(__amdgpu_buffer_rsrc_t r, uint32_t off, float (&v)[4]) {
+    const uint4 q = buf_load16(r, off);
+    v[0] = __uint_as_float(q.x);
+    v[1] = __uint_as_float(q.y);
+    v[2] = __uint_as_float(q.z);
+    v[3] = __uint_as_float(q.w);
+  }
+};
+template <>
+struct BufIo4<double> {
+  __device__ static void ld(__amdgpu_buffer_rsrc_t r, uint32_t off, double (&v)[4]) {
+    const uint4 a = buf_load16(r, off);
+    const uint4 b = buf_load16(r, off == kOob ? kOob : off + 16);
+    v[0] = __hiloint2double(a.y, a.x);
+    v[1] = __hiloint2double(a.w, a.z);
+    v[2] = __hiloint2double(b.y, b.x);
+    v[3] = __hiloint2double(b.w, b.z);
+  }
+};
+
+// fill_band for W % 4 == 0: the interior of each staged row is loaded in
+// 4-column chunks (a quarter of the load instructions and index arithmetic),
+// and the 2P padding columns of every row are written as zeros.
+constexpr int kChunkBatch = 4;
 
 template <typename T, typename Acc, int P>
-__device__ inline void fill_volume(Acc* __restrict__ lds, const T* __restrict__ src, const VolGeom& g,
-                                   int64_t slab0, int d0) {
-  const int Hp = g.H + 2 * P, Wp = g.W + 2 * P, planes = g.TDp + 2 * P, hwp = Hp * Wp;
-  const int64_t plane = static_cast<int64_t>(g.H) * g.W;
-  for (int e2 = threadIdx.x; e2 < hwp; e2 += kVolThreads) {
-    const int ph = e2 / Wp, pw = e2 - ph * Wp;
-    const int gh = ph - P, gw = pw - P;
-    const bool in_plane = gh >= 0 && gh < g.H && gw >= 0 && gw < g.W;
-    for (int s = 0; s < g.cpw; ++s) {
-      const int64_t slab = slab0 + s;
-      const bool ok = in_plane && slab < g.slabs;
-      const int64_t base = ok ? (slab * g.D) * plane + static_cast<int64_t>(gh) * g.W + gw : 0;
-      Acc* __restrict__ out = lds + static_cast<int64_t>(s) * planes * hwp + e2;
-      for (int pd0 = 0; pd0 < planes; pd0 += kFillBatch) {
-        Acc v[kFillBatch];
+__device__ inline void fill_band_w4(Acc* __restrict__ lds, const T* __restrict__ x, const BandGeom& g, int64_t slab,
+                                    int d0, int hb0, int nthreads) {
+  const int Wp = g.W + 2 * P, W4 = g.W >> 2;
+  const int rows = (g.TDk + 2 * P) * g.SR;
+  const int total = rows * W4;
+  const int plane = g.H * g.W;
+  const __amdgpu_buffer_rsrc_t src =
+      slab_rsrc(x + slab * g.D * plane, static_cast<uint32_t>(g.D * plane * static_cast<int>(sizeof(T))));
+  for (int base = 0; base < total; base += nthreads * kChunkBatch) {
+    Acc v[kChunkBatch][4];
+    int dst[kChunkBatch];  // LDS element offset of the chunk, -1: nothing to store
 #pragma unroll
-        for (int b = 0; b < kFillBatch; ++b) {
-          const int gd = d0 - P + pd0 + b;
-          v[b] = (ok && pd0 + b < planes && gd >= 0 && gd < g.D) ? load_acc<T, Acc>(src, base + gd * plane) : Acc(0);
-        }
+    for (int b = 0; b < kChunkBatch; ++b) dst[b] = -1;
 #pragma unroll
-        for (int b = 0; b < kFillBatch; ++b) {
-          if (pd0 + b < planes) out[(pd0 + b) * hwp] = v[b];
-        }
+    for (int b = 0; b < kChunkBatch; ++b) {
+      if (base + b * nthreads >= total) break;  // uniform
+      const int e = base + b * nthreads + static_cast<int>(threadIdx.x);
+      const int row = div_magic(e, g.w4_magic);
+      const int cx = e - row * W4;
+      const int pd = div_magic(row, g.sr_magic);
+      const int sr = row - pd * g.SR;
+      const int gh = hb0 + sr - P;
+      const int gd = d0 + pd - P;
+      const bool ok = e < total && gd >= 0 && gd < g.D && gh >= 0 && gh < g.H;
+      BufIo4<T>::ld(src, boff<T>(ok, gd * plane + gh * g.W + 4 * cx), v[b]);
+      dst[b] = e < total ? row * Wp + P + 4 * cx : -1;
+    }
+#pragma unroll
+    for (int b = 0; b < kChunkBatch; ++b) {
+      if (dst[b] >= 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lds[dst[b] + j] = v[b][j];
       }
     }
   }
+  if (P > 0) {
+    for (int row = threadIdx.x; row < rows; row += nthreads) {
+#pragma unroll
+      for (int j = 0; j < P; ++j) {
+        lds[row * Wp + j] = Acc(0);
+        lds[row * Wp + P + g.W + j] = Acc(0);
+      }
+    }
+  }
+}
+
+template <typename T, typename Acc, int P>
+__device__ inline void stage_input(Acc* __restrict__ lds, const T* __restrict__ x, const BandGeom& g, int64_t slab,
+                                   int d0, int hb0, int nthreads) {
+  if ((g.W & 3) == 0)
+    fill_band_w4<T, Acc, P>(lds, x, g, slab, d0, hb0, nthreads);
+  else
+    fill_band<T, Acc, P>(lds, x, g, slab, d0, hb0, nthreads);
+}
+
+// Workgroup -> (slab, band, D-run); the D-run varies fastest.
+struct BandTile {
+  int64_t slab;
+  int band, dc, d0, nd, p0, hb0;
+};
+
+__device__ inline BandTile band_tile(const BandGeom& g) {
+  BandTile t;
+  t.dc = static_cast<int>(blockIdx.x % g.nDc);
+  const int rest = static_cast<int>(blockIdx.x / g.nDc);
+  t.band = rest % g.nbands;
+  t.slab = rest / g.nbands;
+  t.d0 = t.dc * g.TD;
+  t.nd = min(g.TD, g.D - t.d0);
+  t.p0 = t.band * kBand;
+  t.hb0 = t.p0 / g.W;
+  return t;
+}
+
+// The weight gradient's staging: grad_output of the band into ds[od][l]
+// (CW consecutive positions per load) around the input planes' staging.
+constexpr int kDyBatch = 4;
+
+template <typename T, typename Acc, int CW>
+__device__ inline void dy_batch_load(Acc (&v)[kDyBatch][CW], __amdgpu_buffer_rsrc_t src, const BandGeom& g,
+                                     const BandTile& t, int base, int nthreads) {
+  const int hw = g.H * g.W;
+  const int nb = min(kBand, hw - t.p0);
+  constexpr int per_plane = kBand / CW;
+  const int total = g.TDk * per_plane;
+#pragma unroll
+  for (int b = 0; b < kDyBatch; ++b) {
+    const int e = base + b * nthreads + static_cast<int>(threadIdx.x);
+    const int od = e / per_plane, l = (e % per_plane) * CW;
+    const uint32_t off = boff<T>(e < total && od < t.nd && l < nb, (t.d0 + od) * hw + t.p0 + l);
+    if constexpr (CW == 4) {
+      BufIo4<T>::ld(src, off, v[b]);
+    } else {
+      v[b][0] = BufIo<T>::ld(src, off);
+    }
+  }
+}
+
+template <typename Acc, int CW>
+__device__ inline void dy_batch_store(Acc* __restrict__ ds, const Acc (&v)[kDyBatch][CW], const BandGeom& g,
+                                      int base, int nthreads) {
+  constexpr int per_plane = kBand / CW;
+  const int total = g.TDk * per_plane;
+#pragma unroll
+  for (int b = 0; b < kDyBatch; ++b) {
+    const int e = base + b * nthreads + static_cast<int>(threadIdx.x);
+    if (e < total) {
+#pragma unroll
+      for (int j = 0; j < CW; ++j) ds[(e / per_plane) * kBand + (e % per_plane) * CW + j] = v[b][j];
+    }
+  }
+}
+
+template <typename T, typename Acc, int P, int CW>
+__device__ inline void stage_band_dy(Acc* __restrict__ xs, Acc* __restrict__ ds, const T* __restrict__ x,
+                                     const T* __restrict__ dy, const BandGeom& g, const BandTile& t, int nthreads) {
+  const int hw = g.H * g.W;
+  const __amdgpu_buffer_rsrc_t src =
+      slab_rsrc(dy + t.slab * g.D * hw, static_cast<uint32_t>(g.D * hw * static_cast<int>(sizeof(T))));
+  const int total = g.TDk * (kBand / CW);
+  Acc v[kDyBatch][CW];
+  dy_batch_load<T, Acc, CW>(v, src, g, t, 0, nthreads);
+  stage_input<T, Acc, P>(xs, x, g, t.slab, t.d0, t.hb0, nthreads);
+  dy_batch_store<Acc, CW>(ds, v, g, 0, nthreads);
+  for (int base = nthreads * kDyBatch; base < total; base += nthreads * kDyBatch) {
+    dy_batch_load<T, Acc, CW>(v, src, g, t, base, nthreads);
+    dy_batch_store<Acc, CW>(ds, v, g, base, nthreads);
+  }
+}
+
+template <typename Acc, int K>
+__device__ inline void load_row(Acc (&xv)[K], const Acc* __restrict__ p) {
+#pragma unroll
+  for (int kw = 0; kw < K; ++kw) xv[kw] = p[kw];
+}
+
+template <typename Acc, int K>
+__device__ inline void shift_ring(Acc (&ring)[K]) {
+#pragma unroll
+  for (int j = K - 1; j > 0; --j) ring[j] = ring[j - 1];
 }
 
 template <typename T, typename Acc, int K, bool FLIP, bool BIAS>
-__global__ __launch_bounds__(kVolThreads) void dw_volume_stencil_kernel(const T* __restrict__ x,
-                                                                        const T* __restrict__ wt,
-                                                                        const T* __restrict__ bias,
-                                                                        T* __restrict__ y, VolGeom g) {
-  constexpr int P = K / 2, K3 = K * K * K, COL = kSeg + K - 1;
+__global__ __launch_bounds__(kBand * K) void dw_band_stencil_kernel(const T* __restrict__ x,
+                                                                    const T* __restrict__ wt,
+                                                                    const T* __restrict__ bias,
+                                                                    T* __restrict__ y, BandGeom g) {
+  constexpr int P = K / 2, K3 = K * K * K, NT = kBand * K;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   Acc* const xs = reinterpret_cast<Acc*>(smem_raw);
-  const int Hp = g.H + 2 * P, Wp = g.W + 2 * P;
-  const int per_slab = (g.TDp + 2 * P) * Hp * Wp;
-  Acc* const ws = xs + g.cpw * per_slab;  // [cpw][K3] taps (flipped for the input gradient)
-  Acc* const bs = ws + g.cpw * K3;        // [cpw] bias
+  const int Wp = g.W + 2 * P;
+  const int per_plane = g.SR * Wp;
+  Acc* const rows = xs + (g.TDk + 2 * P) * per_plane;  // [K][TDk][kBand] per-kernel-row sums
 
-  const int dc = static_cast<int>(blockIdx.x % g.nDc);
-  const int64_t slab0 = static_cast<int64_t>(blockIdx.x / g.nDc) * g.cpw;
-  const int d0 = dc * g.TD;
-  const int nd = min(g.TD, g.D - d0);
+  const BandTile t = band_tile(g);
+  stage_input<T, Acc, P>(xs, x, g, t.slab, t.d0, t.hb0, NT);
 
-  fill_volume<T, Acc, P>(xs, x, g, slab0, d0);
-  for (int e = threadIdx.x; e < g.cpw * K3; e += kVolThreads) {
-    const int s = e / K3, t = e - s * K3;
-    const int64_t slab = slab0 + s;
-    const int64_t c = slab % g.C;
-    ws[e] = slab < g.slabs ? load_acc<T, Acc>(wt, c * K3 + (FLIP ? K3 - 1 - t : t)) : Acc(0);
-  }
-  if (BIAS) {
-    for (int s = threadIdx.x; s < g.cpw; s += kVolThreads) {
-      const int64_t slab = slab0 + s;
-      bs[s] = slab < g.slabs ? load_acc<T, Acc>(bias, slab % g.C) : Acc(0);
+  // Wave kh holds the k * k taps of kernel row kh (flipped for the input gradient).
+  const int kh = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kBand);
+  const int lane = static_cast<int>(threadIdx.x) % kBand;
+  const int64_t c = t.slab % g.C;
+  Acc wr[K][K];
+#pragma unroll
+  for (int kd = 0; kd < K; ++kd)
+#pragma unroll
+    for (int kw = 0; kw < K; ++kw) {
+      const int tap = (kd * K + kh) * K + kw;
+      wr[kd][kw] = load_acc<T, Acc>(wt, c * K3 + (FLIP ? K3 - 1 - tap : tap));
     }
+  __syncthreads();
+
+  // Lanes past the plane walk its last position and store nothing.
+  const int hw = g.H * g.W;
+  const int pos = min(t.p0 + lane, hw - 1);
+  const int h = pos / g.W, w = pos - h * g.W;
+  const Acc* __restrict__ xr = xs + (h - t.hb0 + kh) * Wp + w;
+  Acc* __restrict__ rr = rows + kh * g.TDk * kBand + lane;
+
+  // ring[j] = this row's sum for output plane pd - j.
+  Acc ring[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) ring[j] = Acc(0);
+  Acc xv[K];
+  // Planes 0 .. K-2: outputs pd - kd < 0 do not exist.
+#pragma unroll
+  for (int pd = 0; pd < K - 1; ++pd) {
+    load_row(xv, xr + pd * per_plane);
+#pragma unroll
+    for (int kd = 0; kd <= pd; ++kd)
+#pragma unroll
+      for (int kw = 0; kw < K; ++kw) ring[kd] += wr[kd][kw] * xv[kw];
+    shift_ring(ring);
+    ring[0] = Acc(0);
+  }
+  for (int pd = K - 1; pd < g.TDk; ++pd) {
+    load_row(xv, xr + pd * per_plane);
+#pragma unroll
+    for (int kd = 0; kd < K; ++kd)
+#pragma unroll
+      for (int kw = 0; kw < K; ++kw) ring[kd] += wr[kd][kw] * xv[kw];
+    rr[(pd - (K - 1)) * kBand] = ring[K - 1];
+    shift_ring(ring);
+    ring[0] = Acc(0);
+  }
+  // Planes TDk .. TDk+K-2: outputs pd - kd >= TDk do not exist.
+#pragma unroll
+  for (int q = 0; q < K - 1; ++q) {
+    const int pd = g.TDk + q;
+    load_row(xv, xr + pd * per_plane);
+#pragma unroll
+    for (int kd = q + 1; kd < K; ++kd)
+#pragma unroll
+      for (int kw = 0; kw < K; ++kw) ring[kd] += wr[kd][kw] * xv[kw];
+    rr[(pd - (K - 1)) * kBand] = ring[K - 1];
+    shift_ring(ring);
+    ring[0] = Acc(0);
   }
   __syncthreads();
 
-  const int hw = g.H * g.W;
-  const int groups = g.TDp / kSeg;
-  const int items = g.cpw * groups * hw;
-  const int64_t plane = hw;
-  for (int item = threadIdx.x; item < items; item += kVolThreads) {
-    const int p = item % hw;
-    const int rest = item / hw;
-    const int grp = rest % groups, s = rest / groups;
-    const int64_t slab = slab0 + s;
-    const int od0 = grp * kSeg;
-    if (slab >= g.slabs || od0 >= nd) continue;
-    const int h = p / g.W, w = p - h * g.W;
-    const Acc* __restrict__ xv = xs + s * per_slab + (od0 * Hp + h) * Wp + w;
-    const Acc* __restrict__ wv = ws + s * K3;
-    Acc acc[kSeg];
+  // Output = bias + row 0 + ... + row K-1, one 64-position run per plane.
+  const Acc b = BIAS ? load_acc<T, Acc>(bias, c) : Acc(0);
+  const int nb = min(kBand, hw - t.p0);
+  T* __restrict__ out = y + (t.slab * g.D + t.d0) * hw + t.p0;
+  for (int e = threadIdx.x; e < t.nd * kBand; e += NT) {
+    const int od = e / kBand, l = e % kBand;
+    if (l >= nb) continue;
+    Acc v = b;
 #pragma unroll
-    for (int j = 0; j < kSeg; ++j) acc[j] = BIAS ? bs[s] : Acc(0);
-    // One kernel row at a time: unrolling kh as well would keep k^2 * COL
-    // loaded values live (k = 5: more registers than a lane has).
-#pragma unroll 1
-    for (int kh = 0; kh < K; ++kh) {
-#pragma unroll
-      for (int kw = 0; kw < K; ++kw) {
-        Acc col[COL];
-#pragma unroll
-        for (int i = 0; i < COL; ++i) col[i] = xv[(i * Hp + kh) * Wp + kw];
-#pragma unroll
-        for (int kd = 0; kd < K; ++kd) {
-          const Acc tap = wv[(kd * K + kh) * K + kw];
-#pragma unroll
-          for (int j = 0; j < kSeg; ++j) acc[j] += tap * col[j + kd];
-        }
-      }
-    }
-    T* __restrict__ out = y + (slab * g.D + d0 + od0) * plane + p;
-#pragma unroll
-    for (int j = 0; j < kSeg; ++j) {
-      if (od0 + j < nd) out[j * plane] = Cvt<T, Acc>::store(acc[j]);
-    }
+    for (int r = 0; r < K; ++r) v += rows[(r * g.TDk + od) * kBand + l];
+    out[static_cast<int64_t>(od) * hw + l] = Cvt<T, Acc>::store(v);
   }
 }
 
-// Taps reduced per LDS round of the weight gradient (fewer for fp64, whose
-// staged planes take twice the LDS) and lanes per first-level segment.
-template <typename Acc>
-constexpr int red_taps() { return sizeof(Acc) == 8 ? 8 : 16; }
-constexpr int kRedSeg = 16;
-
-// Input-plane D-run KDP of the k taps along D accumulated per pass: all of
-// them (one pass) unless fp64 accumulators for k = 5 would exceed the lanes'
-// registers (then one kd per pass).
+// Values per lane (one kernel row's taps + the bias sum) reduced per LDS
+// round: all of them, except fp64 at k = 5, whose 26 values per lane are
+// reduced in two rounds to stay within the staged LDS footprint.
 template <typename Acc, int K>
-constexpr int kd_per_pass() { return sizeof(Acc) == 8 && K == 5 ? 1 : K; }
+constexpr int band_red_values() {
+  return sizeof(Acc) == 8 && K == 5 ? 13 : K * K + 1;
+}
 
 template <typename T, typename Acc, int K>
-__global__ __launch_bounds__(kVolThreads) void dw_volume_wgrad_kernel(const T* __restrict__ x,
-                                                                      const T* __restrict__ dy,
-                                                                      Acc* __restrict__ partial, VolGeom g,
-                                                                      int splits) {
-  constexpr int P = K / 2, K2 = K * K, K3 = K2 * K;
-  constexpr int KDP = kd_per_pass<Acc, K>();
-  constexpr int NACC = KDP * K2 + 1;  // taps of one pass + the bias sum
-  constexpr int RT = red_taps<Acc>();
+__global__ __launch_bounds__(kBand * K) void dw_band_wgrad_kernel(const T* __restrict__ x,
+                                                                  const T* __restrict__ dy,
+                                                                  Acc* __restrict__ partial, BandGeom g,
+                                                                  int splits) {
+  constexpr int P = K / 2, K2 = K * K, K3 = K2 * K, NT = kBand * K;
+  constexpr int NACC = K2 + 1;  // this kernel row's taps + the bias sum
+  constexpr int RT = band_red_values<Acc, K>();
+  constexpr int PITCH = RT | 1;  // odd: lane-strided LDS accesses hit distinct banks
   extern __shared__ __align__(16) unsigned char smem_raw[];
   Acc* const xs = reinterpret_cast<Acc*>(smem_raw);
-  const int Hp = g.H + 2 * P, Wp = g.W + 2 * P;
+  const int Wp = g.W + 2 * P;
+  const int per_plane = g.SR * Wp;
+  Acc* const ds = xs + (g.TDk + 2 * P) * per_plane;  // [TDk][kBand] grad_output of the band
+
+  const BandTile t = band_tile(g);
   const int hw = g.H * g.W;
-  const int planes = g.TDp + 2 * P;
-  const int x_slab = planes * Hp * Wp;
-  Acc* const ds = xs + g.cpw * x_slab;          // [cpw][TDp][H][W] grad_output
-  Acc* const red = ds + g.cpw * g.TDp * hw;      // [RT][kVolThreads] lane values of one round
-  Acc* const segs = red + RT * kVolThreads;      // [RT][kVolThreads / kRedSeg] segment sums
-
-  const int dc = static_cast<int>(blockIdx.x % g.nDc);
-  const int64_t slab0 = static_cast<int64_t>(blockIdx.x / g.nDc) * g.cpw;
-  const int d0 = dc * g.TD;
-  const int nd = min(g.TD, g.D - d0);
-
-  fill_volume<T, Acc, P>(xs, x, g, slab0, d0);
-  {
-    const int64_t plane = hw;
-    for (int p = threadIdx.x; p < hw; p += kVolThreads) {
-      for (int s = 0; s < g.cpw; ++s) {
-        const int64_t slab = slab0 + s;
-        const bool ok = slab < g.slabs;
-        const int64_t base = ok ? (slab * g.D + d0) * plane + p : 0;
-        Acc* __restrict__ out = ds + static_cast<int64_t>(s) * g.TDp * hw + p;
-        for (int od0 = 0; od0 < g.TDp; od0 += kFillBatch) {
-          Acc v[kFillBatch];
-#pragma unroll
-          for (int b = 0; b < kFillBatch; ++b)
-            v[b] = (ok && od0 + b < nd) ? load_acc<T, Acc>(dy, base + (od0 + b) * plane) : Acc(0);
-#pragma unroll
-          for (int b = 0; b < kFillBatch; ++b) {
-            if (od0 + b < g.TDp) out[(od0 + b) * hw] = v[b];
-          }
-        }
-      }
-    }
-  }
+  // grad_output of the band, ds[od][l] for the band's position l: the first
+  // batch of loads is issued before the input planes are staged and stays in
+  // flight meanwhile. With W % 4 == 0 a band is whole 4-position chunks.
+  if ((g.W & 3) == 0)
+    stage_band_dy<T, Acc, P, 4>(xs, ds, x, dy, g, t, NT);
+  else
+    stage_band_dy<T, Acc, P, 1>(xs, ds, x, dy, g, t, NT);
   __syncthreads();
 
-  // Lane -> (slab s, position p); lanes past cpw * hw only add zeros.
-  const int t = threadIdx.x;
-  const int s = t / hw, p = t - s * hw;
-  const bool active = s < g.cpw;
-  const int h = active ? p / g.W : 0, w = active ? p - h * g.W : 0;
-  const Acc* __restrict__ xv = xs + (active ? s : 0) * x_slab + h * Wp + w;
-  const Acc* __restrict__ dv = ds + (active ? s : 0) * g.TDp * hw + p;
-  // Two-level fixed-order lane sums when slabs start on segment boundaries
-  // (H * W % kRedSeg == 0; the 8^3 and 16^3 planes), else one lane per
-  // (slab, tap) adds the slab's lanes in order.
-  const bool by_segment = hw % kRedSeg == 0;
+  const int kh = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kBand);
+  const int lane = static_cast<int>(threadIdx.x) % kBand;
+  // Lanes past the plane walk its last position against zero grad_output.
+  const int pos = min(t.p0 + lane, hw - 1);
+  const int h = pos / g.W, w = pos - h * g.W;
+  const Acc* __restrict__ xr = xs + (h - t.hb0 + kh) * Wp + w;
+  const Acc* __restrict__ dr = ds + lane;
 
-  // Passes and reduction rounds are unrolled so that every register-array
-  // index (accumulator, grad_output ring) is a compile-time constant.
+  Acc acc[K][K];
 #pragma unroll
-  for (int kd0 = 0; kd0 < K; kd0 += KDP) {
-    // Input plane pd (padded index) meets grad_output plane pd - kd through tap kd.
-    Acc acc[NACC];
+  for (int kd = 0; kd < K; ++kd)
 #pragma unroll
-    for (int i = 0; i < NACC; ++i) acc[i] = Acc(0);
-    if (active) {
-      Acc ring[K];  // ring[j] = grad_output plane pd - j (zero outside [0, TDp))
+    for (int kw = 0; kw < K; ++kw) acc[kd][kw] = Acc(0);
+  Acc bsum = Acc(0);
+  Acc ring[K];  // ring[j] = grad_output plane pd - j
 #pragma unroll
-      for (int j = 0; j < K; ++j) ring[j] = Acc(0);
-      for (int pd = 0; pd < planes; ++pd) {
+  for (int j = 0; j < K; ++j) ring[j] = Acc(0);
+  Acc xv[K];
+  // Input plane pd meets grad_output plane pd - kd through tap kd; planes
+  // 0 .. K-2 have no grad_output plane pd - kd < 0.
 #pragma unroll
-        for (int j = K - 1; j > 0; --j) ring[j] = ring[j - 1];
-        ring[0] = pd < g.TDp ? dv[pd * hw] : Acc(0);
-        if (kd0 == 0) acc[NACC - 1] += ring[0];
+  for (int pd = 0; pd < K - 1; ++pd) {
+    shift_ring(ring);
+    ring[0] = dr[pd * kBand];
+    bsum += ring[0];
+    load_row(xv, xr + pd * per_plane);
 #pragma unroll
-        for (int kh = 0; kh < K; ++kh)
+    for (int kd = 0; kd <= pd; ++kd)
 #pragma unroll
-          for (int kw = 0; kw < K; ++kw) {
-            const Acc xval = xv[(pd * Hp + kh) * Wp + kw];
+      for (int kw = 0; kw < K; ++kw) acc[kd][kw] += xv[kw] * ring[kd];
+  }
+  for (int pd = K - 1; pd < g.TDk; ++pd) {
+    shift_ring(ring);
+    ring[0] = dr[pd * kBand];
+    bsum += ring[0];
+    load_row(xv, xr + pd * per_plane);
 #pragma unroll
-            for (int j = 0; j < KDP; ++j) acc[(j * K + kh) * K + kw] += xval * ring[kd0 + j];
-          }
-      }
+    for (int kd = 0; kd < K; ++kd)
+#pragma unroll
+      for (int kw = 0; kw < K; ++kw) acc[kd][kw] += xv[kw] * ring[kd];
+  }
+  // Planes TDk .. TDk+K-2 have no grad_output plane pd - kd >= TDk.
+#pragma unroll
+  for (int q = 0; q < K - 1; ++q) {
+    const int pd = g.TDk + q;
+    shift_ring(ring);
+    ring[0] = Acc(0);
+    load_row(xv, xr + pd * per_plane);
+#pragma unroll
+    for (int kd = q + 1; kd < K; ++kd)
+#pragma unroll
+      for (int kw = 0; kw < K; ++kw) acc[kd][kw] += xv[kw] * ring[kd];
+  }
+
+  // Per-wave fixed-order reduction over the 64 lanes, through LDS that aliases
+  // the staged planes: value r0 + i of lane l at red[l * PITCH + i].
+  Acc* __restrict__ red = xs + kh * kBand * PITCH;
+  const int64_t c = t.slab % g.C, n = t.slab / g.C;
+  const int64_t split = (n * g.nbands + t.band) * g.nDc + t.dc;
+#pragma unroll
+  for (int r0 = 0; r0 < NACC; r0 += RT) {
+    __syncthreads();  // staged planes (first round) / previous round read by every wave
+#pragma unroll
+    for (int i = 0; i < RT; ++i) {
+      const int v = r0 + i;
+      if (v < NACC) red[lane * PITCH + i] = v < K2 ? acc[v / K][v % K] : bsum;
     }
-    // Reduce acc over the lanes of each slab, RT taps per round.
-    const int ntaps = kd0 == 0 ? NACC : NACC - 1;
+    __syncthreads();
+    const int nr = min(RT, NACC - r0);
+    // Item j = (value i, 16-lane segment q); the four segments of a value sit
+    // in one lane quad and are added with two butterflies.
+    for (int j0 = 0; j0 < nr * 4; j0 += kBand) {
+      const int j = j0 + lane;
+      const int i = j >> 2, q = j & 3;
+      Acc s = Acc(0);
+      if (j < nr * 4) {
 #pragma unroll
-    for (int r0 = 0; r0 < NACC; r0 += RT) {
-      if (r0 >= ntaps) break;
-#pragma unroll
-      for (int i = 0; i < NACC; ++i) {
-        if (i >= r0 && i < r0 + RT) red[(i - r0) * kVolThreads + t] = acc[i];
+        for (int l = 0; l < 16; ++l) s += red[(q * 16 + l) * PITCH + i];
       }
-      __syncthreads();
-      const int nr = min(RT, ntaps - r0);
-      if (by_segment) {
-        constexpr int NSEG = kVolThreads / kRedSeg;
-        for (int e = t; e < nr * NSEG; e += kVolThreads) {
-          const int i = e / NSEG, q = e - i * NSEG;
-          Acc v = Acc(0);
-#pragma unroll
-          for (int l = 0; l < kRedSeg; ++l) v += red[i * kVolThreads + q * kRedSeg + l];
-          segs[i * NSEG + q] = v;
-        }
-        __syncthreads();
+      s += __shfl_xor(s, 1);
+      s += __shfl_xor(s, 2);
+      const int v = r0 + i;
+      if (j < nr * 4 && q == 0 && (v < K2 || kh == 0)) {
+        const int tap = v < K2 ? ((v / K) * K + kh) * K + v % K : K3;
+        partial[(c * (K3 + 1) + tap) * splits + split] = s;
       }
-      for (int e = t; e < g.cpw * nr; e += kVolThreads) {
-        const int ss = e / nr, i = e - ss * nr;
-        const int64_t slab = slab0 + ss;
-        if (slab >= g.slabs) continue;
-        Acc v = Acc(0);
-        if (by_segment) {
-          const int NSEG = kVolThreads / kRedSeg;
-          for (int q = ss * hw / kRedSeg; q < (ss + 1) * hw / kRedSeg; ++q) v += segs[i * NSEG + q];
-        } else {
-          for (int q = ss * hw; q < (ss + 1) * hw; ++q) v += red[i * kVolThreads + q];
-        }
-        const int ai = r0 + i;
-        const int tap = ai == NACC - 1 ? K3 : kd0 * K2 + ai;
-        const int64_t c = slab % g.C, n = slab / g.C;
-        partial[(c * (K3 + 1) + tap) * splits + n * g.nDc + dc] = v;
-      }
-      __syncthreads();
     }
   }
 }
 
-size_t volume_lds_bytes(const VolGeom& g, int k, int acc_bytes, bool wgrad) {
-  const int P = k / 2, k3 = k * k * k, k2 = k * k;
-  const size_t x = static_cast<size_t>(g.cpw) * (g.TDp + 2 * P) * (g.H + 2 * P) * (g.W + 2 * P);
-  if (!wgrad) return (x + static_cast<size_t>(g.cpw) * (k3 + 1)) * acc_bytes;
-  const size_t dys = static_cast<size_t>(g.cpw) * g.TDp * g.H * g.W;
-  // One round of lane values plus its segment sums.
-  const int rt = acc_bytes == 8 ? 8 : 16;
-  const size_t red = static_cast<size_t>(rt) * kVolThreads + static_cast<size_t>(rt) * (kVolThreads / kRedSeg);
-  (void)k2;
-  return (x + dys + red) * acc_bytes;
+int64_t band_rows(int64_t h, int64_t w) {
+  const int64_t hw = h * w;
+  int64_t most = 1;
+  for (int64_t p0 = 0; p0 < hw; p0 += kBand) {
+    const int64_t last = std::min<int64_t>(p0 + kBand, hw) - 1;
+    most = std::max<int64_t>(most, last / w - p0 / w + 1);
+  }
+  return most;
 }
 
-int volume_plan(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int dtype, int seg, int depth_chunk,
-                bool wgrad, VolGeom* g, size_t* lds) {
+size_t band_lds_bytes(const BandGeom& g, int k, int acc_bytes, bool wgrad) {
+  const int P = k / 2;
+  const size_t staged = static_cast<size_t>(g.TDk + 2 * P) * g.SR * (g.W + 2 * P);
+  if (!wgrad) return (staged + static_cast<size_t>(k) * g.TDk * kBand) * acc_bytes;
+  const int rt = acc_bytes == 8 && k == 5 ? 13 : k * k + 1;
+  const size_t red = static_cast<size_t>(k) * kBand * (rt | 1);
+  return std::max(staged + static_cast<size_t>(g.TDk) * kBand, red) * acc_bytes;
+}
+
+uint32_t magic31(int64_t d) { return static_cast<uint32_t>(((int64_t(1) << 31) + d - 1) / d); }
+
+int band_plan(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int dtype, int band, int depth_chunk,
+              bool wgrad, BandGeom* g, size_t* lds) {
   MEDNEXT_CHECK_ARG(n >= 1 && c >= 1 && d >= 1 && h >= 1 && w >= 1, "shape must be positive");
   MEDNEXT_CHECK_ARG(k == 1 || k == 3 || k == 5, "kernel_size must be 1, 3 or 5");
-  MEDNEXT_CHECK_ARG(h * w <= kVolThreads, "the volume engine takes planes of at most 256 elements (H * W)");
-  MEDNEXT_CHECK_ARG(seg == kSeg, "the volume engine's tile_w (output planes per lane) must be 4");
+  MEDNEXT_CHECK_ARG(h * w <= 4 * kBand, "the volume engine takes planes of at most 256 elements (H * W)");
+  MEDNEXT_CHECK_ARG(band == kBand, "the volume engine's tile_w (plane positions per workgroup) must be 64");
   MEDNEXT_CHECK_ARG(depth_chunk >= 1, "depth_chunk must be >= 1");
-  MEDNEXT_CHECK_ARG(d < (int64_t(1) << 31) && n * c < (int64_t(1) << 40), "shape out of range");
+  MEDNEXT_CHECK_ARG(d < (int64_t(1) << 24) && n * c < (int64_t(1) << 40), "shape out of range");
+  const int64_t elem = dtype == MEDNEXT_DTYPE_F64 ? 8 : dtype == MEDNEXT_DTYPE_F32 ? 4 : 2;
+  MEDNEXT_CHECK_ARG(d * h * w * elem < (int64_t(1) << 31), "one (n, c) slab must be under 2 GiB");
+  const int P = k / 2;
   const int acc = dtype == MEDNEXT_DTYPE_F64 ? 8 : 4;
   g->C = static_cast<int>(c);
   g->D = static_cast<int>(d);
   g->H = static_cast<int>(h);
   g->W = static_cast<int>(w);
   g->TD = static_cast<int>(std::min<int64_t>(depth_chunk, d));
-  g->TDp = static_cast<int>(cdiv(g->TD, kSeg) * kSeg);
+  g->TDk = std::max(g->TD, k - 1);
   g->nDc = static_cast<int>(cdiv(d, g->TD));
+  g->nbands = static_cast<int>(cdiv(h * w, kBand));
+  g->SR = static_cast<int>(band_rows(h, w)) + 2 * P;
+  g->wp_magic = magic31(w + 2 * P);
+  g->plane_magic = magic31(static_cast<int64_t>(g->SR) * (w + 2 * P));
+  g->w4_magic = magic31(std::max<int64_t>(1, w / 4));
+  g->sr_magic = magic31(g->SR);
   g->slabs = n * c;
-  g->cpw = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kVolThreads / (h * w), n * c)));
-  // Fewer slabs per workgroup until the staged planes fit 64 KiB of LDS.
-  while (g->cpw > 1 && volume_lds_bytes(*g, k, acc, wgrad) > 64 * 1024) --g->cpw;
-  *lds = volume_lds_bytes(*g, k, acc, wgrad);
+  *lds = band_lds_bytes(*g, k, acc, wgrad);
   MEDNEXT_CHECK_ARG(*lds <= 64 * 1024, "depth_chunk too long: the staged planes exceed 64 KiB of LDS");
-  const int64_t blocks = cdiv(g->slabs, g->cpw) * g->nDc;
+  const int64_t blocks = g->slabs * g->nbands * g->nDc;
   MEDNEXT_CHECK_ARG(blocks < (int64_t(1) << 31), "grid too large");
   return MEDNEXT_STATUS_OK;
 }
 
+dim3 band_grid(const BandGeom& g) { return dim3(static_cast<unsigned>(g.slabs * g.nbands * g.nDc)); }
+
 template <typename T, int K, bool FLIP>
-int launch_volume_stencil(const void* x, const void* wt, const void* bias, void* y, const VolGeom& g, size_t lds,
-                          hipStream_t st) {
+int launch_band_stencil(const void* x, const void* wt, const void* bias, void* y, const BandGeom& g, size_t lds,
+                        hipStream_t st) {
   using Acc = typename AccOf<T>::type;
-  const dim3 grid(static_cast<unsigned>(cdiv(g.slabs, g.cpw) * g.nDc));
   auto px = static_cast<const T*>(x);
   auto pw = static_cast<const T*>(wt);
   auto pb = static_cast<const T*>(bias);
   auto py = static_cast<T*>(y);
   if (bias != nullptr)
-    hipLaunchKernelGGL((dw_volume_stencil_kernel<T, Acc, K, FLIP, true>), grid, dim3(kVolThreads), lds, st, px, pw,
-                       pb, py, g);
+    hipLaunchKernelGGL((dw_band_stencil_kernel<T, Acc, K, FLIP, true>), band_grid(g), dim3(kBand * K), lds, st, px,
+                       pw, pb, py, g);
   else
-    hipLaunchKernelGGL((dw_volume_stencil_kernel<T, Acc, K, FLIP, false>), grid, dim3(kVolThreads), lds, st, px,
+    hipLaunchKernelGGL((dw_band_stencil_kernel<T, Acc, K, FLIP, false>), band_grid(g), dim3(kBand * K), lds, st, px,
                        pw, pb, py, g);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }
 
 template <typename T, bool FLIP>
-int volume_stencil_t(const void* x, const void* wt, const void* bias, void* y, const VolGeom& g, int k, size_t lds,
-                     hipStream_t st) {
+int band_stencil_t(const void* x, const void* wt, const void* bias, void* y, const BandGeom& g, int k, size_t lds,
+                   hipStream_t st) {
   switch (k) {
-    case 1: return launch_volume_stencil<T, 1, FLIP>(x, wt, bias, y, g, lds, st);
-    case 3: return launch_volume_stencil<T, 3, FLIP>(x, wt, bias, y, g, lds, st);
-    default: return launch_volume_stencil<T, 5, FLIP>(x, wt, bias, y, g, lds, st);
+    case 1: return launch_band_stencil<T, 1, FLIP>(x, wt, bias, y, g, lds, st);
+    case 3: return launch_band_stencil<T, 3, FLIP>(x, wt, bias, y, g, lds, st);
+    default: return launch_band_stencil<T, 5, FLIP>(x, wt, bias, y, g, lds, st);
   }
 }
 
-template <typename T>
-int volume_wgrad_t(const void* x, const void* dy, void* partial, const VolGeom& g, int k, int splits, size_t lds,
-                   hipStream_t st) {
+template <typename T, int K>
+int launch_band_wgrad(const void* x, const void* dy, void* partial, const BandGeom& g, int splits, size_t lds,
+                      hipStream_t st) {
   using Acc = typename AccOf<T>::type;
-  const dim3 grid(static_cast<unsigned>(cdiv(g.slabs, g.cpw) * g.nDc));
-  auto px = static_cast<const T*>(x);
-  auto pd = static_cast<const T*>(dy);
-  auto part = static_cast<Acc*>(partial);
-  switch (k) {
-    case 1:
-      hipLaunchKernelGGL((dw_volume_wgrad_kernel<T, Acc, 1>), grid, dim3(kVolThreads), lds, st, px, pd, part, g, splits);
-      break;
-    case 3:
-      hipLaunchKernelGGL((dw_volume_wgrad_kernel<T, Acc, 3>), grid, dim3(kVolThreads), lds, st, px, pd, part, g, splits);
-      break;
-    default:
-      hipLaunchKernelGGL((dw_volume_wgrad_kernel<T, Acc, 5>), grid, dim3(kVolThreads), lds, st, px, pd, part, g, splits);
-      break;
-  }
+  hipLaunchKernelGGL((dw_band_wgrad_kernel<T, Acc, K>), band_grid(g), dim3(kBand * K), lds, st,
+                     static_cast<const T*>(x), static_cast<const T*>(dy), static_cast<Acc*>(partial), g, splits);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }
 
-}  // namespace
-
-bool dw_volume_supported(int64_t h, int64_t w) { return h >= 1 && w >= 1 && h * w <= kVolThreads; }
-
-int dw_volume_stencil(const void* x, const void* weight, const void* bias, void* y, int64_t n, int64_t c, int64_t d,
-                      int64_t h, int64_t w, int k, int dtype, bool flip, int seg, int depth_chunk, hipStream_t st) {
-  VolGeom g{};
-  size_t lds = 0;
-  if (int status = volume_plan(n, c, d, h, w, k, dtype, seg, depth_chunk, false, &g, &lds)) return status;
-#define MEDNEXT_VOL_STENCIL(T) \
-  return flip ? volume_stencil_t<T, true>(x, weight, bias, y, g, k, lds, st) \
-              : volume_stencil_t<T, false>(x, weight, bias, y, g, k, lds, st)
-  switch (dtype) {
-    case MEDNEXT_DTYPE_F32: MEDNEXT_VOL_STENCIL(float);
-    case MEDNEXT_DTYPE_F64: MEDNEXT_VOL_STENCIL(double);
-    case MEDNEXT_DTYPE_F16: MEDNEXT_VOL_STENCIL(f16_t);
-    default: MEDNEXT_VOL_STENCIL(bf16_t);
+template <typename T>
+int band_wgrad_t(const void* x, const void* dy, void* partial, const BandGeom& g, int k, int splits, size_t lds,
+                 hipStream_t st) {
+  switch (k) {
+    case 1: return launch_band_wgrad<T, 1>(x, dy, partial, g, splits, lds, st);
+    case 3: return launch_band_wgrad<T, 3>(x, dy, partial, g, splits, lds, st);
+    default: return launch_band_wgrad<T, 5>(x, dy, partial, g, splits, lds, st);
   }
-#undef MEDNEXT_VOL_STENCIL
 }
 
-int dw_volume_wgrad_splits(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int dtype, int seg,
-                           int depth_chunk) {
-  VolGeom g{};
+}  // namespace
+
+bool dw_volume_supported(int64_t h, int64_t w) { return h >= 1 && w >= 1 && h * w <= 4 * kBand; }
+
+int dw_volume_stencil(const void* x, const void* weight, const void* bias, void* y, int64_t n, int64_t c, int64_t d,
+                      int64_t h, int64_t w, int k, int dtype, bool flip, int band, int depth_chunk, hipStream_t st) {
+  BandGeom g{};
   size_t lds = 0;
-  if (volume_plan(n, c, d, h, w, k, dtype, seg, depth_chunk, true, &g, &lds) != MEDNEXT_STATUS_OK) return 0;
-  const int64_t splits = n * g.nDc;
+  if (int status = band_plan(n, c, d, h, w, k, dtype, band, depth_chunk, false, &g, &lds)) return status;
+#define MEDNEXT_BAND_STENCIL(T) \
+  return flip ? band_stencil_t<T, true>(x, weight, bias, y, g, k, lds, st) \
+              : band_stencil_t<T, false>(x, weight, bias, y, g, k, lds, st)
+  switch (dtype) {
+    case MEDNEXT_DTYPE_F32: MEDNEXT_BAND_STENCIL(float);
+    case MEDNEXT_DTYPE_F64: MEDNEXT_BAND_STENCIL(double);
+    case MEDNEXT_DTYPE_F16: MEDNEXT_BAND_STENCIL(f16_t);
+    default: MEDNEXT_BAND_STENCIL(bf16_t);
+  }
+#undef MEDNEXT_BAND_STENCIL
+}
+
+int dw_volume_wgrad_splits(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int dtype, int band,
+                           int depth_chunk) {
+  BandGeom g{};
+  size_t lds = 0;
+  if (band_plan(n, c, d, h, w, k, dtype, band, depth_chunk, true, &g, &lds) != MEDNEXT_STATUS_OK) return 0;
+  const int64_t splits = n * g.nbands * g.nDc;
   return splits < (int64_t(1) << 31) ? static_cast<int>(splits) : 0;
 }
 
 int dw_volume_wgrad(const void* x, const void* dy, void* partial, int64_t n, int64_t c, int64_t d, int64_t h,
-                    int64_t w, int k, int dtype, int seg, int depth_chunk, hipStream_t st) {
-  VolGeom g{};
+                    int64_t w, int k, int dtype, int band, int depth_chunk, hipStream_t st) {
+  BandGeom g{};
   size_t lds = 0;
-  if (int status = volume_plan(n, c, d, h, w, k, dtype, seg, depth_chunk, true, &g, &lds)) return status;
-  const int64_t splits = n * g.nDc;
+  if (int status = band_plan(n, c, d, h, w, k, dtype, band, depth_chunk, true, &g, &lds)) return status;
+  const int64_t splits = n * g.nbands * g.nDc;
   MEDNEXT_CHECK_ARG(splits < (int64_t(1) << 31), "too many partials");
+  const int s = static_cast<int>(splits);
   switch (dtype) {
-    case MEDNEXT_DTYPE_F32: return volume_wgrad_t<float>(x, dy, partial, g, k, static_cast<int>(splits), lds, st);
-    case MEDNEXT_DTYPE_F64: return volume_wgrad_t<double>(x, dy, partial, g, k, static_cast<int>(splits), lds, st);
-    case MEDNEXT_DTYPE_F16: return volume_wgrad_t<f16_t>(x, dy, partial, g, k, static_cast<int>(splits), lds, st);
-    default: return volume_wgrad_t<bf16_t>(x, dy, partial, g, k, static_cast<int>(splits), lds, st);
+    case MEDNEXT_DTYPE_F32: return band_wgrad_t<float>(x, dy, partial, g, k, s, lds, st);
+    case MEDNEXT_DTYPE_F64: return band_wgrad_t<double>(x, dy, partial, g, k, s, lds, st);
+    case MEDNEXT_DTYPE_F16: return band_wgrad_t<f16_t>(x, dy, partial, g, k, s, lds, st);
+    default: return band_wgrad_t<bf16_t>(x, dy, partial, g, k, s, lds, st);
   }
 }
 

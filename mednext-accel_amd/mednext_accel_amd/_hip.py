@@ -116,7 +116,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

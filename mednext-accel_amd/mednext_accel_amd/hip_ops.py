@@ -28,7 +28,7 @@ from .tiles import (
     ENGINE_MFMA,
     ENGINE_VALU,
     ENGINE_VOLUME,
-    VOLUME_SEG,
+    VOLUME_BAND,
     depthwise_recipe,
     group_norm_splits,
     pointwise_blocks,
@@ -64,8 +64,8 @@ def _checked_recipe(recipe: tuple[int, int, int]) -> tuple[int, int, int]:
         if tile_w not in (32, 64, 128):
             raise ValueError("MFMA tile_w must be 32, 64 or 128")
     elif engine == ENGINE_VOLUME:
-        if tile_w != VOLUME_SEG:
-            raise ValueError(f"volume-engine tile_w must be {VOLUME_SEG}")
+        if tile_w != VOLUME_BAND:
+            raise ValueError(f"volume-engine tile_w must be {VOLUME_BAND}")
     else:
         raise ValueError("engine must be 0 (VALU), 1 (MFMA) or 2 (VOLUME)")
     if depth_chunk < 1:

@@ -87,7 +87,7 @@ def validate_parameters(implementation: str, parameters: Mapping[str, object]) -
         raise ValueError("parameters.engine must be 0 (VALU), 1 (MFMA) or 2 (VOLUME)")
     if "tile_w" in parameters:
         tile_w = _positive_int("tile_w", parameters["tile_w"])
-        widths = {tiles.ENGINE_MFMA: (32, 64, 128), tiles.ENGINE_VOLUME: (tiles.VOLUME_SEG,)}.get(
+        widths = {tiles.ENGINE_MFMA: (32, 64, 128), tiles.ENGINE_VOLUME: (tiles.VOLUME_BAND,)}.get(
             engine, tiles.TILE_WIDTHS
         )
         if tile_w not in widths:

@@ -138,12 +138,11 @@ def mfma_wgrad_rows(kernel_size: int, tile_w: int) -> int:
 
 # ----------------------------------------------------------- small planes
 
-VOLUME_SEG = 4  # output planes per lane of the volume kernels (their tile_w)
-VOLUME_MAX_PLANE = MAX_THREADS  # H * W the volume kernels take
+VOLUME_BAND = 64  # plane positions per workgroup of the volume kernels (their tile_w)
+VOLUME_MAX_PLANE = 4 * VOLUME_BAND  # H * W the volume kernels take
 VOLUME_TARGET_WORKGROUPS = 2 * CU_COUNT
-# Phases whose default recipe is the volume engine on small planes (the weight
-# gradient keeps the VALU stencil until its volume kernel is faster there).
-VOLUME_PHASES = ("forward", "input_grad")
+# Phases whose default recipe is the volume engine on small planes.
+VOLUME_PHASES = ("forward", "input_grad", "weight_grad")
 LDS_LIMIT = 64 * 1024  # per-workgroup LDS the kernels request at most
 
 
@@ -155,54 +154,71 @@ def volume_supported(spatial: tuple[int, int, int]) -> bool:
 
 @dataclass(frozen=True, slots=True)
 class VolumePlan:
-    """Launch shape of the volume kernels (mirrors volume_plan in depthwise_volume.hip)."""
+    """Launch shape of the volume kernels (mirrors band_plan in depthwise_volume.hip):
+    one workgroup of k waves per (slab, band of 64 plane positions, D-run)."""
 
-    slabs_per_workgroup: int
     depth_chunk: int
     chunks_d: int
+    bands: int
+    staged_rows: int
     workgroups: int
+    threads: int
     lds_bytes: int
 
 
-def volume_lds_bytes(cpw: int, depth_chunk: int, spatial, kernel_size: int, acc_bytes: int, wgrad: bool) -> int:
-    _d, h, w = spatial
+def volume_band_rows(h: int, w: int) -> int:
+    """The most plane rows one band of VOLUME_BAND positions spans."""
+    most = 1
+    for p0 in range(0, h * w, VOLUME_BAND):
+        last = min(p0 + VOLUME_BAND, h * w) - 1
+        most = max(most, last // w - p0 // w + 1)
+    return most
+
+
+def volume_lds_bytes(depth_chunk: int, spatial, kernel_size: int, acc_bytes: int, wgrad: bool) -> int:
+    d, h, w = spatial
     p = kernel_size // 2
-    tdp = _cdiv(depth_chunk, VOLUME_SEG) * VOLUME_SEG
-    staged = cpw * (tdp + 2 * p) * (h + 2 * p) * (w + 2 * p)
+    walk = max(min(depth_chunk, d), kernel_size - 1)
+    staged = (walk + 2 * p) * (volume_band_rows(h, w) + 2 * p) * (w + 2 * p)
     if not wgrad:
-        return (staged + cpw * (kernel_size**3 + 1)) * acc_bytes
-    taps = 8 if acc_bytes == 8 else 16  # lane values reduced per LDS round
-    red = taps * MAX_THREADS + taps * (MAX_THREADS // 16)
-    return (staged + cpw * tdp * h * w + red) * acc_bytes
+        return (staged + kernel_size * walk * VOLUME_BAND) * acc_bytes
+    values = 13 if (acc_bytes == 8 and kernel_size == 5) else kernel_size**2 + 1
+    red = kernel_size * VOLUME_BAND * (values | 1)
+    return max(staged + walk * VOLUME_BAND, red) * acc_bytes
 
 
 def volume_plan(batch: int, channels: int, spatial, kernel_size: int, depth_chunk: int, *, acc_bytes: int = 4,
                 wgrad: bool = False) -> VolumePlan:
     d, h, w = spatial
     td = min(depth_chunk, d)
-    slabs = batch * channels
-    cpw = max(1, min(MAX_THREADS // (h * w), slabs))
-    while cpw > 1 and volume_lds_bytes(cpw, td, spatial, kernel_size, acc_bytes, wgrad) > LDS_LIMIT:
-        cpw -= 1
     chunks = _cdiv(d, td)
-    return VolumePlan(cpw, td, chunks, _cdiv(slabs, cpw) * chunks,
-                      volume_lds_bytes(cpw, td, spatial, kernel_size, acc_bytes, wgrad))
+    bands = _cdiv(h * w, VOLUME_BAND)
+    return VolumePlan(td, chunks, bands, volume_band_rows(h, w) + 2 * (kernel_size // 2),
+                      batch * channels * bands * chunks, VOLUME_BAND * kernel_size,
+                      volume_lds_bytes(td, spatial, kernel_size, acc_bytes, wgrad))
 
 
 def volume_depth_chunk(batch: int, channels: int, spatial, kernel_size: int, acc_bytes: int) -> int:
-    """The longest D-run (a multiple of VOLUME_SEG, or D) whose grid still has
-    VOLUME_TARGET_WORKGROUPS workgroups and whose staged planes (weight
-    gradient, the larger footprint) fit the LDS limit."""
+    """The longest D-run (D, halved) whose grid still has
+    VOLUME_TARGET_WORKGROUPS workgroups (down to k - 1 planes, the walk's
+    minimum) and whose staged planes fit the LDS limit in both the stencil and
+    the weight-gradient kernel."""
     d = spatial[0]
-    td = d
+    floor = max(2, kernel_size - 1)
 
     def fits(td: int) -> bool:
-        return volume_plan(batch, channels, spatial, kernel_size, td, acc_bytes=acc_bytes, wgrad=True).lds_bytes <= LDS_LIMIT
+        return all(
+            volume_plan(batch, channels, spatial, kernel_size, td, acc_bytes=acc_bytes, wgrad=wgrad).lds_bytes
+            <= LDS_LIMIT
+            for wgrad in (False, True)
+        )
 
-    while td > VOLUME_SEG and (
-        volume_plan(batch, channels, spatial, kernel_size, td).workgroups < VOLUME_TARGET_WORKGROUPS or not fits(td)
+    td = d
+    while td > 1 and (
+        not fits(td)
+        or (td > floor and volume_plan(batch, channels, spatial, kernel_size, td).workgroups < VOLUME_TARGET_WORKGROUPS)
     ):
-        td = max(VOLUME_SEG, _cdiv(td // 2, VOLUME_SEG) * VOLUME_SEG)
+        td = _cdiv(td, 2)
     return td
 
 
@@ -222,8 +238,9 @@ def depthwise_recipe(
     weight-grad tiles ``mfma_wgrad_rows(k, tile_w)``. The D-run per workgroup is
     the longest that still yields ``MFMA_TARGET_WORKGROUPS``.
     Small planes (H * W <= 256: the 16^3 and 8^3 stages) run the volume
-    kernels, which stage whole planes in LDS, with ``tile_w = VOLUME_SEG`` and
-    the D-run of ``volume_depth_chunk``, in the phases of ``VOLUME_PHASES``.
+    kernels (one workgroup per 64-position band of a plane and D-run) with
+    ``tile_w = VOLUME_BAND`` and the D-run of ``volume_depth_chunk``, in the
+    phases of ``VOLUME_PHASES``.
     Everything else runs the VALU stencil with the widest tile the plane allows
     (up to 64 columns) and a D-run that yields TARGET_WORKGROUPS workgroups. In
     both cases at least k - 1 planes per workgroup (``depth_chunk_floor``).
@@ -244,7 +261,7 @@ def depthwise_recipe(
         return [ENGINE_MFMA, tile_w, _depth_chunk(d, slabs, kernel_size, target)]
     if volume_supported(spatial) and phase in VOLUME_PHASES:
         acc_bytes = 8 if dtype == "float64" else 4
-        return [ENGINE_VOLUME, VOLUME_SEG, volume_depth_chunk(batch, channels, spatial, kernel_size, acc_bytes)]
+        return [ENGINE_VOLUME, VOLUME_BAND, volume_depth_chunk(batch, channels, spatial, kernel_size, acc_bytes)]
     tile_w = 4
     while tile_w < 64 and tile_w < w:
         tile_w *= 2

@@ -17,7 +17,7 @@ import torch
 
 from helpers import BF16, FP32_OUT, FP32_WGRAD, max_rel
 from mednext_accel_amd import hip_ops
-from mednext_accel_amd.tiles import ENGINE_VOLUME, VOLUME_SEG, depthwise_recipe
+from mednext_accel_amd.tiles import ENGINE_VOLUME, VOLUME_BAND, depthwise_recipe
 from oracle import depthwise as odw
 
 pytestmark = pytest.mark.gpu
@@ -36,7 +36,7 @@ def check(shape, k, dtype, depth_chunk, seed):
     w = (torch.randn(shape[1], 1, k, k, k, generator=gen) / k**1.5).to(dtype)
     b = torch.randn(shape[1], generator=gen).to(dtype)
     dy = torch.randn(shape, generator=gen).to(dtype)
-    recipe = [ENGINE_VOLUME, VOLUME_SEG, depth_chunk]
+    recipe = [ENGINE_VOLUME, VOLUME_BAND, depth_chunk]
     xg, wg, bg, dyg = (t.to(DEV) for t in (x, w, b, dy))
     y = hip_ops.depthwise_forward(xg, wg, bg, recipe)
     y_nobias = hip_ops.depthwise_forward(xg, wg, None, recipe)
@@ -85,7 +85,7 @@ def test_volume_weight_grad_is_deterministic():
     gen = torch.Generator(device=DEV).manual_seed(3)
     x = torch.randn(2, 64, 16, 16, 16, generator=gen, device=DEV)
     dy = torch.randn(2, 64, 16, 16, 16, generator=gen, device=DEV)
-    recipe = [ENGINE_VOLUME, VOLUME_SEG, 4]
+    recipe = [ENGINE_VOLUME, VOLUME_BAND, 4]
     a = hip_ops.depthwise_weight_grad(x, dy, 5, recipe)
     b = hip_ops.depthwise_weight_grad(x, dy, 5, recipe)
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])

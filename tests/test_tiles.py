@@ -25,13 +25,13 @@ def test_depthwise_recipe_invariants(channels, size, k, dtype, phase):
         kind = "weight_grad" if phase == "weight_grad" else "stencil"
         target = tiles.MFMA_TARGET_WORKGROUPS[(kind, k)]
     elif engine == tiles.ENGINE_VOLUME:
-        assert tiles.volume_supported((size,) * 3) and tile_w == tiles.VOLUME_SEG
+        assert tiles.volume_supported((size,) * 3) and tile_w == tiles.VOLUME_BAND
         acc = 8 if dtype == "float64" else 4
         plan = tiles.volume_plan(1, channels, (size,) * 3, k, depth_chunk, acc_bytes=acc, wgrad=phase == "weight_grad")
         assert plan.lds_bytes <= tiles.LDS_LIMIT
         wgs = plan.workgroups
-        # Fill the chip unless the shortest D-run (one lane's planes) forbids it.
-        assert wgs >= tiles.VOLUME_TARGET_WORKGROUPS or depth_chunk == tiles.VOLUME_SEG
+        # Fill the chip unless the shortest D-run (the walk's k - 1 planes) forbids it.
+        assert wgs >= tiles.VOLUME_TARGET_WORKGROUPS or depth_chunk <= max(2, k - 1)
         return
     else:
         plan = tiles.depthwise_plan(1, channels, (size,) * 3, k, tile_w, depth_chunk)
@@ -84,7 +84,7 @@ def test_small_planes_use_the_volume_engine():
                     if phase not in tiles.VOLUME_PHASES:
                         assert engine == tiles.ENGINE_VALU
                         continue
-                    assert (engine, tile_w) == (tiles.ENGINE_VOLUME, tiles.VOLUME_SEG)
+                    assert (engine, tile_w) == (tiles.ENGINE_VOLUME, tiles.VOLUME_BAND)
                     acc = 8 if dtype == "float64" else 4
                     for wgrad in (False, True):
                         plan = tiles.volume_plan(1, channels, (size,) * 3, k, depth_chunk, acc_bytes=acc, wgrad=wgrad)
