@@ -436,6 +436,17 @@ int launch_finish(const Acc* part, void* dw, void* db, int64_t c, int splits, in
   return MEDNEXT_STATUS_OK;
 }
 
+// launch_finish for a dtype known only at run time (partials in its accumulation type).
+int finish_partials(int dtype, const void* part, void* dw, void* db, int64_t c, int splits, int k3, hipStream_t st) {
+  switch (dtype) {
+    case MEDNEXT_DTYPE_F32: return launch_finish<float, float>(static_cast<const float*>(part), dw, db, c, splits, k3, st);
+    case MEDNEXT_DTYPE_F64:
+      return launch_finish<double, double>(static_cast<const double*>(part), dw, db, c, splits, k3, st);
+    case MEDNEXT_DTYPE_F16: return launch_finish<f16_t, float>(static_cast<const float*>(part), dw, db, c, splits, k3, st);
+    default: return launch_finish<bf16_t, float>(static_cast<const float*>(part), dw, db, c, splits, k3, st);
+  }
+}
+
 // ------------------------------------------------------------------ host side
 
 struct Plan {
@@ -978,6 +989,8 @@ int s2_map_entry(const void* in, const void* w, const void* b, void* out, int64_
   if (int st = s2_plan(n, c, db, hb, wb, ds, hs, ws, k, dtype, GATHER ? kSmallDomain : kBigCellDomain, &g))
     return st;
   auto s = static_cast<hipStream_t>(stream);
+  if (GATHER && dw_s2band_chosen(n, c, db, hb, wb, ds, hs, ws, k, dtype))
+    return dw_s2band_gather(in, w, b, out, n, c, db, hb, wb, ds, hs, ws, k, dtype, s);
 #define MEDNEXT_S2_K(T)                                                          \
   switch (k) {                                                                   \
     case 1: return launch_s2_map_k<T, 1, GATHER>(in, w, b, out, g, s);           \
@@ -1097,20 +1110,7 @@ extern "C" int32_t mednext_depthwise3d_wgrad(const void* x, const void* grad_out
     MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
     int st = dw_volume_wgrad(x, grad_output, workspace, n, c, d, h, w, kernel_size, dtype, tile_w, depth_chunk, s);
     if (st != MEDNEXT_STATUS_OK) return st;
-    switch (dtype) {
-      case MEDNEXT_DTYPE_F32:
-        return launch_finish<float, float>(static_cast<const float*>(workspace), grad_weight, grad_bias, c, splits,
-                                           static_cast<int>(k3), s);
-      case MEDNEXT_DTYPE_F64:
-        return launch_finish<double, double>(static_cast<const double*>(workspace), grad_weight, grad_bias, c, splits,
-                                             static_cast<int>(k3), s);
-      case MEDNEXT_DTYPE_F16:
-        return launch_finish<f16_t, float>(static_cast<const float*>(workspace), grad_weight, grad_bias, c, splits,
-                                           static_cast<int>(k3), s);
-      default:
-        return launch_finish<bf16_t, float>(static_cast<const float*>(workspace), grad_weight, grad_bias, c, splits,
-                                            static_cast<int>(k3), s);
-    }
+    return finish_partials(dtype, workspace, grad_weight, grad_bias, c, splits, static_cast<int>(k3), s);
   }
   if (engine == MEDNEXT_ENGINE_MFMA) {
     MEDNEXT_CHECK_ARG(dtype == MEDNEXT_DTYPE_BF16, "the MFMA engine is bf16 only");
@@ -1244,9 +1244,13 @@ extern "C" size_t mednext_depthwise3d_s2_wgrad_workspace_bytes(int64_t n, int64_
                                                                int32_t kernel_size, int32_t dtype) {
   S2Dims g;
   if (s2_plan(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, kSmallDomain, &g) != MEDNEXT_STATUS_OK) return 0;
+  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
+  if (dw_s2band_chosen(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype)) {
+    const int64_t splits = dw_s2band_wgrad_splits(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype);
+    return static_cast<size_t>(c * splits * (k3 + 1) * acc_bytes_of(dtype));
+  }
   int bpc = 0;
   s2_wgrad_split(n, &g, &bpc);
-  const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
   return static_cast<size_t>(c * n * bpc * (k3 + 1) * acc_bytes_of(dtype));
 }
 
@@ -1265,6 +1269,13 @@ extern "C" int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* sma
       mednext_depthwise3d_s2_wgrad_workspace_bytes(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype);
   MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
   auto s = static_cast<hipStream_t>(stream);
+  if (dw_s2band_chosen(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype)) {
+    const int splits = dw_s2band_wgrad_splits(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype);
+    if (int st = dw_s2band_wgrad(big, small, workspace, n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, s))
+      return st;
+    return finish_partials(dtype, workspace, grad_weight, grad_bias, c, splits,
+                           kernel_size * kernel_size * kernel_size, s);
+  }
 #define MEDNEXT_S2W_K(T)                                                                            \
   switch (kernel_size) {                                                                            \
     case 1: return launch_s2_wgrad_k<T, 1>(big, small, grad_weight, grad_bias, workspace, g, n, bpc, s); \

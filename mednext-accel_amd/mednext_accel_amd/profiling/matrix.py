@@ -90,8 +90,17 @@ def _depthwise_candidates(batch: int, channels: int, s: int, k: int, dtype: str,
             if tw <= max(32, s) and tw != tile_w:
                 add(engine, tw, depth_chunk)
     for dc in (depth_chunk // 2, depth_chunk * 2):
-        if dc >= 1:
-            add(engine, tile_w, dc)
+        if dc < 1:
+            continue
+        if engine == tiles.ENGINE_VOLUME:
+            acc = 8 if dtype == "float64" else 4
+            plan = tiles.volume_plan(batch, channels, (s, s, s), k, dc, acc_bytes=acc, wgrad=phase == "weight_grad")
+            if plan.lds_bytes > tiles.LDS_LIMIT:
+                continue
+        add(engine, tile_w, dc)
+    if engine == tiles.ENGINE_VOLUME:
+        # The VALU stencil the volume kernels replace, measured beside them.
+        add(*tiles.valu_recipe(batch, channels, (s, s, s), k))
     return out
 
 

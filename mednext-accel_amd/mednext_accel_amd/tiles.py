@@ -262,6 +262,13 @@ def depthwise_recipe(
     if volume_supported(spatial) and phase in VOLUME_PHASES:
         acc_bytes = 8 if dtype == "float64" else 4
         return [ENGINE_VOLUME, VOLUME_BAND, volume_depth_chunk(batch, channels, spatial, kernel_size, acc_bytes)]
+    return valu_recipe(batch, channels, spatial, kernel_size)
+
+
+def valu_recipe(batch: int, channels: int, spatial: tuple[int, int, int], kernel_size: int) -> list[int]:
+    """The VALU stencil's ``[engine, tile_w, depth_chunk]``: the widest tile the
+    plane allows (up to 64 columns) and a D-run that yields TARGET_WORKGROUPS."""
+    d, _h, w = spatial
     tile_w = 4
     while tile_w < 64 and tile_w < w:
         tile_w *= 2

@@ -2,7 +2,8 @@
 
 Raw maps (gather / scatter / weight-grad) against the float64 oracle on the
 same dtype-rounded inputs, for every dtype, k in {1, 3, 5}, odd and even sizes
-and batch 2; the two autograd ops against PyTorch's F.conv3d /
+and batch 2, through both the band kernels and (rows too wide for them) the
+row-task kernels; the two autograd ops against PyTorch's F.conv3d /
 F.conv_transpose3d at MedNeXt down / up shapes. Tolerances: fp64 1e-12; fp32
 1e-5 outputs / input grads, 1e-4 weight grads; bf16 / fp16 2e-2.
 """
@@ -63,6 +64,30 @@ def test_maps_against_oracle(k, dtype, big):
     assert max_rel(dw, want_dw) <= w_tol
     assert max_rel(ds, want_db) <= w_tol
     assert y.dtype == dx.dtype == dw.dtype == ds.dtype == dtype
+
+
+@pytest.mark.parametrize("k", [3, 5])
+@pytest.mark.parametrize(
+    "n,c,big",
+    [
+        (1, 1000, (8, 40, 32)),  # band kernels: 5 bands per small plane, 2 per reduce workgroup (last group ragged)
+        (2, 2, (3, 3, 2000)),  # rows too wide for the staged LDS block: the row-task kernels
+    ],
+)
+def test_maps_band_and_row_paths(n, c, big, k):
+    print(f"[s2 maps paths] n={n} c={c} big={big} k={k}", flush=True)
+    gen = torch.Generator().manual_seed(c + k + sum(big))
+    dtype = torch.float32
+    small = tuple((s - 1) // 2 + 1 for s in big)
+    x = rounded((n, c, *big), gen, dtype)
+    w = rounded((c, 1, k, k, k), gen, dtype, 1.0 / k)
+    b = rounded((c,), gen, dtype)
+    g = rounded((n, c, *small), gen, dtype)
+    y = hip_ops.depthwise_s2_gather(x.to(DEV), w.to(DEV), b.to(DEV), small)
+    assert max_rel(y, odw.strided_forward(f64(x), f64(w), f64(b))) <= FP32_OUT
+    dw, ds = hip_ops.depthwise_s2_wgrad(x.to(DEV), g.to(DEV), k)
+    want_dw, want_db = odw.strided_weight_grad(f64(x), f64(g), k)
+    assert max_rel(dw, want_dw) <= FP32_WGRAD and max_rel(ds, want_db) <= FP32_WGRAD
 
 
 DOWN_UP = [(32, 128, 3), (64, 64, 3), (128, 32, 3), (64, 64, 5)]
