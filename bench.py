@@ -440,9 +440,9 @@ def _emit(record: dict) -> None:
 def sweep(args, torch, hip_ops, lead: GpuLead) -> None:
     """configs[1] stage sweep (depthwise k3/k5 fwd, dX, dW at every MedNeXt
     stage shape, N=1, bf16) plus the other kernels of the training step at the
-    same shapes: stride-2 gather / scatter / reduce, GroupNorm forward and
-    backward, and the four pointwise GEMMs of a fused MedNeXt-Base block
-    expansion. One JSON line per kernel phase: mean microseconds per launch
+    same shapes: stride-2 gather / scatter / reduce (k3 and k5), GroupNorm
+    forward and backward, and the six pointwise GEMMs of a fused MedNeXt-Base
+    block expansion in the form the training step runs at that width. One JSON line per kernel phase: mean microseconds per launch
     (events around ``reps`` back-to-back launches, the GPU kept ahead of the
     host), algorithmic bytes, GB/s and, for the GEMMs, TFLOP/s."""
     dev = torch.device("cuda:0")
@@ -509,17 +509,20 @@ def sweep(args, torch, hip_ops, lead: GpuLead) -> None:
             us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_weight_grad(xs[i], dys[i], k), nsets, reps)
             record(f"depthwise_k{k}_weight_grad", shape, us, 4 * e)
         if s >= 16:
-            # Stride-2 maps of the down block entering the next stage (C -> C at S -> S/2), k3.
+            # Stride-2 maps of the down block entering the next stage (C -> C at S -> S/2), k3 and k5.
             small = hip_ops.strided_spatial((s, s, s))
             es = c * small[0] * small[1] * small[2]
-            w3 = randn(c, 1, 3, 3, 3) * 0.2
             smalls = [randn(1, c, *small) for _ in range(nsets)]
-            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_gather(xs[i], w3, None, small), nsets, reps)
-            record("depthwise_s2_k3_gather", shape, us, 2 * (e + es))
-            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_scatter(smalls[i], w3, None, (s, s, s)), nsets, reps)
-            record("depthwise_s2_k3_scatter", shape, us, 2 * (e + es))
-            us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_wgrad(xs[i], smalls[i], 3), nsets, reps)
-            record("depthwise_s2_k3_wgrad", shape, us, 2 * (e + es))
+            for k2 in (3, 5):
+                wk = randn(c, 1, k2, k2, k2) * (0.6 / k2**1.5)
+                us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_gather(xs[i], wk, None, small), nsets,
+                                     reps)
+                record(f"depthwise_s2_k{k2}_gather", shape, us, 2 * (e + es))
+                us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_scatter(smalls[i], wk, None, (s, s, s)),
+                                     nsets, reps)
+                record(f"depthwise_s2_k{k2}_scatter", shape, us, 2 * (e + es))
+                us = _timed_launches(torch, lead, lambda i: hip_ops.depthwise_s2_wgrad(xs[i], smalls[i], k2), nsets, reps)
+                record(f"depthwise_s2_k{k2}_wgrad", shape, us, 2 * (e + es))
             del smalls
         gamma = torch.ones(c, device=dev)
         beta = torch.zeros(c, device=dev)
@@ -554,19 +557,46 @@ def sweep(args, torch, hip_ops, lead: GpuLead) -> None:
         v = s**3
         fl = 2 * m * c * v
         P = hip_ops
-        us = _timed_launches(torch, lead, lambda i: P.pointwise_conv(xs[i % nh], w1, b1), nh, reps)
-        record("pointwise_expand_fwd", f"{shape} {c}->{m}", us, 2 * v * (c + m), fl)
-        us = _timed_launches(
-            torch, lead,
-            lambda i: P.pointwise_conv(hs[i], w2, b2, aux=xs[i], prologue=P.PW_PROLOGUE_GELU, epilogue=P.PW_EPILOGUE_BIAS_RESIDUAL),
-            nh, reps)
-        record("pointwise_project_fwd_gelu_residual", f"{shape} {m}->{c}", us, 2 * v * (m + 2 * c), fl)
-        us = _timed_launches(
-            torch, lead,
-            lambda i: P.pointwise_conv(dys[i], w2, aux=hs[i], epilogue=P.PW_EPILOGUE_GELU_GRAD, transpose=True), nh, reps)
-        record("pointwise_project_dgrad_gelu_grad", f"{shape} {c}->{m}", us, 2 * v * (c + 2 * m), fl)
-        us = _timed_launches(torch, lead, lambda i: P.pointwise_weight_grad(dys[i], hs[i], prologue=P.PW_PROLOGUE_GELU), nh, reps)
-        record("pointwise_project_wgrad_gelu", f"{shape} {m}x{c}", us, 2 * v * (m + c), fl)
+        from mednext_accel_amd.adaptive import AdaptiveExpansion
+
+        if m >= AdaptiveExpansion.stored_gelu_from:
+            # The fused expansion's stored-GELU form (what the training step
+            # runs at this width): expand writes GELU and GELU', project reads
+            # GELU as is, its input gradient scales by the stored GELU'.
+            gs = [randn(1, m, s, s, s) for _ in range(nh)]
+            us = _timed_launches(
+                torch, lead, lambda i: P.pointwise_conv(xs[i % nh], w1, b1, epilogue=P.PW_EPILOGUE_BIAS_GELU_PAIR),
+                nh, reps)
+            record("pointwise_expand_fwd_gelu_pair", f"{shape} {c}->{m}", us, 2 * v * (c + 2 * m), fl)
+            us = _timed_launches(
+                torch, lead, lambda i: P.pointwise_conv(hs[i], w2, b2, aux=xs[i], epilogue=P.PW_EPILOGUE_BIAS_RESIDUAL),
+                nh, reps)
+            record("pointwise_project_fwd_residual", f"{shape} {m}->{c}", us, 2 * v * (m + 2 * c), fl)
+            us = _timed_launches(
+                torch, lead,
+                lambda i: P.pointwise_conv(dys[i], w2, aux=gs[i], epilogue=P.PW_EPILOGUE_AUX_SCALE, transpose=True),
+                nh, reps)
+            record("pointwise_project_dgrad_aux_scale", f"{shape} {c}->{m}", us, 2 * v * (c + 2 * m), fl)
+            us = _timed_launches(torch, lead, lambda i: P.pointwise_weight_grad(dys[i], hs[i]), nh, reps)
+            record("pointwise_project_wgrad", f"{shape} {m}x{c}", us, 2 * v * (m + c), fl)
+            del gs
+        else:
+            us = _timed_launches(torch, lead, lambda i: P.pointwise_conv(xs[i % nh], w1, b1), nh, reps)
+            record("pointwise_expand_fwd", f"{shape} {c}->{m}", us, 2 * v * (c + m), fl)
+            us = _timed_launches(
+                torch, lead,
+                lambda i: P.pointwise_conv(hs[i], w2, b2, aux=xs[i], prologue=P.PW_PROLOGUE_GELU,
+                                           epilogue=P.PW_EPILOGUE_BIAS_RESIDUAL),
+                nh, reps)
+            record("pointwise_project_fwd_gelu_residual", f"{shape} {m}->{c}", us, 2 * v * (m + 2 * c), fl)
+            us = _timed_launches(
+                torch, lead,
+                lambda i: P.pointwise_conv(dys[i], w2, aux=hs[i], epilogue=P.PW_EPILOGUE_GELU_GRAD, transpose=True),
+                nh, reps)
+            record("pointwise_project_dgrad_gelu_grad", f"{shape} {c}->{m}", us, 2 * v * (c + 2 * m), fl)
+            us = _timed_launches(
+                torch, lead, lambda i: P.pointwise_weight_grad(dys[i], hs[i], prologue=P.PW_PROLOGUE_GELU), nh, reps)
+            record("pointwise_project_wgrad_gelu", f"{shape} {m}x{c}", us, 2 * v * (m + c), fl)
         us = _timed_launches(torch, lead, lambda i: P.pointwise_weight_grad(hs[i], xs[i]), nh, reps)
         record("pointwise_expand_wgrad", f"{shape} {m}x{c}", us, 2 * v * (m + c), fl)
         us = _timed_launches(torch, lead, lambda i: P.pointwise_conv(hs[i], w1, transpose=True), nh, reps)

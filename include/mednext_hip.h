@@ -275,13 +275,33 @@ int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* 
                                  void* row_partial, int32_t dtype, int32_t blocks_per_sample,
                                  void* stream);
 
+/* mednext_pointwise_fwd_ex with a caller workspace (16-byte aligned) for the
+ * tiled product's K split: where the tiled grid alone would leave the chip
+ * short of 256 workgroups, K is split over workgroups that write fp32 tile
+ * partials to the workspace, and a second kernel adds them in a fixed order
+ * and applies the epilogue. With a NULL or too small workspace it behaves as
+ * mednext_pointwise_fwd_ex. No counterpart in the reference (its GEMMs are
+ * library calls). */
+int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, const void* bias, const void* aux,
+                                 const void* aux2, void* y, void* y2, int64_t n, int64_t k, int64_t m,
+                                 int64_t v, int32_t weight_layout, int32_t prologue, int32_t epilogue,
+                                 const void* prologue_coef, const void* epilogue_coef,
+                                 void* row_partial, int32_t dtype, int32_t blocks_per_sample,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace bytes mednext_pointwise_fwd_ws uses for this shape and mode under
+ * the current kernel choice (0: no K split). */
+size_t mednext_pointwise_fwd_workspace_bytes(int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
+                                             int32_t epilogue);
+
 /* Kernel family for mednext_pointwise_fwd(_ex). The streaming kernels keep X
  * out of LDS and read it once per group of 16-64 output rows; the tiled
  * kernel stages X and the weight through LDS for 64 or 128 output rows at a
  * time (K % 32 == 0, M % 16 == 0, no GELU prologue, no ROW_REDUCE, and
  * blocks_per_sample == 0). AUTO takes the tiled kernel for K >= 256 where
  * the streaming plan would read X twice or more and the tiled grid has at
- * least 256 workgroups; TILED takes it wherever it applies; STREAMING never. The tiled
+ * least 256 workgroups, and (given the workspace of mednext_pointwise_fwd_ws)
+ * for K >= 256 with a smaller grid, K split over workgroups; TILED takes it
+ * wherever it applies; STREAMING never. The tiled
  * kernel applies the AFFINE prologue to X (bf16(x s + t) per element). The
  * same choice governs the weight gradient's tile: AUTO uses 128 x 128
  * workgroup tiles when M >= 128, K >= 128 and the grid keeps at least 256

@@ -55,6 +55,8 @@ struct PwGeom {
   int mgroups;  // ceil(M / (16 * MT))
   int wgs;      // workgroups per (sample, row group)
   int wt;       // 1: weight stored [K][M] (A = W^T), 0: [M][K]
+  int ksplit;   // tiled product: K ranges over workgroups (1: whole K, epilogue in the kernel)
+  int kslices;  // tiled product: 32-channel slices per K range
 };
 
 __device__ inline uint32_t gelu_word(uint32_t w) {
@@ -81,6 +83,7 @@ struct PwExtra {
   const bf16_t* aux2;   // AFFINE_SCALE: second per-element operand, shaped like y
   bf16_t* y2;           // BIAS_GELU_PAIR: second output, shaped like y
   int slots;
+  float* kpart;         // tiled K-split: [ksplit][N][M][V rounded up to 8] fp32 partial products
 };
 
 constexpr bool epi_has_bias(int epi) {
@@ -744,6 +747,12 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
 // prologue is applied to X (bf16(x s + t) per channel, coefficients staged in
 // LDS), so no per-launch weight folding is needed. Requirements (checked by
 // the host): K % 32 == 0, M % 16 == 0, no ROW_REDUCE epilogue.
+//
+// K split over workgroups (g.ksplit > 1, the deep products whose tiles alone
+// leave the chip short of workgroups): workgroup (tile, r) multiplies only the
+// slices [r * kslices, (r + 1) * kslices) and stores its fp32 tile to
+// ex.kpart; pw_ksplit_epilogue_kernel then adds the K ranges in range order
+// (deterministic) and applies the epilogue.
 constexpr int kTileSlices = 2;
 
 template <int MT, int PRO, int EPI>
@@ -764,16 +773,21 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
   constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_AFFINE;
   extern __shared__ __align__(16) uint16_t pw_lds[];
   uint4* const stages = reinterpret_cast<uint4*>(pw_lds);
-  // LDS holds only the slices used: min(2, ks) per stage, and a second stage
-  // only when K takes more than one step.
-  const int sps = min(kTileSlices, g.ks);
-  const int nstages = g.ks > kTileSlices ? 2 : 1;
+  // This workgroup's K range: slices [kbase, kbase + nks).
+  int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int ksp = static_cast<int>(lin % g.ksplit);
+  lin /= g.ksplit;
+  const int kbase = ksp * g.kslices;
+  const int nks = min(g.kslices, g.ks - kbase);
+  // LDS holds only the slices used: min(2, nks) per stage, and a second stage
+  // only when the range takes more than one step.
+  const int sps = min(kTileSlices, nks);
+  const int nstages = nks > kTileSlices ? 2 : 1;
   float* const bias_lds = reinterpret_cast<float*>(stages + nstages * sps * SLICE);
   float* const c0_lds = bias_lds + BM;
   float* const c1_lds = c0_lds + BM;
   float* const kcoef = c1_lds + BM;  // AFFINE: (s, t) per input channel
 
-  const int64_t lin = xcd_swizzle(blockIdx.x, gridDim.x);
   const int mg = static_cast<int>(lin % g.mgroups);
   const int64_t rest = lin / g.mgroups;
   const int chunk = static_cast<int>(rest % g.chunks);
@@ -781,6 +795,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
   const int m0 = mg * BM;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n_col = lane & 15, q = lane >> 4;
+  const bool split = g.ksplit > 1;
 
   for (int r = threadIdx.x; r < BM; r += kPwThreads) {
     const int m = m0 + r;
@@ -813,7 +828,8 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
   const int oct = lane >> 2, oq = lane & 3;
 
   uint4 rg[8];  // the loads of one slice (X rows or weight fragments)
-  auto load_slice = [&](int slice) {
+  auto load_slice = [&](int local) {
+    const int slice = kbase + local;
     if (loads_x) {
       const uint32_t row0 = 32u * slice + 8u * q;
 #pragma unroll
@@ -838,7 +854,8 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
       }
     }
   };
-  auto store_slice = [&](int slice, uint4* stage) {
+  auto store_slice = [&](int local, uint4* stage) {
+    const int slice = kbase + local;
     if (loads_x) {
       uint4 cur[8];
       if constexpr (kAffine) {
@@ -890,24 +907,25 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
     for (int r = 0; r < 4; ++r) {
       av[mt][r] = av2[mt][r] = make_uint4(0u, 0u, 0u, 0u);
       const uint32_t off = (static_cast<uint32_t>(m0 + 16 * MT * wave + 16 * mt + 4 * q + r) * V + vl) * 2u;
-      if constexpr (kAux) av[mt][r] = load_group(ar, off, live ? nv : 0u);
-      if constexpr (kAux2) av2[mt][r] = load_group(a2r, off, live ? nv : 0u);
+      const uint32_t nload = live && !split ? nv : 0u;  // K-split: the epilogue kernel reads them
+      if constexpr (kAux) av[mt][r] = load_group(ar, off, nload);
+      if constexpr (kAux2) av2[mt][r] = load_group(a2r, off, nload);
     }
   }
-  const int steps = (g.ks + kTileSlices - 1) / kTileSlices;
+  const int steps = (nks + kTileSlices - 1) / kTileSlices;
   const int my_slice = loads_x ? wave : wslot;
-  if (my_slice < g.ks) load_slice(my_slice);
+  if (my_slice < nks) load_slice(my_slice);
   __syncthreads();  // row vectors and AFFINE coefficients
   for (int s = 0; s < steps; ++s) {
     uint4* const stage = stages + (s & 1) * sps * SLICE;
     const int slice = kTileSlices * s + my_slice;
-    if (slice < g.ks) store_slice(slice, stage);
-    if (slice + kTileSlices < g.ks) load_slice(slice + kTileSlices);
+    if (slice < nks) store_slice(slice, stage);
+    if (slice + kTileSlices < nks) load_slice(slice + kTileSlices);
     __syncthreads();
     if (rows_live) {
 #pragma unroll
       for (int sl = 0; sl < kTileSlices; ++sl) {
-        if (kTileSlices * s + sl < g.ks) {
+        if (kTileSlices * s + sl < nks) {
           const uint4* xs = stage + sl * SLICE + lane;
           const uint4* ws = stage + sl * SLICE + XS + (MT * wave) * 64 + lane;
           uint4 a[MT];
@@ -924,6 +942,24 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
     }
   }
   if (!rows_live) return;
+
+  if (split) {
+    // fp32 tile of this K range: kpart[n][ksp][m][8 * ceil(V / 8)], 8 voxels per row and lane.
+    const int64_t vp = static_cast<int64_t>((V + 7u) & ~7u);
+    float* __restrict__ part = ex.kpart + (n * g.ksplit + ksp) * g.M * vp;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (m0 + 16 * MT * wave + 16 * mt >= g.M || nv == 0u) continue;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = m0 + 16 * MT * wave + 16 * mt + 4 * q + r;
+        float4* dst = reinterpret_cast<float4*>(part + m * vp + vl);
+        dst[0] = make_float4(acc[mt][0][r], acc[mt][1][r], acc[mt][2][r], acc[mt][3][r]);
+        dst[1] = make_float4(acc[mt][4][r], acc[mt][5][r], acc[mt][6][r], acc[mt][7][r]);
+      }
+    }
+    return;
+  }
 
   const __amdgpu_buffer_rsrc_t yr = slab_rsrc(y + yoff, g.M * V * 2u);
   const __amdgpu_buffer_rsrc_t y2r = slab_rsrc(ex.y2 != nullptr ? ex.y2 + yoff : y, ex.y2 != nullptr ? g.M * V * 2u : 0u);
@@ -942,6 +978,51 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
       store_group(yr, off, nv, pack8(v));
       if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR) store_group(y2r, off, nv, pack8(v2));
     }
+  }
+}
+
+// Epilogue of the K-split tiled product: per thread one row's 8 consecutive
+// voxels, the K ranges' fp32 partials added in range order, then the same
+// value epilogue as the fused kernels (bias, GELU, residual, GELU', scales).
+template <int EPI>
+__global__ __launch_bounds__(kPwThreads) void pw_ksplit_epilogue_kernel(const bf16_t* __restrict__ bias,
+                                                                        const bf16_t* __restrict__ aux,
+                                                                        bf16_t* __restrict__ y, PwGeom g,
+                                                                        PwExtra ex, int64_t n_samples) {
+  const uint32_t V = g.V;
+  const uint32_t groups = (V + 7u) / 8u;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kPwThreads + threadIdx.x;
+  if (t >= n_samples * g.M * groups) return;
+  const int64_t row = t / groups;  // n * M + m
+  const uint32_t gi = static_cast<uint32_t>(t - row * groups);
+  const int64_t n = row / g.M;
+  const int m = static_cast<int>(row - n * g.M);
+  const int64_t vp = static_cast<int64_t>(groups) * 8;
+  const float* __restrict__ p = ex.kpart + ((n * g.ksplit) * g.M + m) * vp + 8 * gi;
+  float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, v2[8];
+  for (int r = 0; r < g.ksplit; ++r) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w;
+    v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+    p += g.M * vp;
+  }
+  const uint32_t vl = 8u * gi;
+  const uint32_t nv = min(8u, V - vl);
+  const int64_t yoff = n * g.M * static_cast<int64_t>(V);
+  const uint32_t off = (static_cast<uint32_t>(m) * V + vl) * 2u;
+  uint4 av = make_uint4(0u, 0u, 0u, 0u), av2 = av;
+  if constexpr (epi_has_aux(EPI)) av = load_group(slab_rsrc(aux + yoff, g.M * V * 2u), off, nv);
+  float c0 = 0.f, c1 = 0.f;
+  if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) {
+    av2 = load_group(slab_rsrc(ex.aux2 + yoff, g.M * V * 2u), off, nv);
+    c0 = static_cast<float>(ex.ecoef[row * 2]);
+    c1 = static_cast<float>(ex.ecoef[row * 2 + 1]);
+  }
+  const float b = (epi_has_bias(EPI) && bias != nullptr) ? bf16_to_f32(bias[m].bits) : 0.f;
+  epilogue_values<EPI>(v, v2, av, av2, b, c0, c1);
+  store_group(slab_rsrc(y + yoff, g.M * V * 2u), off, nv, pack8(v));
+  if constexpr (EPI == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR) {
+    store_group(slab_rsrc(ex.y2 + yoff, g.M * V * 2u), off, nv, pack8(v2));
   }
 }
 
@@ -1519,6 +1600,8 @@ FwdPlan plan_fwd(int64_t n, int64_t k, int64_t m, int64_t v, int epi, int32_t bl
   g.chunks = static_cast<int>(cdiv(v, kChunk));
   g.mgroups = static_cast<int>(cdiv(m, 16 * p.mt));
   g.wt = 0;
+  g.ksplit = 1;
+  g.kslices = g.ks;
   p.splitk = g.ks >= kSplitKSlices;
   const int64_t groups = n * g.mgroups;
   // Every wave (split-K: every workgroup) gets at least one chunk.
@@ -1556,10 +1639,63 @@ bool tiled_pays(const FwdPlan& p, int64_t n, int64_t m, int64_t v) {
   return p.splitk && p.g.mgroups >= kTiledMinRereads && tiled_blocks(n, m, v, tiled_mt(n, m, v)) >= kTiledMinBlocks;
 }
 
-int32_t launch_tiled(const void* x, const void* weight, const void* bias, const void* aux, void* y, const PwExtra& ex,
+// The tiled product's launch: row-group height and, for grids short of
+// kTiledMinBlocks workgroups, the K ranges that bring them to twice that
+// (each range at least one two-slice step).
+struct TiledPlan {
+  bool tiled;
+  int mt;
+  int ksplit, kslices;
+  size_t kpart_bytes;  // fp32 partials of the K-split (0 without one)
+};
+
+TiledPlan plan_tiled(int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue, int32_t epilogue, bool allow_split) {
+  TiledPlan t{false, 1, 1, static_cast<int>(k / 32), 0};
+  if (n < 1 || k < 1 || k > kMaxK || m < 1 || v < 1 || !pro_epi_supported(prologue, epilogue)) return t;
+  const int choice = g_product_kernels.load(std::memory_order_relaxed);
+  if (choice == MEDNEXT_PW_KERNELS_STREAMING || !tiled_eligible(k, m, prologue, epilogue)) return t;
+  t.mt = choice == MEDNEXT_PW_KERNELS_TILED_64 ? 1 : tiled_mt(n, m, v);
+  const FwdPlan p = plan_fwd(n, k, m, v, epilogue, 0);
+  const int64_t blocks = tiled_blocks(n, m, v, t.mt);
+  const int ks = static_cast<int>(k / 32);
+  int split = 1;
+  if (allow_split && blocks < kTiledMinBlocks && ks >= 2 * kTileSlices) {
+    split = static_cast<int>(std::min<int64_t>(cdiv(2 * kTiledMinBlocks, blocks), ks / kTileSlices));
+  }
+  t.kslices = static_cast<int>(cdiv(ks, split));
+  t.ksplit = static_cast<int>(cdiv(ks, t.kslices));
+  if (choice == MEDNEXT_PW_KERNELS_TILED || choice == MEDNEXT_PW_KERNELS_TILED_64) {
+    t.tiled = true;
+  } else {
+    t.tiled = tiled_pays(p, n, m, v) || (p.splitk && t.ksplit > 1);
+  }
+  if (!t.tiled || t.ksplit == 1) {
+    t.ksplit = 1;
+    t.kslices = ks;
+  } else {
+    t.kpart_bytes = static_cast<size_t>(n) * t.ksplit * m * (cdiv(v, 8) * 8) * sizeof(float);
+  }
+  return t;
+}
+
+using KsplitEpilogue = void (*)(const bf16_t*, const bf16_t*, bf16_t*, PwGeom, PwExtra, int64_t);
+
+KsplitEpilogue ksplit_epilogue(int epi) {
+  switch (epi) {
+    case MEDNEXT_PW_EPILOGUE_BIAS: return pw_ksplit_epilogue_kernel<MEDNEXT_PW_EPILOGUE_BIAS>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_ksplit_epilogue_kernel<MEDNEXT_PW_EPILOGUE_BIAS_GELU>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_ksplit_epilogue_kernel<MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL>;
+    case MEDNEXT_PW_EPILOGUE_GELU_GRAD: return pw_ksplit_epilogue_kernel<MEDNEXT_PW_EPILOGUE_GELU_GRAD>;
+    case MEDNEXT_PW_EPILOGUE_AFFINE_SCALE: return pw_ksplit_epilogue_kernel<MEDNEXT_PW_EPILOGUE_AFFINE_SCALE>;
+    case MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR: return pw_ksplit_epilogue_kernel<MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR>;
+    default: return pw_ksplit_epilogue_kernel<MEDNEXT_PW_EPILOGUE_AUX_SCALE>;
+  }
+}
+
+int32_t launch_tiled(const void* x, const void* weight, const void* bias, const void* aux, void* y, PwExtra ex,
                      int64_t n, int64_t k, int64_t m, int64_t v, int32_t weight_layout, int32_t prologue,
-                     int32_t epilogue, void* stream) {
-  const int mt = g_product_kernels.load(std::memory_order_relaxed) == MEDNEXT_PW_KERNELS_TILED_64 ? 1 : tiled_mt(n, m, v);
+                     int32_t epilogue, const TiledPlan& t, void* workspace, void* stream) {
+  const int mt = t.mt;
   PwGeom g{};
   g.K = static_cast<int>(k);
   g.M = static_cast<int>(m);
@@ -1569,18 +1705,29 @@ int32_t launch_tiled(const void* x, const void* weight, const void* bias, const 
   g.mgroups = static_cast<int>(cdiv(m, 64 * mt));
   g.wgs = 1;
   g.wt = weight_layout;
-  const int64_t blocks = n * g.mgroups * g.chunks;
+  g.ksplit = t.ksplit;
+  g.kslices = t.kslices;
+  ex.kpart = static_cast<float*>(workspace);
+  const int64_t blocks = n * g.mgroups * g.chunks * g.ksplit;
   MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
-  const int64_t sps = std::min<int64_t>(kTileSlices, g.ks);
-  const int64_t nstages = g.ks > kTileSlices ? 2 : 1;
+  const int64_t sps = std::min<int64_t>(kTileSlices, g.kslices);
+  const int64_t nstages = g.kslices > kTileSlices ? 2 : 1;
   const size_t slice = static_cast<size_t>(8 * 64 + 4 * mt * 64) * 16;
   const size_t lds = static_cast<size_t>(nstages * sps) * slice + 3 * 64 * mt * sizeof(float) +
                      (prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? 2 * static_cast<size_t>(k) * sizeof(float) : 0);
   FwdKernel fn = mt == 1 ? tiled_instance<1>(prologue, epilogue) : tiled_instance<2>(prologue, epilogue);
-  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds, static_cast<hipStream_t>(stream),
+  const auto st = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds, st,
                      static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(weight),
                      static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(aux), static_cast<bf16_t*>(y), g, ex);
   MEDNEXT_CHECK_LAUNCH();
+  if (g.ksplit > 1) {
+    const int64_t threads = n * m * cdiv(v, 8);
+    hipLaunchKernelGGL(ksplit_epilogue(epilogue), dim3(static_cast<unsigned>(cdiv(threads, kPwThreads))),
+                       dim3(kPwThreads), 0, st, static_cast<const bf16_t*>(bias), static_cast<const bf16_t*>(aux),
+                       static_cast<bf16_t*>(y), g, ex, n);
+    MEDNEXT_CHECK_LAUNCH();
+  }
   return MEDNEXT_STATUS_OK;
 }
 
@@ -1595,11 +1742,12 @@ extern "C" int32_t mednext_pointwise_set_kernels(int32_t choice) {
 
 extern "C" int32_t mednext_pointwise_uses_tiled(int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
                                                 int32_t epilogue) {
-  if (n < 1 || k < 1 || k > kMaxK || m < 1 || v < 1 || !pro_epi_supported(prologue, epilogue)) return 0;
-  const int choice = g_product_kernels.load(std::memory_order_relaxed);
-  if (choice == MEDNEXT_PW_KERNELS_STREAMING || !tiled_eligible(k, m, prologue, epilogue)) return 0;
-  if (choice == MEDNEXT_PW_KERNELS_TILED || choice == MEDNEXT_PW_KERNELS_TILED_64) return 1;
-  return tiled_pays(plan_fwd(n, k, m, v, epilogue, 0), n, m, v) ? 1 : 0;
+  return plan_tiled(n, k, m, v, prologue, epilogue, false).tiled ? 1 : 0;
+}
+
+extern "C" size_t mednext_pointwise_fwd_workspace_bytes(int64_t n, int64_t k, int64_t m, int64_t v,
+                                                        int32_t prologue, int32_t epilogue) {
+  return plan_tiled(n, k, m, v, prologue, epilogue, true).kpart_bytes;
 }
 
 extern "C" int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, int64_t v,
@@ -1608,12 +1756,12 @@ extern "C" int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, 
   return plan_fwd(n, k, m, v, MEDNEXT_PW_EPILOGUE_ROW_REDUCE, blocks_per_sample).slots;
 }
 
-extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* bias, const void* aux,
+extern "C" int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, const void* bias, const void* aux,
                                             const void* aux2, void* y, void* y2, int64_t n, int64_t k, int64_t m,
                                             int64_t v, int32_t weight_layout, int32_t prologue, int32_t epilogue,
                                             const void* prologue_coef, const void* epilogue_coef,
                                             void* row_partial, int32_t dtype, int32_t blocks_per_sample,
-                                            void* stream) {
+                                            void* workspace, size_t workspace_bytes, void* stream) {
   if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
   const bool reduce = epilogue == MEDNEXT_PW_EPILOGUE_ROW_REDUCE;
   MEDNEXT_CHECK_ARG(x != nullptr && weight != nullptr && (y != nullptr || reduce), "null tensor pointer");
@@ -1638,9 +1786,16 @@ extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, c
                     "pointwise tensors must be bf16-aligned and the weight 16-byte aligned");
   MEDNEXT_CHECK_ARG(blocks_per_sample >= 0, "blocks_per_sample must be >= 0 (0 = automatic)");
   PwExtra ex{static_cast<const double*>(prologue_coef), static_cast<const double*>(epilogue_coef),
-             static_cast<double*>(row_partial), static_cast<const bf16_t*>(aux2), static_cast<bf16_t*>(y2), 0};
-  if (blocks_per_sample == 0 && mednext_pointwise_uses_tiled(n, k, m, v, prologue, epilogue)) {
-    return launch_tiled(x, weight, bias, aux, y, ex, n, k, m, v, weight_layout, prologue, epilogue, stream);
+             static_cast<double*>(row_partial), static_cast<const bf16_t*>(aux2), static_cast<bf16_t*>(y2), 0,
+             nullptr};
+  if (blocks_per_sample == 0) {
+    // The K-split tiled product when the caller's workspace holds its partials.
+    TiledPlan t = plan_tiled(n, k, m, v, prologue, epilogue, true);
+    if (t.ksplit > 1 && (workspace == nullptr || workspace_bytes < t.kpart_bytes || !aligned(workspace, 16)))
+      t = plan_tiled(n, k, m, v, prologue, epilogue, false);
+    if (t.tiled)
+      return launch_tiled(x, weight, bias, aux, y, ex, n, k, m, v, weight_layout, prologue, epilogue, t, workspace,
+                          stream);
   }
   FwdPlan p = plan_fwd(n, k, m, v, epilogue, blocks_per_sample);
   p.g.wt = weight_layout;
@@ -1655,6 +1810,17 @@ extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, c
                      static_cast<const bf16_t*>(aux), static_cast<bf16_t*>(y), p.g, ex);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
+}
+
+extern "C" int32_t mednext_pointwise_fwd_ex(const void* x, const void* weight, const void* bias, const void* aux,
+                                            const void* aux2, void* y, void* y2, int64_t n, int64_t k, int64_t m,
+                                            int64_t v, int32_t weight_layout, int32_t prologue, int32_t epilogue,
+                                            const void* prologue_coef, const void* epilogue_coef,
+                                            void* row_partial, int32_t dtype, int32_t blocks_per_sample,
+                                            void* stream) {
+  return mednext_pointwise_fwd_ws(x, weight, bias, aux, aux2, y, y2, n, k, m, v, weight_layout, prologue, epilogue,
+                                  prologue_coef, epilogue_coef, row_partial, dtype, blocks_per_sample, nullptr, 0,
+                                  stream);
 }
 
 extern "C" int32_t mednext_pointwise_fwd(const void* x, const void* weight, const void* bias, const void* aux,

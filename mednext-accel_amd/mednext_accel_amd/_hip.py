@@ -72,6 +72,12 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p),
     ),
+    "mednext_pointwise_fwd_ws": (
+        _i32,
+        (_p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p, _p, _p, _i32, _i32, _p, c_size_t,
+         _p),
+    ),
+    "mednext_pointwise_fwd_workspace_bytes": (c_size_t, (_i64, _i64, _i64, _i64, _i32, _i32)),
     "mednext_pointwise_row_slots": (_i64, (_i64, _i64, _i64, _i64, _i32)),
     "mednext_pointwise_set_kernels": (_i32, (_i32,)),
     "mednext_pointwise_uses_tiled": (_i32, (_i64, _i64, _i64, _i64, _i32, _i32)),
@@ -116,7 +122,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -351,6 +351,7 @@ PW_KERNELS_AUTO, PW_KERNELS_STREAMING, PW_KERNELS_TILED, PW_KERNELS_TILED_64 = 0
 def set_pointwise_kernels(choice: int) -> None:
     """Process-wide choice of the forward kernel family (``PW_KERNELS_*``)."""
     _hip.check(_hip.load().mednext_pointwise_set_kernels(int(choice)), "mednext_pointwise_set_kernels")
+    pointwise_fwd_workspace_bytes.cache_clear()
 
 
 def pointwise_uses_tiled(n: int, k: int, m: int, v: int, prologue: int = 0, epilogue: int = 0) -> bool:
@@ -433,16 +434,26 @@ def pointwise_conv(
         if t is not None and (t.dtype != torch.float64 or not t.is_contiguous() or t.numel() != n * rows):
             raise ValueError(f"{name} must be a contiguous float64 tensor of {n * rows} values")
     lib = _hip.load()
+    ws_bytes = pointwise_fwd_workspace_bytes(n, k, m, v, prologue, epilogue) if int(blocks) == 0 else 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
     _hip.check(
-        lib.mednext_pointwise_fwd_ex(
+        lib.mednext_pointwise_fwd_ws(
             x.data_ptr(), w2.data_ptr(), _hip.ptr(bias), _hip.ptr(aux), _hip.ptr(aux2), _hip.ptr(y), _hip.ptr(y2),
             n, k, m, v, 1 if transpose else 0, prologue, epilogue, _hip.ptr(prologue_coef),
             _hip.ptr(epilogue_coef), _hip.ptr(row_partial), _hip.DTYPE_CODES[torch.bfloat16],
-            int(blocks), _hip.stream_of(x),
+            int(blocks), _hip.ptr(ws), ws_bytes, _hip.stream_of(x),
         ),
-        "mednext_pointwise_fwd_ex",
+        "mednext_pointwise_fwd_ws",
     )
     return (y, y2) if y2 is not None else y
+
+
+@functools.lru_cache(maxsize=4096)
+def pointwise_fwd_workspace_bytes(n: int, k: int, m: int, v: int, prologue: int, epilogue: int) -> int:
+    """Bytes of fp32 partials a ``pointwise_conv`` of this shape needs for the
+    tiled product's K split (0: the launch splits nothing). Depends on the
+    kernel-family choice, so ``set_pointwise_kernels`` clears this cache."""
+    return int(_hip.load().mednext_pointwise_fwd_workspace_bytes(n, k, m, v, prologue, epilogue))
 
 
 @functools.lru_cache(maxsize=4096)
