@@ -325,8 +325,9 @@ int32_t mednext_pointwise_uses_tiled(int64_t n, int64_t k, int64_t m, int64_t v,
 int64_t mednext_pointwise_row_slots(int64_t n, int64_t k, int64_t m, int64_t v,
                                     int32_t blocks_per_sample);
 
-/* Bytes of workspace the weight-gradient launch needs: fp32 per-split
- * partials followed by fp64 range sums (8-byte aligned). */
+/* Bytes of workspace the weight-gradient launch needs: its fp32 per-split
+ * partials, which one reduction launch sums in fixed order (fp64) into the
+ * bf16 gradients. */
 size_t mednext_pointwise_wgrad_workspace_bytes(int64_t n, int64_t k, int64_t m, int64_t v,
                                                int32_t splits);
 

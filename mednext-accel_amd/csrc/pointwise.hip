@@ -1358,52 +1358,48 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_wgrad_wide_kernel(const bf16
   }
 }
 
-// dW / dB = fixed-order fp64 sum of the per-split partials, in two passes so
-// the reduction spreads over the whole GPU. Pass 1: block (eb, r) sums slot
-// range r of R (slots r, r + R, ...) for 64 consecutive outputs; its four
-// thread groups take every fourth slot of the range and are added in group
-// order. Pass 2 adds the R range sums of each output in order and rounds to
-// bf16. R (at most kFinRanges) gives each range about 16 slots, so small slot
-// counts do not launch empty ranges. Partials are [slot][M * K + M] (row-contiguous, so a wave
-// reads 256 bytes per slot).
-constexpr int kFinOut = 64;
-constexpr int kFinGroups = 4;
-constexpr int kFinRanges = 32;
+// dW / dB = fixed-order fp64 sum of the per-split fp32 partials, rounded to
+// bf16, in one launch. Partials are [slot][M * K + M]. A block covers OUT
+// consecutive outputs with W waves; each wave holds 64 / OUT lane groups, so
+// the block has G = W * 64 / OUT groups, and lane group g reads OUT
+// consecutive floats of slots g, g + G, ... (summed in slot order). The G
+// group sums of each output are then added in group order. The host picks
+// OUT (64, 32 or 16) so the grid reaches kFinMinBlocks where the outputs allow
+// it, and W so each lane sums at most about kFinSlotsPerLane slots.
+constexpr int kFinMinBlocks = 512;
+constexpr int kFinSlotsPerLane = 16;
+constexpr int kFinMaxWaves = 16;
 
-__global__ __launch_bounds__(kFinOut* kFinGroups) void pw_wgrad_sum_kernel(const float* __restrict__ partial,
-                                                                           double* __restrict__ sums, int64_t total,
-                                                                           int64_t slots, int64_t stride) {
-  __shared__ double part[kFinGroups][kFinOut];
-  const int lo = threadIdx.x % kFinOut, grp = threadIdx.x / kFinOut;
-  const int64_t e = blockIdx.x * static_cast<int64_t>(kFinOut) + lo;
-  const int64_t r = blockIdx.y, nr = gridDim.y;
+template <int OUT>
+__global__ __launch_bounds__(64 * kFinMaxWaves) void pw_wgrad_reduce_kernel(const float* __restrict__ partial,
+                                                                          bf16_t* __restrict__ dw,
+                                                                          bf16_t* __restrict__ db, int64_t mk,
+                                                                          int64_t m, int64_t slots,
+                                                                          int64_t stride) {
+  extern __shared__ double group_sums[];  // [G][OUT]
+  constexpr int kSub = 64 / OUT;
+  const int lane = threadIdx.x & 63, o = lane % OUT;
+  const int g = (threadIdx.x >> 6) * kSub + lane / OUT;
+  const int groups = static_cast<int>(blockDim.x >> 6) * kSub;
+  const int64_t total = mk + m;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * OUT + o;
   double s = 0.0;
   if (e < total) {
-    for (int64_t t = r + nr * grp; t < slots; t += nr * kFinGroups) s += partial[t * stride + e];
+    const float* p = partial + e;
+#pragma unroll 8
+    for (int64_t t = g; t < slots; t += groups) s += p[t * stride];
   }
-  part[grp][lo] = s;
+  group_sums[g * OUT + o] = s;
   __syncthreads();
-  if (grp == 0 && e < total) {
+  if (threadIdx.x < OUT && e < total && (e < mk || db != nullptr)) {
     double acc = 0.0;
-#pragma unroll
-    for (int gi = 0; gi < kFinGroups; ++gi) acc += part[gi][lo];
-    sums[r * total + e] = acc;
-  }
-}
-
-__global__ __launch_bounds__(256) void pw_wgrad_finish_kernel(const double* __restrict__ sums,
-                                                              bf16_t* __restrict__ dw, bf16_t* __restrict__ db,
-                                                              int64_t mk, int64_t m, int ranges) {
-  const int64_t e = blockIdx.x * static_cast<int64_t>(256) + threadIdx.x;
-  const int64_t total = mk + m;
-  if (e >= total || (e >= mk && db == nullptr)) return;
-  double acc = 0.0;
-  for (int r = 0; r < ranges; ++r) acc += sums[r * total + e];
-  const uint16_t v = f32_to_bf16(static_cast<float>(acc));
-  if (e < mk) {
-    dw[e].bits = v;
-  } else {
-    db[e - mk].bits = v;
+    for (int gi = 0; gi < groups; ++gi) acc += group_sums[gi * OUT + o];
+    const uint16_t v = f32_to_bf16(static_cast<float>(acc));
+    if (e < mk) {
+      dw[e].bits = v;
+    } else {
+      db[e - mk].bits = v;
+    }
   }
 }
 
@@ -1842,7 +1838,7 @@ int64_t wgrad_span(int64_t v, int32_t splits) { return cdiv(cdiv(v, kWgStage), s
 
 namespace {
 
-// Bytes of per-split fp32 partials; the fp64 range sums follow, 8-byte aligned.
+// Bytes of per-split fp32 partials (a whole number of 8-byte words).
 size_t wgrad_partial_bytes(int64_t n, int64_t k, int64_t m, int64_t v, int32_t splits) {
   const int64_t used = cdiv(v, wgrad_span(v, splits));
   return static_cast<size_t>(cdiv(static_cast<int64_t>(n) * used * (m * k + m), 2) * 2) * sizeof(float);
@@ -1853,7 +1849,7 @@ size_t wgrad_partial_bytes(int64_t n, int64_t k, int64_t m, int64_t v, int32_t s
 extern "C" size_t mednext_pointwise_wgrad_workspace_bytes(int64_t n, int64_t k, int64_t m, int64_t v,
                                                           int32_t splits) {
   if (n < 1 || k < 1 || m < 1 || v < 1 || splits < 1) return 0;
-  return wgrad_partial_bytes(n, k, m, v, splits) + static_cast<size_t>(kFinRanges) * (m * k + m) * sizeof(double);
+  return wgrad_partial_bytes(n, k, m, v, splits);
 }
 
 extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const void* x, void* grad_weight,
@@ -1913,15 +1909,18 @@ extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const voi
   }
   MEDNEXT_CHECK_LAUNCH();
   const int64_t total = m * k + m;
-  auto* sums = reinterpret_cast<double*>(static_cast<unsigned char*>(workspace) +
-                                         wgrad_partial_bytes(n, k, m, v, splits));
   const int64_t slots = n * g.splits;
-  const int ranges = static_cast<int>(std::min<int64_t>(kFinRanges, cdiv(slots, 16)));
-  hipLaunchKernelGGL(pw_wgrad_sum_kernel, dim3(static_cast<unsigned>(cdiv(total, kFinOut)), ranges),
-                     dim3(kFinOut * kFinGroups), 0, s, part, sums, total, slots, g.stride);
-  MEDNEXT_CHECK_LAUNCH();
-  hipLaunchKernelGGL(pw_wgrad_finish_kernel, dim3(static_cast<unsigned>(cdiv(total, 256))), dim3(256), 0, s, sums,
-                     static_cast<bf16_t*>(grad_weight), static_cast<bf16_t*>(grad_bias), m * k, m, ranges);
+  int out = 64;
+  while (out > 16 && cdiv(total, static_cast<int64_t>(out)) < kFinMinBlocks) out /= 2;
+  const int waves = static_cast<int>(
+      std::clamp<int64_t>(cdiv(cdiv(slots, static_cast<int64_t>(kFinSlotsPerLane)), static_cast<int64_t>(64 / out)),
+                          1, kFinMaxWaves));
+  const dim3 fin_grid(static_cast<unsigned>(cdiv(total, static_cast<int64_t>(out))));
+  const size_t fin_lds = static_cast<size_t>(waves) * 64 * sizeof(double);
+  auto reduce = out == 64 ? pw_wgrad_reduce_kernel<64> : out == 32 ? pw_wgrad_reduce_kernel<32>
+                                                                   : pw_wgrad_reduce_kernel<16>;
+  hipLaunchKernelGGL(reduce, fin_grid, dim3(64 * waves), fin_lds, s, part, static_cast<bf16_t*>(grad_weight),
+                     static_cast<bf16_t*>(grad_bias), m * k, m, slots, g.stride);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }

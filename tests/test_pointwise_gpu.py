@@ -126,6 +126,32 @@ def test_weight_grad_splits_and_determinism(splits):
     assert max_rel(a[0], want_dw) <= BF16 and max_rel(a[1], want_db) <= BF16
 
 
+@pytest.mark.parametrize(
+    "n,cin,cout,spatial,splits,with_bias",
+    [
+        (2, 32, 96, (16, 32, 128), 512, True),  # 1024 slots, 16 outputs per block, 16 waves
+        (2, 32, 96, (16, 32, 128), 512, False),
+        (1, 128, 160, (8, 8, 40), 7, True),  # 32 outputs per block, one wave
+        (3, 256, 192, (4, 4, 50), 20, False),  # 64 outputs per block, two waves
+    ],
+)
+def test_weight_grad_reduction_shapes(n, cin, cout, spatial, splits, with_bias):
+    """The one-launch partial reduction at each of its block shapes (outputs
+    per block, waves), with and without the bias gradient; run twice."""
+    print(f"[pw wgrad reduce] n={n} cin={cin} cout={cout} spatial={spatial} splits={splits}", flush=True)
+    gen = torch.Generator().manual_seed(cin + cout + splits)
+    x = bf((n, cin, *spatial), gen).to(DEV)
+    dy = bf((n, cout, *spatial), gen).to(DEV)
+    a = hip_ops.pointwise_weight_grad(dy, x, splits=splits, with_bias=with_bias)
+    b = hip_ops.pointwise_weight_grad(dy, x, splits=splits, with_bias=with_bias)
+    assert torch.equal(a[0], b[0])
+    assert (a[1] is None) == (not with_bias)
+    _, want_dw, want_db = opw.conv1x1_backward(f64(dy), f64(x), np.zeros((cout, cin, 1, 1, 1)))
+    assert max_rel(a[0], want_dw) <= BF16
+    if with_bias:
+        assert torch.equal(a[1], b[1]) and max_rel(a[1], want_db) <= BF16
+
+
 STAGES = [(32, 64, 128), (64, 32, 128), (64, 192, 64), (192, 64, 64), (128, 512, 32), (512, 128, 32)]
 
 
