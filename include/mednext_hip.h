@@ -203,7 +203,10 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
  * for the input gradient: grad_x = W^T . grad_y with W the conv's [M][K]).
  * Requirements: bf16, 1 <= K <= 2048, any M >= 1 and V >= 1 (a row's last
  * partial 8-voxel group uses element accesses), one sample's x and y each
- * < 2 GiB, bf16-aligned tensors and a 16-byte aligned weight.
+ * < 2 GiB, bf16-aligned tensors and a 16-byte aligned weight. K up to 8192
+ * runs the tiled product (see mednext_pw_kernels) and needs what it needs:
+ * K % 32 == 0, M % 16 == 0, no GELU or AFFINE prologue, no ROW_REDUCE,
+ * blocks_per_sample 0 and the AUTO or TILED choice.
  * Prologue, applied to every x element as loaded:
  *   MEDNEXT_PW_PROLOGUE_GELU: x -> GELU(x) (exact erf form).
  *   MEDNEXT_PW_PROLOGUE_AFFINE: x -> x * s[n][k] + t[n][k], (s, t) = entries 0

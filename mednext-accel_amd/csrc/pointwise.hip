@@ -44,6 +44,7 @@ namespace {
 constexpr int kPwThreads = 256;  // 4 waves
 constexpr int kChunk = 128;      // voxels per wave task (16 MFMA columns x 8 MFMAs)
 constexpr int kMaxK = 2048;      // LDS weight block: 16 x 2048 bf16 = 64 KiB
+constexpr int kMaxTiledK = 8192;  // the tiled product streams K in 32-channel slices
 constexpr size_t kMaxWeightLds = 64 * 1024;
 constexpr int kResidentWgs = 2 * 256;  // two 4-wave workgroups per CU fill the chip
 
@@ -322,7 +323,8 @@ __device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, c
 // with a runtime slice loop, prefetching one slice ahead inside a chunk.
 // Channels at or past K read as zero (X rows and weight columns), rows at or
 // past M are not stored, and a row's last partial 8-voxel group (V % 8 != 0)
-// goes through element accesses, so any K <= 2048, M and V are accepted.
+// goes through element accesses, so any K <= 2048, M and V are accepted
+// (larger K: the tiled product below).
 template <int KS, int MT, int PRO, int EPI>
 __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __restrict__ x,
                                                                const bf16_t* __restrict__ w,
@@ -1645,9 +1647,14 @@ struct TiledPlan {
   size_t kpart_bytes;  // fp32 partials of the K-split (0 without one)
 };
 
+// K above kMaxK (the streaming kernels' LDS weight block) only runs tiled,
+// without the AFFINE prologue (its per-channel coefficients sit in LDS).
+bool tiled_only(int64_t k) { return k > kMaxK; }
+
 TiledPlan plan_tiled(int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue, int32_t epilogue, bool allow_split) {
   TiledPlan t{false, 1, 1, static_cast<int>(k / 32), 0};
-  if (n < 1 || k < 1 || k > kMaxK || m < 1 || v < 1 || !pro_epi_supported(prologue, epilogue)) return t;
+  if (n < 1 || k < 1 || k > kMaxTiledK || m < 1 || v < 1 || !pro_epi_supported(prologue, epilogue)) return t;
+  if (tiled_only(k) && prologue == MEDNEXT_PW_PROLOGUE_AFFINE) return t;
   const int choice = g_product_kernels.load(std::memory_order_relaxed);
   if (choice == MEDNEXT_PW_KERNELS_STREAMING || !tiled_eligible(k, m, prologue, epilogue)) return t;
   t.mt = choice == MEDNEXT_PW_KERNELS_TILED_64 ? 1 : tiled_mt(n, m, v);
@@ -1660,7 +1667,7 @@ TiledPlan plan_tiled(int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologu
   }
   t.kslices = static_cast<int>(cdiv(ks, split));
   t.ksplit = static_cast<int>(cdiv(ks, t.kslices));
-  if (choice == MEDNEXT_PW_KERNELS_TILED || choice == MEDNEXT_PW_KERNELS_TILED_64) {
+  if (choice == MEDNEXT_PW_KERNELS_TILED || choice == MEDNEXT_PW_KERNELS_TILED_64 || tiled_only(k)) {
     t.tiled = true;
   } else {
     t.tiled = tiled_pays(p, n, m, v) || (p.splitk && t.ksplit > 1);
@@ -1761,7 +1768,6 @@ extern "C" int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, c
   if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
   const bool reduce = epilogue == MEDNEXT_PW_EPILOGUE_ROW_REDUCE;
   MEDNEXT_CHECK_ARG(x != nullptr && weight != nullptr && (y != nullptr || reduce), "null tensor pointer");
-  MEDNEXT_CHECK_ARG(k <= kMaxK, "input channels above 2048 are not supported by the matrix-core GEMM");
   MEDNEXT_CHECK_ARG(weight_layout == 0 || weight_layout == 1, "weight_layout must be 0 ([M][K]) or 1 ([K][M])");
   MEDNEXT_CHECK_ARG(pro_epi_supported(prologue, epilogue), "unsupported prologue / epilogue combination");
   MEDNEXT_CHECK_ARG(!epi_has_aux(epilogue) || aux != nullptr, "this epilogue needs the aux tensor");
@@ -1793,6 +1799,10 @@ extern "C" int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, c
       return launch_tiled(x, weight, bias, aux, y, ex, n, k, m, v, weight_layout, prologue, epilogue, t, workspace,
                           stream);
   }
+  MEDNEXT_CHECK_ARG(k <= kMaxK,
+                    "input channels above 2048 take the tiled product only (K <= 8192 and a multiple of 32, M a "
+                    "multiple of 16, no GELU / AFFINE prologue or ROW_REDUCE epilogue, AUTO or TILED kernels, "
+                    "blocks_per_sample 0)");
   FwdPlan p = plan_fwd(n, k, m, v, epilogue, blocks_per_sample);
   p.g.wt = weight_layout;
   ex.slots = p.slots;

@@ -289,6 +289,7 @@ def group_norm_splits(batch: int, channels: int, spatial_volume: int) -> int:
 
 PW_CHUNK = 128  # voxels per wave task of pw_fwd_kernel
 PW_MAX_K = 2048  # reduction channels the LDS weight block holds (16 x 2048 bf16)
+PW_MAX_TILED_K = 8192  # the tiled product streams K in 32-channel slices
 PW_WG_VOXELS = 128  # voxels one pw_wgrad workgroup covers per round (4 waves x 32)
 
 
@@ -297,12 +298,21 @@ def pointwise_supported(in_channels: int, out_channels: int, voxels: int) -> boo
     """Shapes the bf16 matrix-core pointwise kernels take (mirrors pointwise.hip).
 
     Any channel counts and voxel count, as long as the reduction of each
-    direction fits the weight block (forward K = in_channels, input gradient K
-    = out_channels, both <= 2048) and one sample's tensor stays below 2 GiB
-    (32-bit buffer offsets).
+    direction (forward K = in_channels, M = out_channels; input gradient the
+    other way round) fits the streaming kernels' weight block (K <= 2048) or
+    the tiled product (K <= 8192, K % 32 == 0, M % 16 == 0; no GELU prologue,
+    which callers only use below 128 hidden channels), and one sample's tensor
+    stays below 2 GiB (32-bit buffer offsets).
     """
+
+    def reduces(k: int, m: int) -> bool:
+        return 1 <= k <= PW_MAX_K or (k <= PW_MAX_TILED_K and k % 32 == 0 and m % 16 == 0)
+
     small = in_channels * voxels * 2 < 2**31 and out_channels * voxels * 2 < 2**31
-    return 1 <= in_channels <= PW_MAX_K and 1 <= out_channels <= PW_MAX_K and voxels >= 1 and small
+    return (
+        in_channels >= 1 and out_channels >= 1 and voxels >= 1 and small
+        and reduces(in_channels, out_channels) and reduces(out_channels, in_channels)
+    )
 
 
 @functools.lru_cache(maxsize=4096)

@@ -218,17 +218,67 @@ def test_opcheck_pointwise_ops():
     torch.library.opcheck(hip_ops.mlp_expansion_stored, (x, w, b, w2, None, res))
 
 
-def test_channels_above_2048_are_rejected_and_not_selected():
-    """The LDS weight block holds K <= 2048 reduction channels: the tile policy
-    does not select the kernel beyond that and the C ABI refuses it."""
+def test_channels_above_2048_take_the_tiled_product():
+    """K above the streaming kernels' 2048-channel weight block runs the tiled
+    product (K <= 8192, K % 32 == 0, M % 16 == 0): the tile policy selects the
+    kernels exactly there, and the C ABI refuses the rest with a message."""
     from mednext_accel_amd.tiles import pointwise_supported
 
-    assert not pointwise_supported(4096, 512, 8**3)
-    assert pointwise_supported(2048, 512, 8**3) and pointwise_supported(1, 32, 127**3)
-    x = torch.randn(1, 4096, 1, 1, 8, device=DEV).bfloat16()
-    w = torch.randn(256, 4096, 1, 1, 1, device=DEV).bfloat16()
-    with pytest.raises(hip_ops._hip.HipLibraryError, match="above 2048"):
-        hip_ops.pointwise_conv(x, w)
+    assert pointwise_supported(4096, 512, 8**3) and pointwise_supported(512, 4096, 8**3)
+    assert pointwise_supported(8192, 16, 8) and not pointwise_supported(8224, 32, 8)
+    assert not pointwise_supported(4112, 512, 8**3) and not pointwise_supported(4096, 520, 8**3)
+    assert pointwise_supported(2048, 520, 8**3) and pointwise_supported(1, 32, 127**3)
+    gen = torch.Generator().manual_seed(4)
+    x = torch.randn(2, 4096, 2, 4, 9, generator=gen).bfloat16()
+    w = (torch.randn(256, 4096, 1, 1, 1, generator=gen) / 64).bfloat16()
+    b = torch.randn(256, generator=gen).bfloat16()
+    res = torch.randn(2, 256, 2, 4, 9, generator=gen).bfloat16()
+    want = torch.einsum("mk,nkv->nmv", w.double().view(256, 4096), x.double().flatten(2)).view(2, 256, 2, 4, 9)
+    y = hip_ops.pointwise_conv(x.to(DEV), w.to(DEV), b.to(DEV), aux=res.to(DEV), epilogue=PW_EPILOGUE_BIAS_RESIDUAL)
+    assert max_rel(y, want + b.double().view(1, -1, 1, 1, 1) + res.double()) <= BF16
+    # transposed product (input gradient of a 4096 -> 256 conv's twin): K = 4096 rows of a [K][M] weight
+    wt = (torch.randn(4096, 256, 1, 1, 1, generator=gen) / 64).bfloat16()
+    dx = hip_ops.pointwise_conv(x.to(DEV), wt.to(DEV), transpose=True)
+    want_t = torch.einsum("km,nkv->nmv", wt.double().view(4096, 256), x.double().flatten(2)).view(2, 256, 2, 4, 9)
+    assert max_rel(dx, want_t) <= BF16
+    with pytest.raises(hip_ops._hip.HipLibraryError, match="tiled product only"):
+        hip_ops.pointwise_conv(x.to(DEV), w.to(DEV), prologue=PW_PROLOGUE_GELU)
+    xr = torch.randn(1, 4112, 1, 1, 8, device=DEV).bfloat16()
+    with pytest.raises(hip_ops._hip.HipLibraryError, match="tiled product only"):
+        hip_ops.pointwise_conv(xr, torch.randn(256, 4112, 1, 1, 1, device=DEV).bfloat16())
+    hip_ops.set_pointwise_kernels(hip_ops.PW_KERNELS_STREAMING)
+    try:
+        with pytest.raises(hip_ops._hip.HipLibraryError, match="tiled product only"):
+            hip_ops.pointwise_conv(x.to(DEV), w.to(DEV))
+    finally:
+        hip_ops.set_pointwise_kernels(hip_ops.PW_KERNELS_AUTO)
+
+
+@pytest.mark.parametrize("s", [8, 5])
+def test_fused_mlp_expansion_at_4096_hidden_channels(s):
+    """The MedNeXt-L bottleneck block's expansion (512 -> 4096 -> 512, expansion
+    ratio 8) fwd + bwd through the fused op vs the same composition in fp32
+    PyTorch: the project product and the expand input gradient reduce over
+    4096 channels (tiled product with K split over workgroups)."""
+    gen = torch.Generator(device=DEV).manual_seed(8)
+    c, h = 512, 4096
+    x = torch.randn(1, c, s, s, s, generator=gen, device=DEV).bfloat16()
+    res = torch.randn(1, c, s, s, s, generator=gen, device=DEV).bfloat16()
+    w1 = (torch.randn(h, c, 1, 1, 1, generator=gen, device=DEV) * c**-0.5).bfloat16()
+    b1 = (torch.randn(h, generator=gen, device=DEV) * 0.1).bfloat16()
+    w2 = (torch.randn(c, h, 1, 1, 1, generator=gen, device=DEV) * h**-0.5).bfloat16()
+    b2 = (torch.randn(c, generator=gen, device=DEV) * 0.1).bfloat16()
+    leaves = [t.clone().requires_grad_() for t in (x, w1, b1, w2, b2, res)]
+    out = hip_ops.mlp_expansion_stored(*leaves)[0]
+    ref_leaves = [t.float().requires_grad_() for t in (x, w1, b1, w2, b2, res)]
+    xf, w1f, b1f, w2f, b2f, rf = ref_leaves
+    ref = F.conv3d(F.gelu(F.conv3d(xf, w1f, b1f)), w2f, b2f) + rf
+    assert max_rel(out, ref) <= BF16
+    g = torch.randn_like(ref).bfloat16()
+    got = torch.autograd.grad(out, leaves, g)
+    want = torch.autograd.grad(ref, ref_leaves, g.float())
+    for name, a, b in zip(["x", "w1", "b1", "w2", "b2", "res"], got, want):
+        assert max_rel(a, b) <= BF16, name
 
 
 # Ragged and odd shapes: K not a multiple of 32 (stem K = 1, head dgrad K = 3),

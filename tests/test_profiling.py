@@ -43,10 +43,11 @@ def test_workload_matrix_candidates_are_valid_recipes():
     fwd = [c for c in cases if c.family == "depthwise_conv3d" and c.phase == "forward" and c.in_channels == 32]
     default = tiles.depthwise_recipe(1, 32, (128, 128, 128), 3, "bfloat16", "forward")
     assert any(c.parameter_map == dict(zip(("engine", "tile_w", "depth_chunk"), default)) for c in fwd)
-    # Hidden widths beyond the matrix-core limit keep only the library candidates.
+    # 4096 hidden channels (Large bottleneck) run the tiled product, so the HIP
+    # candidate is offered there too (the limits themselves: test_tiles.py).
     big = [c for c in build_workload_cases("large", size=128) if c.family == "pointwise_conv3d" and 4096 in
            (c.in_channels, c.out_channels)]
-    assert big and {c.implementation for c in big} == {"reference", "pointwise_gemm_per_sample"}
+    assert big and {c.implementation for c in big} == {"reference", "pointwise_gemm_per_sample", "hip_pointwise_gemm"}
     # Every 1x1x1 context offers the per-sample GEMM; v2 contexts use the v2 widths and ratios.
     pw = [c for c in cases if c.family == "pointwise_conv3d"]
     assert {c.implementation for c in pw} == {"reference", "pointwise_gemm_per_sample", "hip_pointwise_gemm"}

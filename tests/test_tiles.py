@@ -90,3 +90,17 @@ def test_small_planes_use_the_volume_engine():
                         plan = tiles.volume_plan(1, channels, (size,) * 3, k, depth_chunk, acc_bytes=acc, wgrad=wgrad)
                         assert plan.lds_bytes <= tiles.LDS_LIMIT
     assert not tiles.volume_supported((32, 32, 32)) and tiles.volume_supported((4, 16, 16))
+
+
+def test_pointwise_supported_mirrors_the_library_limits():
+    """Each direction's reduction K either fits the streaming kernels' weight
+    block (<= 2048) or the tiled product (<= 8192, K % 32 == 0, the other side
+    % 16 == 0); one sample's tensors stay below 2 GiB."""
+    ok = tiles.pointwise_supported
+    assert ok(2048, 2048, 512) and ok(1, 3, 127**3) and ok(2048, 3, 8)
+    assert ok(512, 4096, 512) and ok(4096, 512, 512)  # MedNeXt-L bottleneck expansion
+    assert ok(8192, 16, 8) and not ok(8224, 32, 8)
+    assert not ok(4112, 512, 8) and not ok(512, 4112, 8)  # K % 32
+    assert not ok(4096, 520, 8) and not ok(520, 4096, 8)  # M % 16 of the wide direction
+    assert not ok(0, 32, 8) and not ok(32, 32, 0)
+    assert not ok(32, 64, 2**25)  # 64 x 2^25 x 2 bytes = 4 GiB per sample
