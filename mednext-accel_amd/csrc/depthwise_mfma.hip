@@ -22,6 +22,20 @@
 // static. For k = 3 finished output planes leave through an LDS staging tile
 // as whole rows (16-byte stores).
 //
+// Block-Toeplitz form (k = 5). The 1-D form spends k^2 = 25 MFMAs per tile
+// and input plane, 5 of every 32 products useful. For k = 5 the 16x16 tile is
+// instead 16 blocks of 4x4 outputs (n = block, i = 4 * row + col inside it)
+// and the K window is a 4-row x 8-column piece of the block's 8x8 input
+// window, so two MFMAs (input rows 0-3 and 4-7 of the window) cover all 25
+// taps of one kd:
+//   A_{kd,h}[i][8 r + c] = tap(kd, kh = 4 h + r - i / 4, kw = c - i % 4)
+//   B_h[8 r + c][n]      = x[d][h0(n) + 4 h + r - p][w0(n) + c - p]
+// 10 MFMAs per tile and input plane (39% of the products useful), and ten
+// instead of 25 tap matrices in registers. The B rows of one lane start two
+// elements before a 4-aligned column, so they are read as four dwords; the
+// LDS row pitch is padded to an odd multiple of four dwords so the 16 blocks
+// of a lane group fall on distinct banks.
+//
 // Buffer helpers and the MFMA lane layout: cdna4.h.
 #include "cdna4.h"
 #include "common.h"
@@ -34,6 +48,10 @@ constexpr int kThreads = 256;
 constexpr int kRT = 2;  // 16-row tiles per workgroup plane (32 rows)
 
 constexpr bool stencil_stages_output(int k) { return k == 3; }
+constexpr bool stencil_blocks(int k) { return k == 5; }
+// LDS row pitch (elements) of the plane buffers: [tw0 - 8, tw0 + TW + 8), plus
+// 8 elements of padding in the block-Toeplitz form.
+constexpr int stencil_pitch(int k, int ct) { return 16 * ct + (stencil_blocks(k) ? 24 : 16); }
 constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
 constexpr int lcm_int(int a, int b) { return a / gcd_int(a, b) * b; }
 
@@ -81,9 +99,10 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   constexpr int P = K / 2;
   constexpr int K3 = K * K * K;
   constexpr int TH = 16 * kRT, TW = 16 * CT;
-  constexpr int LR = TH + 2 * P;  // LDS rows: h = th0 - P + r
-  constexpr int LC = TW + 16;     // LDS cols: w = tw0 - 8 + col
-  constexpr int CPR = LC / 8;     // 16-byte chunks per LDS row
+  constexpr bool BLK = stencil_blocks(K);
+  constexpr int LR = TH + 2 * P;              // LDS rows: h = th0 - P + r
+  constexpr int LC = stencil_pitch(K, CT);    // LDS cols: w = tw0 - 8 + col
+  constexpr int CPR = (TW + 16) / 8;          // 16-byte chunks per LDS row
   constexpr int NCHUNK = LR * CPR;
   constexpr int NCH = (NCHUNK + kThreads - 1) / kThreads;
   constexpr int TPW = kRT * CT / 4;  // tiles per wave
@@ -93,6 +112,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   // k = 5 keeps the direct 8-byte stores: its LDS and register footprint
   // already bound occupancy, and measured faster that way.
   constexpr bool STAGE = stencil_stages_output(K);
+  static_assert(!(BLK && STAGE), "the block-Toeplitz form stores its outputs directly");
   constexpr int OC = TW + 8;           // output staging row pitch (elements)
   constexpr int OBUF = TH * OC;
   constexpr int OCH = TH * (TW / 8);   // 16-byte output chunks per plane
@@ -115,24 +135,29 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   const int n16 = lane & 15;
   const int q = lane >> 4;
 
-  // A operands: Toeplitz tap matrices, one per (kd, kh).
-  bf16x8_t amat[K][K];
+  // A operands: Toeplitz tap matrices, one per (kd, kh); block-Toeplitz, one
+  // per (kd, window half).
+  constexpr int NA = BLK ? 2 : K;
+  bf16x8_t amat[K][NA];
   {
     const uint16_t* __restrict__ wraw =
         reinterpret_cast<const uint16_t*>(wt) + static_cast<int64_t>(bp.c) * K3;
 #pragma unroll
     for (int kd = 0; kd < K; ++kd)
 #pragma unroll
-      for (int kh = 0; kh < K; ++kh)
+      for (int a = 0; a < NA; ++a)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const int kw = 8 * q + j - 8 - n16 + P;
+          // 1-D: row i = n16 is output column i, kk = 8 q + j the window column.
+          // Block: i = n16 is output (n16 / 4, n16 % 4) of the block, kk = (q, j).
+          const int kh = BLK ? 4 * a + q - (n16 >> 2) : a;
+          const int kw = BLK ? j - (n16 & 3) : 8 * q + j - 8 - n16 + P;
           uint16_t bits = 0;
-          if (kw >= 0 && kw < K) {
+          if (kh >= 0 && kh < K && kw >= 0 && kw < K) {
             const int t = (kd * K + kh) * K + kw;
             bits = wraw[FLIP ? K3 - 1 - t : t];
           }
-          amat[kd][kh][j] = __builtin_bit_cast(__bf16, bits);
+          amat[kd][a][j] = __builtin_bit_cast(__bf16, bits);
         }
   }
   float b0 = 0.f;
@@ -210,15 +235,35 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
         const int tile = wave + 4 * t;
         const int ty = tile / CT;
         const int tx = tile % CT;
-        const uint16_t* bp0 = buf + (16 * ty + n16) * LC + 16 * tx + 8 * q;
+        if constexpr (BLK) {
+          // Block n16 = (row n16 / 4, column n16 % 4) of the tile; lane group q
+          // reads window row q (+ 4 for the second half), 8 columns from 2 to
+          // the left of the block: a 4-byte aligned run.
+          const uint32_t* bp0 = reinterpret_cast<const uint32_t*>(
+              buf + (16 * ty + 4 * (n16 >> 2) + q) * LC + 16 * tx + 4 * (n16 & 3) + 8 - P);
 #pragma unroll
-        for (int kh = 0; kh < K; ++kh) {
-          const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, lds_read16(bp0 + kh * LC));
+          for (int h2 = 0; h2 < 2; ++h2) {
+            const uint32_t* row = bp0 + h2 * 2 * LC;  // 4 rows = 4 * LC elements = 2 * LC dwords
+            const uint4 raw = make_uint4(row[0], row[1], row[2], row[3]);
+            const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, raw);
 #pragma unroll
-          for (int kd = 0; kd < K; ++kd) {
-            const int slot = ((s - kd) % K + K) % K;
-            acc[slot][t] =
-                __builtin_amdgcn_mfma_f32_16x16x32_bf16(amat[kd][kh], bm, acc[slot][t], 0, 0, 0);
+            for (int kd = 0; kd < K; ++kd) {
+              const int slot = ((s - kd) % K + K) % K;
+              acc[slot][t] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(amat[kd][h2], bm, acc[slot][t], 0, 0, 0);
+            }
+          }
+        } else {
+          const uint16_t* bp0 = buf + (16 * ty + n16) * LC + 16 * tx + 8 * q;
+#pragma unroll
+          for (int kh = 0; kh < K; ++kh) {
+            const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, lds_read16(bp0 + kh * LC));
+#pragma unroll
+            for (int kd = 0; kd < K; ++kd) {
+              const int slot = ((s - kd) % K + K) % K;
+              acc[slot][t] =
+                  __builtin_amdgcn_mfma_f32_16x16x32_bf16(amat[kd][kh], bm, acc[slot][t], 0, 0, 0);
+            }
           }
         }
         {
@@ -228,8 +273,10 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
           if constexpr (STAGE) {
             *reinterpret_cast<bf16x4_t*>(obuf + (16 * ty + n16) * OC + 16 * tx + 4 * q) = packed;
           } else {
-            const int h = th0 + 16 * ty + n16;
-            const int w = tw0 + 16 * tx + 4 * q;
+            // Lane (n16, q) holds 4 consecutive outputs: 1-D, row n16 columns
+            // 4 q ..; block, row 4 (n16 / 4) + q columns 4 (n16 % 4) ..
+            const int h = th0 + 16 * ty + (BLK ? 4 * (n16 >> 2) + q : n16);
+            const int w = tw0 + 16 * tx + (BLK ? 4 * (n16 & 3) : 4 * q);
             const bool ok = write_o && h < g.H && w < g.W;
             const uint32_t off = ok ? obase + static_cast<uint32_t>(2 * (h * g.W + w)) : kOob;
             u32x2_t words = __builtin_bit_cast(u32x2_t, packed);
@@ -562,7 +609,7 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
   constexpr int P = K / 2;
   // two plane buffers + one dummy 16-byte slot for threads without a fill chunk
   constexpr size_t stage = stencil_stages_output(K) ? static_cast<size_t>(2) * (16 * kRT) * (16 * CT + 8) : 0;
-  constexpr size_t lds = (static_cast<size_t>(2) * (16 * kRT + 2 * P) * (16 * CT + 16) + 8 + stage) * 2;
+  constexpr size_t lds = (static_cast<size_t>(2) * (16 * kRT + 2 * P) * stencil_pitch(K, CT) + 8 + stage) * 2;
   auto px = static_cast<const bf16_t*>(x);
   auto pw = static_cast<const bf16_t*>(wt);
   auto pb = static_cast<const bf16_t*>(bias);

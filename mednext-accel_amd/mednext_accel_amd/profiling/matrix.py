@@ -89,6 +89,7 @@ def _depthwise_candidates(batch: int, channels: int, s: int, k: int, dtype: str,
         for tw in (32, 64, 128):
             if tw <= max(32, s) and tw != tile_w:
                 add(engine, tw, depth_chunk)
+                add(engine, tw, depth_chunk * tile_w // tw)  # the same workgroup count
     for dc in (depth_chunk // 2, depth_chunk * 2):
         if dc < 1:
             continue

@@ -115,16 +115,18 @@ def _depth_chunk(d: int, slabs: int, kernel_size: int, target: int = TARGET_WORK
 
 
 # Workgroups a matrix-core depthwise launch aims for, per (phase kind, k). The
-# forward / input-grad kernel holds two 16x(tile_w) accumulator rows per wave and
-# runs at 2 workgroups per CU (k=3) or 1 (k=5, larger LDS halo), so it wants
-# long D-runs and ~1-2 workgroups per CU. The weight-grad kernel (4 waves of
-# 16 - (k-1) grad_output rows x 32 columns each) wants ~2-2.5 per CU. Measured
-# on MI355X at the MedNeXt stage shapes (C32 128^3, C64 64^3, C128 32^3; k=3
-# and 5): these targets reproduce the best depth_chunk of a sweep over
-# {8..64} within run-to-run noise.
+# forward / input-grad kernel holds two 16x(tile_w) accumulator rows per wave
+# and k rotating output planes, so it wants long D-runs and ~2 workgroups per CU
+# (k=5 in its block-Toeplitz form: 2-3 resident per CU). The weight-grad kernel
+# (4 waves of 16 - (k-1) grad_output rows x 32 columns each) wants ~2-2.5 per
+# CU. Measured on MI355X at the MedNeXt stage shapes (C32 128^3, C64 64^3,
+# C128 32^3; k=3 and 5): these targets reproduce the best depth_chunk of a
+# sweep over {4..128} within run-to-run noise (k=5 forward at 128^3: tile 128
+# / D-run 32 55.5 us, tile 64 / 64 54.1 us, the former target's 128 / 64
+# 60.4 us).
 MFMA_TARGET_WORKGROUPS = {
     ("stencil", 3): 2 * CU_COUNT,
-    ("stencil", 5): CU_COUNT,
+    ("stencil", 5): 2 * CU_COUNT,
     ("weight_grad", 3): 5 * CU_COUNT // 2,
     ("weight_grad", 5): 2 * CU_COUNT,
 }

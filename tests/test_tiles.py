@@ -69,7 +69,8 @@ def test_mfma_stage0_recipes_match_measured_best():
     assert r(1, 32, (128,) * 3, 3, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 128, 64]
     assert r(1, 32, (128,) * 3, 5, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 128, 64]
     assert r(1, 64, (64,) * 3, 3, "bfloat16", "weight_grad") == [tiles.ENGINE_MFMA, 64, 16]
-    assert r(1, 32, (128,) * 3, 5, "bfloat16", "forward") == [tiles.ENGINE_MFMA, 128, 64]
+    assert r(1, 32, (128,) * 3, 5, "bfloat16", "forward") == [tiles.ENGINE_MFMA, 128, 32]
+    assert r(1, 64, (64,) * 3, 5, "bfloat16", "input_grad") == [tiles.ENGINE_MFMA, 64, 16]
     assert r(1, 64, (64,) * 3, 3, "bfloat16", "input_grad") == [tiles.ENGINE_MFMA, 64, 16]
 
 
