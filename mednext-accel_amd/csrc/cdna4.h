@@ -95,6 +95,9 @@ __device__ inline uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 __device__ inline u32x2_t buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
 }
+__device__ inline void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
+}
 __device__ inline void buf_store8(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t lo, uint32_t hi) {
   const u32x2_t v = {lo, hi};
   __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0);

@@ -981,6 +981,13 @@ int launch_s2_map_k(const void* in, const void* w, const void* b, void* out, S2D
   return MEDNEXT_STATUS_OK;
 }
 
+// bf16 stride-2 maps whose big plane is too large for the band kernels
+// (small plane above 256 positions) run on the matrix-core stencil / weight
+// gradient when the shape is the down block's (even big dims, W % 32 == 0).
+bool s2_mfma_chosen(int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k, int dtype) {
+  return dtype == MEDNEXT_DTYPE_BF16 && hs * ws > 256 && dw_mfma_s2_supported(db, hb, wb, ds, hs, ws, k);
+}
+
 template <bool GATHER>
 int s2_map_entry(const void* in, const void* w, const void* b, void* out, int64_t n, int64_t c, int64_t db,
                  int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int32_t k, int32_t dtype, void* stream) {
@@ -989,6 +996,10 @@ int s2_map_entry(const void* in, const void* w, const void* b, void* out, int64_
   if (int st = s2_plan(n, c, db, hb, wb, ds, hs, ws, k, dtype, GATHER ? kSmallDomain : kBigCellDomain, &g))
     return st;
   auto s = static_cast<hipStream_t>(stream);
+  if (s2_mfma_chosen(db, hb, wb, ds, hs, ws, k, dtype)) {
+    return GATHER ? dw_mfma_s2_gather(in, w, b, out, n, c, db, hb, wb, ds, hs, ws, k, s)
+                  : dw_mfma_s2_scatter(in, w, b, out, n, c, db, hb, wb, ds, hs, ws, k, s);
+  }
   if (GATHER && dw_s2band_chosen(n, c, db, hb, wb, ds, hs, ws, k, dtype))
     return dw_s2band_gather(in, w, b, out, n, c, db, hb, wb, ds, hs, ws, k, dtype, s);
 #define MEDNEXT_S2_K(T)                                                          \
@@ -1245,6 +1256,10 @@ extern "C" size_t mednext_depthwise3d_s2_wgrad_workspace_bytes(int64_t n, int64_
   S2Dims g;
   if (s2_plan(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, kSmallDomain, &g) != MEDNEXT_STATUS_OK) return 0;
   const int64_t k3 = int64_t(kernel_size) * kernel_size * kernel_size;
+  if (s2_mfma_chosen(db, hb, wb, ds, hs, ws, kernel_size, dtype)) {
+    const int64_t splits = dw_mfma_s2_wgrad_splits(n, c, db, hb, wb, ds, hs, ws, kernel_size);
+    return static_cast<size_t>(c * splits * (k3 + 1) * sizeof(float));
+  }
   if (dw_s2band_chosen(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype)) {
     const int64_t splits = dw_s2band_wgrad_splits(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype);
     return static_cast<size_t>(c * splits * (k3 + 1) * acc_bytes_of(dtype));
@@ -1269,6 +1284,14 @@ extern "C" int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* sma
       mednext_depthwise3d_s2_wgrad_workspace_bytes(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype);
   MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= need, "workspace too small");
   auto s = static_cast<hipStream_t>(stream);
+  if (s2_mfma_chosen(db, hb, wb, ds, hs, ws, kernel_size, dtype)) {
+    const int splits = dw_mfma_s2_wgrad_splits(n, c, db, hb, wb, ds, hs, ws, kernel_size);
+    if (int st = dw_mfma_s2_wgrad(big, small, static_cast<float*>(workspace), n, c, db, hb, wb, ds, hs, ws,
+                                  kernel_size, s))
+      return st;
+    return finish_partials(dtype, workspace, grad_weight, grad_bias, c, splits,
+                           kernel_size * kernel_size * kernel_size, s);
+  }
   if (dw_s2band_chosen(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype)) {
     const int splits = dw_s2band_wgrad_splits(n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype);
     if (int st = dw_s2band_wgrad(big, small, workspace, n, c, db, hb, wb, ds, hs, ws, kernel_size, dtype, s))

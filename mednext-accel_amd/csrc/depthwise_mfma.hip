@@ -36,7 +36,22 @@
 // LDS row pitch is padded to an odd multiple of four dwords so the 16 blocks
 // of a lane group fall on distinct banks.
 //
+// Stride-2 modes. The MedNeXt down block's stride-2 depthwise conv (padding
+// k/2) and its input gradient are this stencil in disguise:
+//   gather  small[o] = sum_t w[t] big[2o + t - p] = stencil(big)[2o]
+//   scatter big[i]   = sum_{2o + t - p = i} w[t] small[o]
+//                    = flipped-tap stencil over up(small), up(small)[2o] =
+//                      small[o] and zero at odd indices.
+// kS2Sub runs the stencil over the big tensor and stores only the even output
+// positions, into the small tensor, skipping the MFMAs of odd output planes;
+// kS2Up fills the LDS planes from the small tensor, expanded with zeros, and
+// skips the MFMAs of the all-zero odd input planes. The weight gradient's
+// kS2 form (dW[t] = sum_o big[2o + t - p] small[o]) is the weight-gradient
+// kernel below with dy = up(small).
+//
 // Buffer helpers and the MFMA lane layout: cdna4.h.
+#include <algorithm>
+
 #include "cdna4.h"
 #include "common.h"
 #include "depthwise_mfma.h"
@@ -48,6 +63,7 @@ constexpr int kThreads = 256;
 constexpr int kRT = 2;  // 16-row tiles per workgroup plane (32 rows)
 
 constexpr bool stencil_stages_output(int k) { return k == 3; }
+constexpr int kS2None = 0, kS2Sub = 1, kS2Up = 2;  // stencil stride-2 modes
 constexpr bool stencil_blocks(int k) { return k == 5; }
 // LDS row pitch (elements) of the plane buffers: [tw0 - 8, tw0 + TW + 8), plus
 // 8 elements of padding in the block-Toeplitz form.
@@ -56,9 +72,10 @@ constexpr int gcd_int(int a, int b) { return b == 0 ? a : gcd_int(b, a % b); }
 constexpr int lcm_int(int a, int b) { return a / gcd_int(a, b) * b; }
 
 struct MGeom {
-  int C, D, H, W;
+  int C, D, H, W;  // the stencil's (big) grid
   int TD;  // output planes per workgroup
   int nDc, nHt, nWt;
+  int Ds, Hs, Ws;  // stride-2 modes: the small tensor
 };
 
 struct BlockPos {
@@ -89,7 +106,7 @@ __device__ inline uint4 lds_read16(const uint16_t* p) { return *reinterpret_cast
 // like y (the gradient that reaches the same input through the block's
 // residual), added to the bf16-rounded stencil value in fp32 and rounded
 // again, exactly as a separate bf16 add would.
-template <int K, bool FLIP, bool BIAS, int CT, int PD, bool ACC = false>
+template <int K, bool FLIP, bool BIAS, int CT, int PD, bool ACC = false, int S2 = kS2None>
 __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t* __restrict__ x,
                                                                    const bf16_t* __restrict__ wt,
                                                                    const bf16_t* __restrict__ bias,
@@ -113,6 +130,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   // already bound occupancy, and measured faster that way.
   constexpr bool STAGE = stencil_stages_output(K);
   static_assert(!(BLK && STAGE), "the block-Toeplitz form stores its outputs directly");
+  static_assert(S2 == kS2None || !ACC, "stride-2 modes take no accumulation input");
   constexpr int OC = TW + 8;           // output staging row pitch (elements)
   constexpr int OBUF = TH * OC;
   constexpr int OCH = TH * (TW / 8);   // 16-byte output chunks per plane
@@ -127,8 +145,11 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   const BlockPos bp = block_pos(g);
   const int th0 = bp.ht * TH, tw0 = bp.wt * TW, d0 = bp.dc * g.TD;
   const int64_t plane = static_cast<int64_t>(g.H) * g.W;
-  const uint16_t* __restrict__ xnc = reinterpret_cast<const uint16_t*>(x) + bp.nc * g.D * plane;
-  uint16_t* __restrict__ ync = reinterpret_cast<uint16_t*>(y) + bp.nc * g.D * plane;
+  const int64_t splane = static_cast<int64_t>(g.Hs) * g.Ws;  // stride-2 modes
+  const int64_t in_slab = S2 == kS2Up ? g.Ds * splane : g.D * plane;
+  const int64_t out_slab = S2 == kS2Sub ? g.Ds * splane : g.D * plane;
+  const uint16_t* __restrict__ xnc = reinterpret_cast<const uint16_t*>(x) + bp.nc * in_slab;
+  uint16_t* __restrict__ ync = reinterpret_cast<uint16_t*>(y) + bp.nc * out_slab;
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -166,8 +187,8 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
 
   // Per-thread chunk coordinates of the fill (the same for every plane).
   // Threads without a chunk write a dummy LDS slot past the two buffers.
-  const __amdgpu_buffer_rsrc_t xr = slab_rsrc(xnc, static_cast<uint32_t>(g.D * plane * 2));
-  const __amdgpu_buffer_rsrc_t yr = slab_rsrc(ync, static_cast<uint32_t>(g.D * plane * 2));
+  const __amdgpu_buffer_rsrc_t xr = slab_rsrc(xnc, static_cast<uint32_t>(in_slab * 2));
+  const __amdgpu_buffer_rsrc_t yr = slab_rsrc(ync, static_cast<uint32_t>(out_slab * 2));
   const __amdgpu_buffer_rsrc_t ar =
       slab_rsrc(ACC ? reinterpret_cast<const uint16_t*>(acc_in) + bp.nc * g.D * plane : ync,
                 ACC ? static_cast<uint32_t>(g.D * plane * 2) : 0u);
@@ -184,7 +205,13 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
       const int h = th0 - P + r;
       const int w = tw0 - 8 + 8 * ch;
       ch_lds[u] = r * LC + 8 * ch;
-      if (h >= 0 && h < g.H && w >= 0 && w < g.W) ch_off[u] = 2 * (h * g.W + w);
+      if constexpr (S2 == kS2Up) {
+        // Even rows only; the chunk's 8 columns hold small columns w/2 .. w/2 + 3.
+        if (h >= 0 && !(h & 1) && (h >> 1) < g.Hs && w >= 0 && (w >> 1) < g.Ws)
+          ch_off[u] = 2 * ((h >> 1) * g.Ws + (w >> 1));
+      } else {
+        if (h >= 0 && h < g.H && w >= 0 && w < g.W) ch_off[u] = 2 * (h * g.W + w);
+      }
     }
   }
   const int nplanes = g.TD + K - 1;
@@ -192,17 +219,34 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   // volume or past this workgroup's range read as zeros without touching memory.
   auto load_plane = [&](int j, uint4* pre) {
     const int di = d0 - P + j;
-    const bool plane_ok = j < nplanes && di >= 0 && di < g.D;
-    const uint32_t pbase = static_cast<uint32_t>(plane_ok ? di : 0) * static_cast<uint32_t>(plane * 2);
+    if constexpr (S2 == kS2Up) {
+      // Odd planes of up(small) are zero; even plane di is small plane di / 2.
+      const bool plane_ok = j < nplanes && di >= 0 && !(di & 1) && (di >> 1) < g.Ds;
+      const uint32_t pbase = static_cast<uint32_t>(plane_ok ? di >> 1 : 0) * static_cast<uint32_t>(splane * 2);
 #pragma unroll
-    for (int u = 0; u < NCH; ++u) {
-      const uint32_t off = (plane_ok && ch_off[u] >= 0) ? pbase + static_cast<uint32_t>(ch_off[u]) : kOob;
-      pre[u] = buf_load16(xr, off);  // halo rows/planes are re-read: keep them cacheable
+      for (int u = 0; u < NCH; ++u) {
+        const uint32_t off = (plane_ok && ch_off[u] >= 0) ? pbase + static_cast<uint32_t>(ch_off[u]) : kOob;
+        const u32x2_t v = buf_load8(xr, off);
+        pre[u] = make_uint4(v[0], v[1], 0u, 0u);
+      }
+    } else {
+      const bool plane_ok = j < nplanes && di >= 0 && di < g.D;
+      const uint32_t pbase = static_cast<uint32_t>(plane_ok ? di : 0) * static_cast<uint32_t>(plane * 2);
+#pragma unroll
+      for (int u = 0; u < NCH; ++u) {
+        const uint32_t off = (plane_ok && ch_off[u] >= 0) ? pbase + static_cast<uint32_t>(ch_off[u]) : kOob;
+        pre[u] = buf_load16(xr, off);  // halo rows/planes are re-read: keep them cacheable
+      }
     }
   };
   auto store_plane = [&](uint16_t* buf, const uint4* pre) {
 #pragma unroll
-    for (int u = 0; u < NCH; ++u) *reinterpret_cast<uint4*>(buf + ch_lds[u]) = pre[u];
+    for (int u = 0; u < NCH; ++u) {
+      uint4 v = pre[u];
+      // kS2Up: 4 small values -> 8 big columns, zeros at the odd ones.
+      if constexpr (S2 == kS2Up) v = make_uint4(v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16);
+      *reinterpret_cast<uint4*>(buf + ch_lds[u]) = v;
+    }
   };
 
   f32x4_t acc[K][TPW];
@@ -227,15 +271,20 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
       const uint16_t* buf = lds + (i & 1) * LR * LC;
       const int o = i - (K - 1);  // output plane completed by this input plane
       const int cs = (s + 1) % K;
-      const bool write_o = o >= 0 && o < g.TD && d0 + o < g.D;
-      const uint32_t obase = static_cast<uint32_t>(write_o ? d0 + o : 0) * static_cast<uint32_t>(plane * 2);
+      const bool write_o = o >= 0 && o < g.TD && d0 + o < g.D && (S2 != kS2Sub || !((d0 + o) & 1));
+      const uint32_t obase = S2 == kS2Sub
+                                 ? static_cast<uint32_t>(write_o ? (d0 + o) >> 1 : 0) * static_cast<uint32_t>(splane * 2)
+                                 : static_cast<uint32_t>(write_o ? d0 + o : 0) * static_cast<uint32_t>(plane * 2);
+      // kS2Up: odd input planes are all zero; kS2Sub: odd output planes are never stored.
+      const bool plane_live = S2 != kS2Up || !((d0 - P + i) & 1);
       uint16_t* const obuf = lds + 2 * LR * LC + 8 + (i & 1) * OBUF;
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int tile = wave + 4 * t;
         const int ty = tile / CT;
         const int tx = tile % CT;
-        if constexpr (BLK) {
+        if (!plane_live) {
+        } else if constexpr (BLK) {
           // Block n16 = (row n16 / 4, column n16 % 4) of the tile; lane group q
           // reads window row q (+ 4 for the second half), 8 columns from 2 to
           // the left of the block: a 4-byte aligned run.
@@ -248,6 +297,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
             const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, raw);
 #pragma unroll
             for (int kd = 0; kd < K; ++kd) {
+              if (S2 == kS2Sub && ((d0 + i - kd) & 1)) continue;  // odd output plane
               const int slot = ((s - kd) % K + K) % K;
               acc[slot][t] =
                   __builtin_amdgcn_mfma_f32_16x16x32_bf16(amat[kd][h2], bm, acc[slot][t], 0, 0, 0);
@@ -260,6 +310,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
             const bf16x8_t bm = __builtin_bit_cast(bf16x8_t, lds_read16(bp0 + kh * LC));
 #pragma unroll
             for (int kd = 0; kd < K; ++kd) {
+              if (S2 == kS2Sub && ((d0 + i - kd) & 1)) continue;  // odd output plane
               const int slot = ((s - kd) % K + K) % K;
               acc[slot][t] =
                   __builtin_amdgcn_mfma_f32_16x16x32_bf16(amat[kd][kh], bm, acc[slot][t], 0, 0, 0);
@@ -272,6 +323,14 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
                                    static_cast<__bf16>(a[2] + b0), static_cast<__bf16>(a[3] + b0)};
           if constexpr (STAGE) {
             *reinterpret_cast<bf16x4_t*>(obuf + (16 * ty + n16) * OC + 16 * tx + 4 * q) = packed;
+          } else if constexpr (S2 == kS2Sub) {
+            // Even rows keep outputs w and w + 2: small columns w / 2, w / 2 + 1.
+            const int h = th0 + 16 * ty + (BLK ? 4 * (n16 >> 2) + q : n16);
+            const int w = tw0 + 16 * tx + (BLK ? 4 * (n16 & 3) : 4 * q);
+            const bool ok = write_o && !(h & 1) && h < g.H && w < g.W;
+            const uint32_t off = ok ? obase + static_cast<uint32_t>(2 * ((h >> 1) * g.Ws + (w >> 1))) : kOob;
+            const u32x2_t words = __builtin_bit_cast(u32x2_t, packed);
+            buf_store4(yr, off, (words[0] & 0xffffu) | (words[1] << 16));
           } else {
             // Lane (n16, q) holds 4 consecutive outputs: 1-D, row n16 columns
             // 4 q ..; block, row 4 (n16 / 4) + q columns 4 (n16 % 4) ..
@@ -295,7 +354,26 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
       if constexpr (STAGE) {
         // Row-contiguous store of the plane this step completed. Buffer i & 1
         // is next written at step i + 2, after the barrier that ends step i + 1.
-        if (write_o) {
+        if (S2 == kS2Sub && write_o) {
+          // Even staged rows, even columns: 8 small outputs per 16-byte store.
+          constexpr int SCH = (TH / 2) * (TW / 16);
+#pragma unroll
+          for (int u = 0; u < (SCH + kThreads - 1) / kThreads; ++u) {
+            const int e = threadIdx.x + u * kThreads;
+            if (e < SCH) {
+              const int r = e / (TW / 16), ch = e - r * (TW / 16);
+              const int h = th0 + 2 * r, w = tw0 + 16 * ch;
+              const uint16_t* src = obuf + 2 * r * OC + 16 * ch;
+              const uint4 a = *reinterpret_cast<const uint4*>(src);
+              const uint4 b = *reinterpret_cast<const uint4*>(src + 8);
+              const uint4 v = make_uint4((a.x & 0xffffu) | (a.y << 16), (a.z & 0xffffu) | (a.w << 16),
+                                         (b.x & 0xffffu) | (b.y << 16), (b.z & 0xffffu) | (b.w << 16));
+              const uint32_t off =
+                  (h < g.H && w < g.W) ? obase + static_cast<uint32_t>(2 * ((h >> 1) * g.Ws + (w >> 1))) : kOob;
+              buf_store16(yr, off, v);
+            }
+          }
+        } else if (write_o) {
 #pragma unroll
           for (int u = 0; u < NOC; ++u) {
             const int e = threadIdx.x + u * kThreads;
@@ -387,9 +465,13 @@ struct WGeom {
   int TD;              // grad_output planes per D-chunk
   int nDc, nRBG, nCG;  // D-chunks, row-block groups, column groups per (n, c)
   int nRB, nCU;        // row blocks (nRBG * 4 / NU) and 32-column units (nCG * NU)
+  int Ds, Hs, Ws;      // UPDY: the small grad tensor dy = up(small)
 };
 
-template <int K, int NU, int PD>
+// UPDY (the stride-2 weight gradient): dy is the small tensor read as
+// up(small) on the big grid (zero at odd planes, rows and columns); the MFMAs
+// of the all-zero odd dy planes are skipped.
+template <int K, int NU, int PD, bool UPDY = false>
 __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* __restrict__ x,
                                                                  const bf16_t* __restrict__ dy,
                                                                  float* __restrict__ partial,
@@ -418,8 +500,11 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
   const uint32_t plane_bytes = static_cast<uint32_t>(plane * 2);
   const __amdgpu_buffer_rsrc_t xr =
       slab_rsrc(reinterpret_cast<const uint16_t*>(x) + nc * g.D * plane, static_cast<uint32_t>(g.D) * plane_bytes);
+  const int64_t splane = static_cast<int64_t>(g.Hs) * g.Ws;
+  const uint32_t splane_bytes = static_cast<uint32_t>(splane * 2);
+  const int64_t dslab = UPDY ? g.Ds * splane : g.D * plane;
   const __amdgpu_buffer_rsrc_t dr =
-      slab_rsrc(reinterpret_cast<const uint16_t*>(dy) + nc * g.D * plane, static_cast<uint32_t>(g.D) * plane_bytes);
+      slab_rsrc(reinterpret_cast<const uint16_t*>(dy) + nc * dslab, static_cast<uint32_t>(dslab * 2));
 
   // Fill chunks (same for every plane): x rows r0-P .. r0+DROWS+P-1, columns
   // [w0-8, w0+COLS+8) in 8-element chunks; dy rows r0 .. r0+DROWS-1, columns
@@ -446,7 +531,12 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
       const int r = e / T::DCPR, ch = e - r * T::DCPR;
       const int h = r0 + r, w = w0 + 8 * ch;
       dl[u] = r * T::DPITCH + 8 * ch;
-      if (h < g.H && w < g.W) dg[u] = 2 * (h * g.W + w);
+      if constexpr (UPDY) {
+        // Even rows only; the chunk's 8 columns hold small columns w/2 .. w/2 + 3.
+        if (!(h & 1) && (h >> 1) < g.Hs && (w >> 1) < g.Ws) dg[u] = 2 * ((h >> 1) * g.Ws + (w >> 1));
+      } else {
+        if (h < g.H && w < g.W) dg[u] = 2 * (h * g.W + w);
+      }
     }
   }
 
@@ -462,12 +552,21 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
     const bool xok = s < nsteps && t >= 0 && t < g.D;
     const uint32_t xb = static_cast<uint32_t>(xok ? t : 0) * plane_bytes;
     const int td = t + P;
-    const bool dok = s < nsteps && td >= d0 && td < dend;
-    const uint32_t dbo = static_cast<uint32_t>(dok ? td : 0) * plane_bytes;
+    const bool dok = s < nsteps && td >= d0 && td < dend && (!UPDY || (!(td & 1) && (td >> 1) < g.Ds));
+    const uint32_t dbo = UPDY ? static_cast<uint32_t>(dok ? td >> 1 : 0) * splane_bytes
+                              : static_cast<uint32_t>(dok ? td : 0) * plane_bytes;
 #pragma unroll
     for (int u = 0; u < T::NXC; ++u) p.xv[u] = buf_load16(xr, xok && xg[u] >= 0 ? xb + xg[u] : kOob);
 #pragma unroll
-    for (int u = 0; u < T::NDC; ++u) p.dv[u] = buf_load16_nt(dr, dok && dg[u] >= 0 ? dbo + dg[u] : kOob);
+    for (int u = 0; u < T::NDC; ++u) {
+      const uint32_t off = dok && dg[u] >= 0 ? dbo + dg[u] : kOob;
+      if constexpr (UPDY) {
+        const u32x2_t v = buf_load8(dr, off);
+        p.dv[u] = make_uint4(v[0], v[1], 0u, 0u);
+      } else {
+        p.dv[u] = buf_load16_nt(dr, off);
+      }
+    }
   };
   auto store = [&](int s, const Pre& p) {
     uint16_t* const xb = lds + (s & 1) * T::XBUF;
@@ -475,7 +574,12 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
 #pragma unroll
     for (int u = 0; u < T::NXC; ++u) *reinterpret_cast<uint4*>(xl[u] >= 0 ? xb + xl[u] : dummy) = p.xv[u];
 #pragma unroll
-    for (int u = 0; u < T::NDC; ++u) *reinterpret_cast<uint4*>(dl[u] >= 0 ? db + dl[u] : dummy) = p.dv[u];
+    for (int u = 0; u < T::NDC; ++u) {
+      uint4 v = p.dv[u];
+      // UPDY: 4 small values -> 8 big columns, zeros at the odd ones.
+      if constexpr (UPDY) v = make_uint4(v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16);
+      *reinterpret_cast<uint4*>(dl[u] >= 0 ? db + dl[u] : dummy) = v;
+    }
   };
 
   // This wave: unit u0 (32 columns), row block j0 of the workgroup.
@@ -539,7 +643,10 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
                           __builtin_amdgcn_alignbit(e[b + 4], e[b + 3], 16));
         }
 #pragma unroll
-        for (int kd = 0; kd < K; ++kd) acc[kw][kd] = mfma16x16x32(av, ring[kd], acc[kw][kd]);
+        for (int kd = 0; kd < K; ++kd) {
+          if (UPDY && ((d0 + st - kd) & 1)) continue;  // ring[kd] holds dy plane d0 + st - kd: odd = zero
+          acc[kw][kd] = mfma16x16x32(av, ring[kd], acc[kw][kd]);
+        }
       }
       store(st + 1, pre[jj % PD]);
       __syncthreads();
@@ -633,6 +740,41 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
   return MEDNEXT_STATUS_OK;
 }
 
+// Stride-2 maps on the stencil: kS2Sub (gather: forward taps over big, small
+// output) or kS2Up (scatter: flipped taps over up(small), big output).
+template <int K, int S2, int CT>
+int launch_stencil_s2(const void* x, const void* wt, const void* bias, void* y, const MGeom& g, int64_t blocks,
+                      hipStream_t st) {
+  constexpr int P = K / 2;
+  constexpr int PD = K == 3 ? 4 : 2;
+  constexpr bool FLIP = S2 == kS2Up;
+  constexpr size_t stage = stencil_stages_output(K) ? static_cast<size_t>(2) * (16 * kRT) * (16 * CT + 8) : 0;
+  constexpr size_t lds = (static_cast<size_t>(2) * (16 * kRT + 2 * P) * stencil_pitch(K, CT) + 8 + stage) * 2;
+  auto px = static_cast<const bf16_t*>(x);
+  auto pw = static_cast<const bf16_t*>(wt);
+  auto pb = static_cast<const bf16_t*>(bias);
+  auto py = static_cast<bf16_t*>(y);
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
+  if (bias)
+    hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, true, CT, PD, false, S2>), grid, block, lds, st, px, pw, pb,
+                       py, g, nullptr);
+  else
+    hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, false, CT, PD, false, S2>), grid, block, lds, st, px, pw,
+                       pb, py, g, nullptr);
+  MEDNEXT_CHECK_LAUNCH();
+  return MEDNEXT_STATUS_OK;
+}
+
+template <int K, int S2>
+int launch_stencil_s2_ct(const void* x, const void* wt, const void* bias, void* y, const MGeom& g, int tile_cols,
+                         int64_t blocks, hipStream_t st) {
+  switch (tile_cols) {
+    case 32: return launch_stencil_s2<K, S2, 2>(x, wt, bias, y, g, blocks, st);
+    case 64: return launch_stencil_s2<K, S2, 4>(x, wt, bias, y, g, blocks, st);
+    default: return launch_stencil_s2<K, S2, 8>(x, wt, bias, y, g, blocks, st);
+  }
+}
+
 template <int K, bool FLIP>
 int launch_stencil_ct(const void* x, const void* wt, const void* bias, void* y, const MGeom& g,
                       int tile_cols, int64_t blocks, hipStream_t st, const void* acc) {
@@ -645,15 +787,32 @@ int launch_stencil_ct(const void* x, const void* wt, const void* bias, void* y, 
 }
 
 
-template <int K, int NU>
+template <int K, int NU, bool UPDY = false>
 int launch_wgrad(const void* x, const void* dy, float* partial, const WGeom& g, int64_t blocks, int splits,
                  hipStream_t st) {
   constexpr int PD = 2;
   const size_t lds = WgradTile<K, NU>::BYTES;
-  hipLaunchKernelGGL((dw_mfma_wgrad_kernel<K, NU, PD>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), lds,
-                     st, static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(dy), partial, g, splits);
+  hipLaunchKernelGGL((dw_mfma_wgrad_kernel<K, NU, PD, UPDY>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
+                     lds, st, static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(dy), partial, g, splits);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
+}
+
+template <bool UPDY>
+int launch_wgrad_k(const void* x, const void* dy, float* partial, const WGeom& g, int k, int tile_cols,
+                   int64_t blocks, int splits, hipStream_t st) {
+  if (k == 3) {
+    switch (tile_cols) {
+      case 32: return launch_wgrad<3, 1, UPDY>(x, dy, partial, g, blocks, splits, st);
+      case 64: return launch_wgrad<3, 2, UPDY>(x, dy, partial, g, blocks, splits, st);
+      default: return launch_wgrad<3, 4, UPDY>(x, dy, partial, g, blocks, splits, st);
+    }
+  }
+  switch (tile_cols) {
+    case 32: return launch_wgrad<5, 1, UPDY>(x, dy, partial, g, blocks, splits, st);
+    case 64: return launch_wgrad<5, 2, UPDY>(x, dy, partial, g, blocks, splits, st);
+    default: return launch_wgrad<5, 4, UPDY>(x, dy, partial, g, blocks, splits, st);
+  }
 }
 
 int plan_wgrad(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int tile_cols,
@@ -729,18 +888,104 @@ int dw_mfma_wgrad(const void* x, const void* dy, float* partial, int64_t n, int6
   int splits = 0;
   const int status = plan_wgrad(n, c, d, h, w, k, tile_cols, depth_chunk, &g, &blocks, &splits);
   if (status != MEDNEXT_STATUS_OK) return status;
-  if (k == 3) {
-    switch (tile_cols) {
-      case 32: return launch_wgrad<3, 1>(x, dy, partial, g, blocks, splits, st);
-      case 64: return launch_wgrad<3, 2>(x, dy, partial, g, blocks, splits, st);
-      default: return launch_wgrad<3, 4>(x, dy, partial, g, blocks, splits, st);
-    }
-  }
-  switch (tile_cols) {
-    case 32: return launch_wgrad<5, 1>(x, dy, partial, g, blocks, splits, st);
-    case 64: return launch_wgrad<5, 2>(x, dy, partial, g, blocks, splits, st);
-    default: return launch_wgrad<5, 4>(x, dy, partial, g, blocks, splits, st);
-  }
+  return launch_wgrad_k<false>(x, dy, partial, g, k, tile_cols, blocks, splits, st);
+}
+
+// ------------------------------------------------------------------ stride 2
+
+namespace {
+
+// Launch shapes of the stride-2 maps (no recipe argument: the entry points
+// keep the reference's signature). Stencil: the widest tile the row allows and
+// D-runs for ~2 workgroups per CU, as for the stride-1 stencil. Weight
+// gradient: the stride-1 weight gradient's targets (2.5 workgroups per CU for
+// k = 3, 2 for k = 5).
+constexpr int64_t kS2StencilTarget = 2 * 256;
+
+int s2_tile_cols(int64_t wb) { return wb >= 128 ? 128 : wb >= 64 ? 64 : 32; }
+
+int s2_depth_chunk(int64_t db, int64_t slabs, int64_t target) {
+  const int64_t chunks = std::max<int64_t>(1, cdiv(target, std::max<int64_t>(1, slabs)));
+  return static_cast<int>(std::max<int64_t>(2, cdiv(db, chunks)));
+}
+
+int s2_stencil_geom(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws,
+                    MGeom* g, int* tile_cols, int64_t* blocks) {
+  *tile_cols = s2_tile_cols(wb);
+  const int64_t slabs = n * c * cdiv(hb, int64_t(16 * kRT)) * cdiv(wb, int64_t(*tile_cols));
+  if (int st = make_geom(c, db, hb, wb, *tile_cols, s2_depth_chunk(db, slabs, kS2StencilTarget), g)) return st;
+  g->Ds = static_cast<int>(ds);
+  g->Hs = static_cast<int>(hs);
+  g->Ws = static_cast<int>(ws);
+  *blocks = n * c * g->nDc * g->nHt * g->nWt;
+  MEDNEXT_CHECK_ARG(*blocks < (int64_t(1) << 31), "grid too large");
+  return MEDNEXT_STATUS_OK;
+}
+
+int s2_wgrad_geom(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws,
+                  int k, WGeom* g, int* tile_cols, int64_t* blocks, int* splits) {
+  *tile_cols = s2_tile_cols(wb);
+  const int64_t rows = int64_t(16 - (k - 1)) * (4 / (*tile_cols / 32));
+  const int64_t slabs = n * c * cdiv(hb, rows) * cdiv(wb, int64_t(*tile_cols));
+  const int64_t target = k == 3 ? 5 * 256 / 2 : 2 * 256;
+  const int dc = s2_depth_chunk(db, slabs, target);
+  if (int st = plan_wgrad(n, c, db, hb, wb, k, *tile_cols, dc, g, blocks, splits)) return st;
+  g->Ds = static_cast<int>(ds);
+  g->Hs = static_cast<int>(hs);
+  g->Ws = static_cast<int>(ws);
+  return MEDNEXT_STATUS_OK;
+}
+
+}  // namespace
+
+bool dw_mfma_s2_supported(int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k) {
+  // Even big dims with small = big / 2 (the down block), rows of whole
+  // 16-column pieces (8 small columns per staged store), and the stride-1
+  // kernels' own limits on the big grid (the weight gradient's W % 32 too).
+  return (k == 3 || k == 5) && db % 2 == 0 && hb % 2 == 0 && wb % 32 == 0 && ds * 2 == db && hs * 2 == hb &&
+         ws * 2 == wb && dw_mfma_supported(db, hb, wb, k);
+}
+
+int dw_mfma_s2_gather(const void* big, const void* weight, const void* bias, void* small, int64_t n, int64_t c,
+                      int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k, hipStream_t st) {
+  MEDNEXT_CHECK_ARG(dw_mfma_s2_supported(db, hb, wb, ds, hs, ws, k), "shape not supported by the MFMA stride-2 maps");
+  MGeom g{};
+  int tile_cols = 0;
+  int64_t blocks = 0;
+  if (int s = s2_stencil_geom(n, c, db, hb, wb, ds, hs, ws, &g, &tile_cols, &blocks)) return s;
+  return k == 3 ? launch_stencil_s2_ct<3, kS2Sub>(big, weight, bias, small, g, tile_cols, blocks, st)
+                : launch_stencil_s2_ct<5, kS2Sub>(big, weight, bias, small, g, tile_cols, blocks, st);
+}
+
+int dw_mfma_s2_scatter(const void* small, const void* weight, const void* bias, void* big, int64_t n, int64_t c,
+                       int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k, hipStream_t st) {
+  MEDNEXT_CHECK_ARG(dw_mfma_s2_supported(db, hb, wb, ds, hs, ws, k), "shape not supported by the MFMA stride-2 maps");
+  MGeom g{};
+  int tile_cols = 0;
+  int64_t blocks = 0;
+  if (int s = s2_stencil_geom(n, c, db, hb, wb, ds, hs, ws, &g, &tile_cols, &blocks)) return s;
+  return k == 3 ? launch_stencil_s2_ct<3, kS2Up>(small, weight, bias, big, g, tile_cols, blocks, st)
+                : launch_stencil_s2_ct<5, kS2Up>(small, weight, bias, big, g, tile_cols, blocks, st);
+}
+
+int dw_mfma_s2_wgrad_splits(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs,
+                            int64_t ws, int k) {
+  if (!dw_mfma_s2_supported(db, hb, wb, ds, hs, ws, k)) return 0;
+  WGeom g{};
+  int tile_cols = 0, splits = 0;
+  int64_t blocks = 0;
+  if (s2_wgrad_geom(n, c, db, hb, wb, ds, hs, ws, k, &g, &tile_cols, &blocks, &splits) != MEDNEXT_STATUS_OK) return 0;
+  return splits;
+}
+
+int dw_mfma_s2_wgrad(const void* big, const void* small, float* partial, int64_t n, int64_t c, int64_t db, int64_t hb,
+                     int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k, hipStream_t st) {
+  MEDNEXT_CHECK_ARG(dw_mfma_s2_supported(db, hb, wb, ds, hs, ws, k), "shape not supported by the MFMA stride-2 maps");
+  WGeom g{};
+  int tile_cols = 0, splits = 0;
+  int64_t blocks = 0;
+  if (int s = s2_wgrad_geom(n, c, db, hb, wb, ds, hs, ws, k, &g, &tile_cols, &blocks, &splits)) return s;
+  return launch_wgrad_k<true>(big, small, partial, g, k, tile_cols, blocks, splits, st);
 }
 
 }  // namespace mednext

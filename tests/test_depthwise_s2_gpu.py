@@ -90,7 +90,35 @@ def test_maps_band_and_row_paths(n, c, big, k):
     assert max_rel(dw, want_dw) <= FP32_WGRAD and max_rel(ds, want_db) <= FP32_WGRAD
 
 
-DOWN_UP = [(32, 128, 3), (64, 64, 3), (128, 32, 3), (64, 64, 5)]
+@pytest.mark.parametrize("k", [3, 5])
+@pytest.mark.parametrize("n,c,big", [(2, 3, (6, 48, 64)), (1, 2, (10, 34, 96)), (1, 1, (4, 32, 32 * 9))])
+def test_mfma_route_maps_against_oracle(n, c, big, k):
+    """bf16 maps whose small plane exceeds the band kernels (even big dims,
+    W % 32 == 0): the matrix-core stencil with the output subsampled (gather),
+    over the zero-upsampled small tensor (scatter), and the weight gradient
+    with dy upsampled. Batch 2, row tiles past H (34, 48 rows), column tiles
+    past W (96 with 64-column tiles), short D-runs."""
+    print(f"[s2 mfma maps] n={n} c={c} big={big} k={k}", flush=True)
+    gen = torch.Generator().manual_seed(7 * k + sum(big))
+    dtype = torch.bfloat16
+    small = tuple(s // 2 for s in big)
+    x = rounded((n, c, *big), gen, dtype)
+    w = rounded((c, 1, k, k, k), gen, dtype, 1.0 / k)
+    b = rounded((c,), gen, dtype)
+    g = rounded((n, c, *small), gen, dtype)
+    y = hip_ops.depthwise_s2_gather(x.to(DEV), w.to(DEV), b.to(DEV), small)
+    assert max_rel(y, odw.strided_forward(f64(x), f64(w), f64(b))) <= BF16
+    dx = hip_ops.depthwise_s2_scatter(g.to(DEV), w.to(DEV), b.to(DEV), big)
+    want_dx = odw.strided_input_grad(f64(g), f64(w), big) + f64(b).reshape(1, c, 1, 1, 1)
+    assert max_rel(dx, want_dx) <= BF16
+    dw, ds = hip_ops.depthwise_s2_wgrad(x.to(DEV), g.to(DEV), k)
+    want_dw, want_db = odw.strided_weight_grad(f64(x), f64(g), k)
+    assert max_rel(dw, want_dw) <= BF16 and max_rel(ds, want_db) <= BF16
+    dw2, _ = hip_ops.depthwise_s2_wgrad(x.to(DEV), g.to(DEV), k)
+    assert torch.equal(dw, dw2)
+
+
+DOWN_UP = [(32, 128, 3), (64, 64, 3), (128, 32, 3), (64, 64, 5), (32, 128, 5)]
 
 
 @pytest.mark.parametrize("channels,size,k", DOWN_UP)
