@@ -95,6 +95,9 @@ __device__ inline uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 __device__ inline u32x2_t buf_load8(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
 }
+__device__ inline void buf_store2(__amdgpu_buffer_rsrc_t r, uint32_t off, uint16_t v) {
+  __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
+}
 __device__ inline void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t v) {
   __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
 }
@@ -105,6 +108,26 @@ __device__ inline void buf_store8(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32
 __device__ inline void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
   const u32x4_t w = {v.x, v.y, v.z, v.w};
   __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, 0);
+}
+
+// 8 consecutive bf16 starting at element e of a tensor whose rows have odd
+// width, of which the first `valid` are real (the rest read zero). Such rows
+// start at any 2-byte boundary, and so may a tensor or slab holding an odd
+// number of elements, while multi-byte buffer loads drop the address bits
+// below their size: the run is read as eight 2-byte loads (run8_load, issued
+// early) and packed once the data is needed (run8_pack).
+struct Run8 {
+  uint32_t h[8];
+};
+__device__ inline Run8 run8_load(__amdgpu_buffer_rsrc_t r, uint32_t e, int valid) {
+  Run8 o;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o.h[j] = __builtin_amdgcn_raw_buffer_load_b16(r, j < valid ? (e + j) * 2u : kOob, 0, 0);
+  return o;
+}
+__device__ inline uint4 run8_pack(const Run8& p) {
+  return make_uint4(p.h[0] | (p.h[1] << 16), p.h[2] | (p.h[3] << 16), p.h[4] | (p.h[5] << 16),
+                    p.h[6] | (p.h[7] << 16));
 }
 
 // MI355X dispatches workgroup i to XCD i % 8, and each XCD has its own L2.

@@ -32,8 +32,9 @@ int dw_mfma_wgrad(const void* x, const void* dy, float* partial, int64_t n, int6
 // gather small[o] = b + sum_t w[t] big[2o + t - p], scatter big[i] = b +
 // sum_{2o + t - p = i} w[t] small[o], and the weight gradient dW[t] = sum_o
 // big[2o + t - p] small[o] (+ dB = sum small) into [C][k^3 + 1][splits] fp32
-// partials. Supported: k in {3, 5}, even big dims with small = big / 2,
-// W % 32 == 0 and the stride-1 limits on the big grid.
+// partials. Supported: k in {3, 5}, big = 2 * small or 2 * small - 1 per
+// dimension (down block / up block), H, W >= 32, even big W a multiple of 32,
+// odd big W with a small W multiple of 8, slabs < 2 GiB.
 bool dw_mfma_s2_supported(int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k);
 int dw_mfma_s2_gather(const void* big, const void* weight, const void* bias, void* small, int64_t n, int64_t c,
                       int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k, hipStream_t st);

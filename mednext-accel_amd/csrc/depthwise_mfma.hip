@@ -106,7 +106,10 @@ __device__ inline uint4 lds_read16(const uint16_t* p) { return *reinterpret_cast
 // like y (the gradient that reaches the same input through the block's
 // residual), added to the bf16-rounded stencil value in fp32 and rounded
 // again, exactly as a separate bf16 add would.
-template <int K, bool FLIP, bool BIAS, int CT, int PD, bool ACC = false, int S2 = kS2None>
+// EW (stride-2 modes on big tensors of odd width, the up block's 2s - 1):
+// the big tensor's rows are not 16-byte aligned, so kS2Sub reads it with
+// run8_load / run8_pack and kS2Up writes it with 2-byte stores.
+template <int K, bool FLIP, bool BIAS, int CT, int PD, bool ACC = false, int S2 = kS2None, bool EW = false>
 __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t* __restrict__ x,
                                                                    const bf16_t* __restrict__ wt,
                                                                    const bf16_t* __restrict__ bias,
@@ -131,6 +134,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   constexpr bool STAGE = stencil_stages_output(K);
   static_assert(!(BLK && STAGE), "the block-Toeplitz form stores its outputs directly");
   static_assert(S2 == kS2None || !ACC, "stride-2 modes take no accumulation input");
+  static_assert(!EW || S2 != kS2None, "element-exact rows are for the stride-2 modes");
   constexpr int OC = TW + 8;           // output staging row pitch (elements)
   constexpr int OBUF = TH * OC;
   constexpr int OCH = TH * (TW / 8);   // 16-byte output chunks per plane
@@ -186,29 +190,39 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   const f32x4_t acc_init = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // Per-thread chunk coordinates of the fill (the same for every plane).
-  // Threads without a chunk write a dummy LDS slot past the two buffers.
+  // Threads without a chunk (ch_lds -1) write the 16-byte sink that follows
+  // the two plane buffers, at a fixed address: an offset from the buffer being
+  // filled would land 2 * LR * LC elements past the second one, inside the
+  // output staging tile (or past the allocation without one).
   const __amdgpu_buffer_rsrc_t xr = slab_rsrc(xnc, static_cast<uint32_t>(in_slab * 2));
   const __amdgpu_buffer_rsrc_t yr = slab_rsrc(ync, static_cast<uint32_t>(out_slab * 2));
   const __amdgpu_buffer_rsrc_t ar =
       slab_rsrc(ACC ? reinterpret_cast<const uint16_t*>(acc_in) + bp.nc * g.D * plane : ync,
                 ACC ? static_cast<uint32_t>(g.D * plane * 2) : 0u);
-  int ch_off[NCH];  // byte offset inside a plane, or -1 outside the plane
+  int ch_off[NCH];  // byte offset inside a plane (EW: element index), or -1 outside the plane
   int ch_lds[NCH];  // LDS element offset
+  int ch_val[NCH];  // EW: elements of the chunk inside the row (1..8)
 #pragma unroll
   for (int u = 0; u < NCH; ++u) {
     const int e = threadIdx.x + u * kThreads;
     ch_off[u] = -1;
-    ch_lds[u] = 2 * LR * LC;
+    ch_lds[u] = -1;
     if (e < NCHUNK) {
       const int r = e / CPR;
       const int ch = e - r * CPR;
       const int h = th0 - P + r;
       const int w = tw0 - 8 + 8 * ch;
       ch_lds[u] = r * LC + 8 * ch;
+      ch_val[u] = 0;
       if constexpr (S2 == kS2Up) {
         // Even rows only; the chunk's 8 columns hold small columns w/2 .. w/2 + 3.
         if (h >= 0 && !(h & 1) && (h >> 1) < g.Hs && w >= 0 && (w >> 1) < g.Ws)
           ch_off[u] = 2 * ((h >> 1) * g.Ws + (w >> 1));
+      } else if constexpr (EW) {
+        if (h >= 0 && h < g.H && w >= 0 && w < g.W) {
+          ch_off[u] = h * g.W + w;
+          ch_val[u] = min(8, g.W - w);
+        }
       } else {
         if (h >= 0 && h < g.H && w >= 0 && w < g.W) ch_off[u] = 2 * (h * g.W + w);
       }
@@ -217,9 +231,15 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   const int nplanes = g.TD + K - 1;
   // Input plane j of this workgroup (absolute d0 - P + j); planes outside the
   // volume or past this workgroup's range read as zeros without touching memory.
-  auto load_plane = [&](int j, uint4* pre) {
+  auto load_plane = [&](int j, uint4* pre, Run8* run) {
     const int di = d0 - P + j;
-    if constexpr (S2 == kS2Up) {
+    if constexpr (EW && S2 == kS2Sub) {
+      const bool plane_ok = j < nplanes && di >= 0 && di < g.D;
+      const uint32_t pe = static_cast<uint32_t>(plane_ok ? di : 0) * static_cast<uint32_t>(plane);
+#pragma unroll
+      for (int u = 0; u < NCH; ++u)
+        run[u] = run8_load(xr, pe + static_cast<uint32_t>(ch_off[u]), plane_ok && ch_off[u] >= 0 ? ch_val[u] : 0);
+    } else if constexpr (S2 == kS2Up) {
       // Odd planes of up(small) are zero; even plane di is small plane di / 2.
       const bool plane_ok = j < nplanes && di >= 0 && !(di & 1) && (di >> 1) < g.Ds;
       const uint32_t pbase = static_cast<uint32_t>(plane_ok ? di >> 1 : 0) * static_cast<uint32_t>(splane * 2);
@@ -239,13 +259,19 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
       }
     }
   };
-  auto store_plane = [&](uint16_t* buf, const uint4* pre) {
+  auto store_plane = [&](uint16_t* buf, const uint4* pre, const Run8* run) {
 #pragma unroll
     for (int u = 0; u < NCH; ++u) {
-      uint4 v = pre[u];
-      // kS2Up: 4 small values -> 8 big columns, zeros at the odd ones.
-      if constexpr (S2 == kS2Up) v = make_uint4(v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16);
-      *reinterpret_cast<uint4*>(buf + ch_lds[u]) = v;
+      uint4 v;
+      if constexpr (EW && S2 == kS2Sub) {
+        v = run8_pack(run[u]);
+      } else if constexpr (S2 == kS2Up) {
+        // 4 small values -> 8 big columns, zeros at the odd ones.
+        v = make_uint4(pre[u].x & 0xffffu, pre[u].x >> 16, pre[u].y & 0xffffu, pre[u].y >> 16);
+      } else {
+        v = pre[u];
+      }
+      *reinterpret_cast<uint4*>(ch_lds[u] >= 0 ? buf + ch_lds[u] : lds + 2 * LR * LC) = v;
     }
   };
 
@@ -255,11 +281,13 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
 #pragma unroll
     for (int t = 0; t < TPW; ++t) acc[s][t] = acc_init;
 
-  uint4 pre[PD][NCH];
-  load_plane(0, pre[0]);
-  store_plane(lds, pre[0]);
+  constexpr bool RUNS = EW && S2 == kS2Sub;
+  uint4 pre[PD][RUNS ? 1 : NCH];
+  Run8 run[PD][RUNS ? NCH : 1];  // EW: the 2-byte loads of each chunk
+  load_plane(0, pre[0], run[0]);
+  store_plane(lds, pre[0], run[0]);
 #pragma unroll
-  for (int j = 1; j < PD; ++j) load_plane(j, pre[(j - 1) % PD]);
+  for (int j = 1; j < PD; ++j) load_plane(j, pre[(j - 1) % PD], run[(j - 1) % PD]);
   __syncthreads();
 
   for (int q0 = 0; q0 < nplanes; q0 += U) {
@@ -267,7 +295,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
     for (int s = 0; s < U; ++s) {
       const int i = q0 + s;
       if (i >= nplanes) break;
-      load_plane(i + PD, pre[(s + PD - 1) % PD]);
+      load_plane(i + PD, pre[(s + PD - 1) % PD], run[(s + PD - 1) % PD]);
       const uint16_t* buf = lds + (i & 1) * LR * LC;
       const int o = i - (K - 1);  // output plane completed by this input plane
       const int cs = (s + 1) % K;
@@ -323,6 +351,16 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
                                    static_cast<__bf16>(a[2] + b0), static_cast<__bf16>(a[3] + b0)};
           if constexpr (STAGE) {
             *reinterpret_cast<bf16x4_t*>(obuf + (16 * ty + n16) * OC + 16 * tx + 4 * q) = packed;
+          } else if constexpr (EW && S2 == kS2Up) {
+            // Odd row width: the outputs inside the row, 2 bytes each.
+            const int h = th0 + 16 * ty + (BLK ? 4 * (n16 >> 2) + q : n16);
+            const int w = tw0 + 16 * tx + (BLK ? 4 * (n16 & 3) : 4 * q);
+            const int valid = (write_o && h < g.H && w < g.W) ? min(4, g.W - w) : 0;
+            const u32x2_t words = __builtin_bit_cast(u32x2_t, packed);
+            const uint32_t off = obase + static_cast<uint32_t>(2 * (h * g.W + w));
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (e < valid) buf_store2(yr, off + 2 * e, static_cast<uint16_t>(words[e >> 1] >> (16 * (e & 1))));
           } else if constexpr (S2 == kS2Sub) {
             // Even rows keep outputs w and w + 2: small columns w / 2, w / 2 + 1.
             const int h = th0 + 16 * ty + (BLK ? 4 * (n16 >> 2) + q : n16);
@@ -349,7 +387,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
         }
         acc[cs][t] = acc_init;
       }
-      store_plane(lds + ((i + 1) & 1) * LR * LC, pre[s % PD]);
+      store_plane(lds + ((i + 1) & 1) * LR * LC, pre[s % PD], run[s % PD]);
       __syncthreads();
       if constexpr (STAGE) {
         // Row-contiguous store of the plane this step completed. Buffer i & 1
@@ -371,6 +409,22 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
               const uint32_t off =
                   (h < g.H && w < g.W) ? obase + static_cast<uint32_t>(2 * ((h >> 1) * g.Ws + (w >> 1))) : kOob;
               buf_store16(yr, off, v);
+            }
+          }
+        } else if (EW && S2 == kS2Up && write_o) {
+          // Odd row width: the staged row pieces inside the row, 2 bytes each.
+#pragma unroll
+          for (int u = 0; u < NOC; ++u) {
+            const int e = threadIdx.x + u * kThreads;
+            if (e < OCH) {
+              const int r = e / (TW / 8), ch = e - r * (TW / 8);
+              const int h = th0 + r, w = tw0 + 8 * ch;
+              const int valid = (h < g.H && w < g.W) ? min(8, g.W - w) : 0;
+              const uint16_t* src = obuf + r * OC + 8 * ch;
+              const uint32_t off = obase + static_cast<uint32_t>(2 * (h * g.W + w));
+#pragma unroll
+              for (int el = 0; el < 8; ++el)
+                if (el < valid) buf_store2(yr, off + 2 * el, src[el]);
             }
           }
         } else if (write_o) {
@@ -471,7 +525,9 @@ struct WGeom {
 // UPDY (the stride-2 weight gradient): dy is the small tensor read as
 // up(small) on the big grid (zero at odd planes, rows and columns); the MFMAs
 // of the all-zero odd dy planes are skipped.
-template <int K, int NU, int PD, bool UPDY = false>
+// EW: x rows of odd width (the up block's 2s - 1 grad_output), read with
+// run8_load / run8_pack.
+template <int K, int NU, int PD, bool UPDY = false, bool EW = false>
 __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* __restrict__ x,
                                                                  const bf16_t* __restrict__ dy,
                                                                  float* __restrict__ partial,
@@ -510,16 +566,25 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
   // [w0-8, w0+COLS+8) in 8-element chunks; dy rows r0 .. r0+DROWS-1, columns
   // [w0, w0+COLS). Byte offsets inside a plane, -1 outside it.
   int xg[T::NXC], xl[T::NXC], dg[T::NDC], dl[T::NDC];
+  int xv[EW ? T::NXC : 1];  // EW: elements of the chunk inside the row
 #pragma unroll
   for (int u = 0; u < T::NXC; ++u) {
     const int e = threadIdx.x + u * kThreads;
     xg[u] = -1;
     xl[u] = -1;
+    if constexpr (EW) xv[u] = 0;
     if (e < T::XROWS * T::XCPR) {
       const int r = e / T::XCPR, ch = e - r * T::XCPR;
       const int h = r0 - P + r, w = w0 - 8 + 8 * ch;
       xl[u] = r * T::XPITCH + 8 * ch;
-      if (h >= 0 && h < g.H && w >= 0 && w < g.W) xg[u] = 2 * (h * g.W + w);
+      if (h >= 0 && h < g.H && w >= 0 && w < g.W) {
+        if constexpr (EW) {
+          xg[u] = h * g.W + w;  // element index
+          xv[u] = min(8, g.W - w);
+        } else {
+          xg[u] = 2 * (h * g.W + w);
+        }
+      }
     }
   }
 #pragma unroll
@@ -544,8 +609,9 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
   // the ring); each is zero outside its valid range.
   const int nsteps = (dend - d0) + 2 * P;
   struct Pre {
-    uint4 xv[T::NXC];
+    uint4 xv[EW ? 1 : T::NXC];
     uint4 dv[T::NDC];
+    Run8 xr8[EW ? T::NXC : 1];  // EW: the 2-byte loads of each x chunk
   };
   auto load = [&](int s, Pre& p) {
     const int t = d0 - P + s;
@@ -556,7 +622,14 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
     const uint32_t dbo = UPDY ? static_cast<uint32_t>(dok ? td >> 1 : 0) * splane_bytes
                               : static_cast<uint32_t>(dok ? td : 0) * plane_bytes;
 #pragma unroll
-    for (int u = 0; u < T::NXC; ++u) p.xv[u] = buf_load16(xr, xok && xg[u] >= 0 ? xb + xg[u] : kOob);
+    for (int u = 0; u < T::NXC; ++u) {
+      if constexpr (EW) {
+        const uint32_t pe = static_cast<uint32_t>(xok ? t : 0) * static_cast<uint32_t>(plane);
+        p.xr8[u] = run8_load(xr, pe + static_cast<uint32_t>(xg[u]), xok && xg[u] >= 0 ? xv[u] : 0);
+      } else {
+        p.xv[u] = buf_load16(xr, xok && xg[u] >= 0 ? xb + xg[u] : kOob);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < T::NDC; ++u) {
       const uint32_t off = dok && dg[u] >= 0 ? dbo + dg[u] : kOob;
@@ -572,7 +645,15 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
     uint16_t* const xb = lds + (s & 1) * T::XBUF;
     uint16_t* const db = dlds + (s & 1) * T::DBUF;
 #pragma unroll
-    for (int u = 0; u < T::NXC; ++u) *reinterpret_cast<uint4*>(xl[u] >= 0 ? xb + xl[u] : dummy) = p.xv[u];
+    for (int u = 0; u < T::NXC; ++u) {
+      uint4 v;
+      if constexpr (EW) {
+        v = run8_pack(p.xr8[u]);
+      } else {
+        v = p.xv[u];
+      }
+      *reinterpret_cast<uint4*>(xl[u] >= 0 ? xb + xl[u] : dummy) = v;
+    }
 #pragma unroll
     for (int u = 0; u < T::NDC; ++u) {
       uint4 v = p.dv[u];
@@ -742,11 +823,11 @@ int launch_stencil(const void* x, const void* wt, const void* bias, void* y, con
 
 // Stride-2 maps on the stencil: kS2Sub (gather: forward taps over big, small
 // output) or kS2Up (scatter: flipped taps over up(small), big output).
-template <int K, int S2, int CT>
+template <int K, int S2, int CT, bool EW>
 int launch_stencil_s2(const void* x, const void* wt, const void* bias, void* y, const MGeom& g, int64_t blocks,
                       hipStream_t st) {
   constexpr int P = K / 2;
-  constexpr int PD = K == 3 ? 4 : 2;
+  constexpr int PD = K == 3 && !(EW && S2 == kS2Sub) ? 4 : 2;  // 2-byte runs hold 8 registers per chunk
   constexpr bool FLIP = S2 == kS2Up;
   constexpr size_t stage = stencil_stages_output(K) ? static_cast<size_t>(2) * (16 * kRT) * (16 * CT + 8) : 0;
   constexpr size_t lds = (static_cast<size_t>(2) * (16 * kRT + 2 * P) * stencil_pitch(K, CT) + 8 + stage) * 2;
@@ -756,23 +837,33 @@ int launch_stencil_s2(const void* x, const void* wt, const void* bias, void* y, 
   auto py = static_cast<bf16_t*>(y);
   const dim3 grid(static_cast<unsigned>(blocks)), block(kThreads);
   if (bias)
-    hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, true, CT, PD, false, S2>), grid, block, lds, st, px, pw, pb,
-                       py, g, nullptr);
+    hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, true, CT, PD, false, S2, EW>), grid, block, lds, st, px, pw,
+                       pb, py, g, nullptr);
   else
-    hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, false, CT, PD, false, S2>), grid, block, lds, st, px, pw,
+    hipLaunchKernelGGL((dw_mfma_stencil_kernel<K, FLIP, false, CT, PD, false, S2, EW>), grid, block, lds, st, px, pw,
                        pb, py, g, nullptr);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }
 
-template <int K, int S2>
+template <int K, int S2, bool EW>
 int launch_stencil_s2_ct(const void* x, const void* wt, const void* bias, void* y, const MGeom& g, int tile_cols,
                          int64_t blocks, hipStream_t st) {
   switch (tile_cols) {
-    case 32: return launch_stencil_s2<K, S2, 2>(x, wt, bias, y, g, blocks, st);
-    case 64: return launch_stencil_s2<K, S2, 4>(x, wt, bias, y, g, blocks, st);
-    default: return launch_stencil_s2<K, S2, 8>(x, wt, bias, y, g, blocks, st);
+    case 32: return launch_stencil_s2<K, S2, 2, EW>(x, wt, bias, y, g, blocks, st);
+    case 64: return launch_stencil_s2<K, S2, 4, EW>(x, wt, bias, y, g, blocks, st);
+    default: return launch_stencil_s2<K, S2, 8, EW>(x, wt, bias, y, g, blocks, st);
   }
+}
+
+template <int S2>
+int launch_stencil_s2_k(const void* x, const void* wt, const void* bias, void* y, const MGeom& g, int k, bool ew,
+                        int tile_cols, int64_t blocks, hipStream_t st) {
+  if (k == 3)
+    return ew ? launch_stencil_s2_ct<3, S2, true>(x, wt, bias, y, g, tile_cols, blocks, st)
+              : launch_stencil_s2_ct<3, S2, false>(x, wt, bias, y, g, tile_cols, blocks, st);
+  return ew ? launch_stencil_s2_ct<5, S2, true>(x, wt, bias, y, g, tile_cols, blocks, st)
+            : launch_stencil_s2_ct<5, S2, false>(x, wt, bias, y, g, tile_cols, blocks, st);
 }
 
 template <int K, bool FLIP>
@@ -787,37 +878,40 @@ int launch_stencil_ct(const void* x, const void* wt, const void* bias, void* y, 
 }
 
 
-template <int K, int NU, bool UPDY = false>
+template <int K, int NU, bool UPDY = false, bool EW = false>
 int launch_wgrad(const void* x, const void* dy, float* partial, const WGeom& g, int64_t blocks, int splits,
                  hipStream_t st) {
   constexpr int PD = 2;
   const size_t lds = WgradTile<K, NU>::BYTES;
-  hipLaunchKernelGGL((dw_mfma_wgrad_kernel<K, NU, PD, UPDY>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads),
-                     lds, st, static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(dy), partial, g, splits);
+  hipLaunchKernelGGL((dw_mfma_wgrad_kernel<K, NU, PD, UPDY, EW>), dim3(static_cast<unsigned>(blocks)),
+                     dim3(kThreads), lds, st, static_cast<const bf16_t*>(x), static_cast<const bf16_t*>(dy), partial,
+                     g, splits);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }
 
-template <bool UPDY>
+template <bool UPDY, bool EW = false>
 int launch_wgrad_k(const void* x, const void* dy, float* partial, const WGeom& g, int k, int tile_cols,
                    int64_t blocks, int splits, hipStream_t st) {
   if (k == 3) {
     switch (tile_cols) {
-      case 32: return launch_wgrad<3, 1, UPDY>(x, dy, partial, g, blocks, splits, st);
-      case 64: return launch_wgrad<3, 2, UPDY>(x, dy, partial, g, blocks, splits, st);
-      default: return launch_wgrad<3, 4, UPDY>(x, dy, partial, g, blocks, splits, st);
+      case 32: return launch_wgrad<3, 1, UPDY, EW>(x, dy, partial, g, blocks, splits, st);
+      case 64: return launch_wgrad<3, 2, UPDY, EW>(x, dy, partial, g, blocks, splits, st);
+      default: return launch_wgrad<3, 4, UPDY, EW>(x, dy, partial, g, blocks, splits, st);
     }
   }
   switch (tile_cols) {
-    case 32: return launch_wgrad<5, 1, UPDY>(x, dy, partial, g, blocks, splits, st);
-    case 64: return launch_wgrad<5, 2, UPDY>(x, dy, partial, g, blocks, splits, st);
-    default: return launch_wgrad<5, 4, UPDY>(x, dy, partial, g, blocks, splits, st);
+    case 32: return launch_wgrad<5, 1, UPDY, EW>(x, dy, partial, g, blocks, splits, st);
+    case 64: return launch_wgrad<5, 2, UPDY, EW>(x, dy, partial, g, blocks, splits, st);
+    default: return launch_wgrad<5, 4, UPDY, EW>(x, dy, partial, g, blocks, splits, st);
   }
 }
 
+// any_width: the caller has checked the shape (the stride-2 form, whose big
+// rows may have odd width).
 int plan_wgrad(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int k, int tile_cols,
-               int depth_chunk, WGeom* g, int64_t* blocks, int* splits) {
-  MEDNEXT_CHECK_ARG(dw_mfma_supported(d, h, w, k) && w % 32 == 0,
+               int depth_chunk, WGeom* g, int64_t* blocks, int* splits, bool any_width = false) {
+  MEDNEXT_CHECK_ARG(any_width || (dw_mfma_supported(d, h, w, k) && w % 32 == 0),
                     "MFMA wgrad needs k in {3,5}, W % 32 == 0, H >= 32 and a slab < 2 GiB");
   MEDNEXT_CHECK_ARG(tile_cols == 32 || tile_cols == 64 || tile_cols == 128,
                     "MFMA wgrad tile_w (columns per workgroup) must be 32, 64 or 128");
@@ -929,7 +1023,7 @@ int s2_wgrad_geom(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int6
   const int64_t slabs = n * c * cdiv(hb, rows) * cdiv(wb, int64_t(*tile_cols));
   const int64_t target = k == 3 ? 5 * 256 / 2 : 2 * 256;
   const int dc = s2_depth_chunk(db, slabs, target);
-  if (int st = plan_wgrad(n, c, db, hb, wb, k, *tile_cols, dc, g, blocks, splits)) return st;
+  if (int st = plan_wgrad(n, c, db, hb, wb, k, *tile_cols, dc, g, blocks, splits, true)) return st;
   g->Ds = static_cast<int>(ds);
   g->Hs = static_cast<int>(hs);
   g->Ws = static_cast<int>(ws);
@@ -939,11 +1033,14 @@ int s2_wgrad_geom(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int6
 }  // namespace
 
 bool dw_mfma_s2_supported(int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs, int64_t ws, int k) {
-  // Even big dims with small = big / 2 (the down block), rows of whole
-  // 16-column pieces (8 small columns per staged store), and the stride-1
-  // kernels' own limits on the big grid (the weight gradient's W % 32 too).
-  return (k == 3 || k == 5) && db % 2 == 0 && hb % 2 == 0 && wb % 32 == 0 && ds * 2 == db && hs * 2 == hb &&
-         ws * 2 == wb && dw_mfma_supported(db, hb, wb, k);
+  // Big = 2 * small (the down block) or 2 * small - 1 (the up block's output)
+  // per dimension. Even big rows: W % 32 == 0 (whole weight-gradient units,
+  // aligned 16-byte row pieces); odd big rows (element-exact access): small
+  // rows of whole 8-column pieces. Both: H, W >= 32 and a slab < 2 GiB.
+  auto pair = [](int64_t b, int64_t s) { return b == 2 * s || b == 2 * s - 1; };
+  const bool width = wb % 2 == 0 ? wb % 32 == 0 : ws % 8 == 0;
+  return (k == 3 || k == 5) && pair(db, ds) && pair(hb, hs) && pair(wb, ws) && width && hb >= 32 && wb >= 32 &&
+         db * hb * wb * 2 < (int64_t(1) << 31) && ds * hs * ws * 2 < (int64_t(1) << 31);
 }
 
 int dw_mfma_s2_gather(const void* big, const void* weight, const void* bias, void* small, int64_t n, int64_t c,
@@ -953,8 +1050,7 @@ int dw_mfma_s2_gather(const void* big, const void* weight, const void* bias, voi
   int tile_cols = 0;
   int64_t blocks = 0;
   if (int s = s2_stencil_geom(n, c, db, hb, wb, ds, hs, ws, &g, &tile_cols, &blocks)) return s;
-  return k == 3 ? launch_stencil_s2_ct<3, kS2Sub>(big, weight, bias, small, g, tile_cols, blocks, st)
-                : launch_stencil_s2_ct<5, kS2Sub>(big, weight, bias, small, g, tile_cols, blocks, st);
+  return launch_stencil_s2_k<kS2Sub>(big, weight, bias, small, g, k, wb % 2 != 0, tile_cols, blocks, st);
 }
 
 int dw_mfma_s2_scatter(const void* small, const void* weight, const void* bias, void* big, int64_t n, int64_t c,
@@ -964,8 +1060,7 @@ int dw_mfma_s2_scatter(const void* small, const void* weight, const void* bias, 
   int tile_cols = 0;
   int64_t blocks = 0;
   if (int s = s2_stencil_geom(n, c, db, hb, wb, ds, hs, ws, &g, &tile_cols, &blocks)) return s;
-  return k == 3 ? launch_stencil_s2_ct<3, kS2Up>(small, weight, bias, big, g, tile_cols, blocks, st)
-                : launch_stencil_s2_ct<5, kS2Up>(small, weight, bias, big, g, tile_cols, blocks, st);
+  return launch_stencil_s2_k<kS2Up>(small, weight, bias, big, g, k, wb % 2 != 0, tile_cols, blocks, st);
 }
 
 int dw_mfma_s2_wgrad_splits(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int64_t ds, int64_t hs,
@@ -985,7 +1080,8 @@ int dw_mfma_s2_wgrad(const void* big, const void* small, float* partial, int64_t
   int tile_cols = 0, splits = 0;
   int64_t blocks = 0;
   if (int s = s2_wgrad_geom(n, c, db, hb, wb, ds, hs, ws, k, &g, &tile_cols, &blocks, &splits)) return s;
-  return launch_wgrad_k<true>(big, small, partial, g, k, tile_cols, blocks, splits, st);
+  return wb % 2 != 0 ? launch_wgrad_k<true, true>(big, small, partial, g, k, tile_cols, blocks, splits, st)
+                     : launch_wgrad_k<true, false>(big, small, partial, g, k, tile_cols, blocks, splits, st);
 }
 
 }  // namespace mednext

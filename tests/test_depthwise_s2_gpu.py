@@ -91,17 +91,26 @@ def test_maps_band_and_row_paths(n, c, big, k):
 
 
 @pytest.mark.parametrize("k", [3, 5])
-@pytest.mark.parametrize("n,c,big", [(2, 3, (6, 48, 64)), (1, 2, (10, 34, 96)), (1, 1, (4, 32, 32 * 9))])
+@pytest.mark.parametrize(
+    "n,c,big",
+    [
+        (2, 3, (6, 48, 64)),  # even big dims (down block)
+        (1, 2, (10, 34, 96)),
+        (1, 1, (4, 32, 32 * 9)),
+        (2, 3, (7, 47, 63)),  # big = 2 small - 1 (up block): odd rows, element-exact big access
+        (1, 2, (9, 33, 79)),
+    ],
+)
 def test_mfma_route_maps_against_oracle(n, c, big, k):
-    """bf16 maps whose small plane exceeds the band kernels (even big dims,
-    W % 32 == 0): the matrix-core stencil with the output subsampled (gather),
+    """bf16 maps whose small plane exceeds the band kernels (big = 2 small or
+    2 small - 1): the matrix-core stencil with the output subsampled (gather),
     over the zero-upsampled small tensor (scatter), and the weight gradient
-    with dy upsampled. Batch 2, row tiles past H (34, 48 rows), column tiles
-    past W (96 with 64-column tiles), short D-runs."""
+    with dy upsampled. Batch 2, row tiles past H (33 .. 48 rows), column tiles
+    past W (63 .. 96 columns), odd widths, short D-runs."""
     print(f"[s2 mfma maps] n={n} c={c} big={big} k={k}", flush=True)
     gen = torch.Generator().manual_seed(7 * k + sum(big))
     dtype = torch.bfloat16
-    small = tuple(s // 2 for s in big)
+    small = tuple((s + 1) // 2 for s in big)
     x = rounded((n, c, *big), gen, dtype)
     w = rounded((c, 1, k, k, k), gen, dtype, 1.0 / k)
     b = rounded((c,), gen, dtype)
@@ -213,3 +222,28 @@ def test_stride2_argument_errors():
     with pytest.raises(ValueError):
         hip_ops.depthwise_s2_wgrad(x, x.double(), 3)
     assert np.isfinite(hip_ops.depthwise_s2_gather(x, torch.randn(2, 1, 3, 3, 3, device=DEV), None, (2, 2, 2)).cpu().numpy()).all()
+
+
+@pytest.mark.parametrize("recipe", [[1, 32, 16], [1, 64, 16]])
+def test_stencil_fill_sink_leaves_staged_rows_alone(recipe):
+    """Regression: fill threads without a chunk once wrote their zeros at an
+    offset from the plane buffer being filled, which for the second buffer
+    fell inside the k = 3 output staging tile (32- and 64-column tiles) and
+    raced with the staged-row stores. Three repeats must agree bit for bit and
+    match the reference: the up-block forward at 63^3 (where the race showed)
+    and the stride-1 forward at the affected tile widths."""
+    gen = torch.Generator().manual_seed(5)
+    c, k = 64, 3
+    small = torch.randn(1, c, 32, 32, 32, generator=gen, dtype=torch.float64).bfloat16()
+    w = (torch.randn(c, 1, k, k, k, generator=gen, dtype=torch.float64) / k).bfloat16()
+    b = torch.randn(c, generator=gen, dtype=torch.float64).bfloat16()
+    big = (63, 63, 63)
+    outs = [hip_ops.depthwise_s2_scatter(small.to(DEV), w.to(DEV), b.to(DEV), big) for _ in range(3)]
+    assert all(torch.equal(outs[0], o) for o in outs[1:])
+    want = odw.strided_input_grad(f64(small), f64(w), big) + f64(b).reshape(1, c, 1, 1, 1)
+    assert max_rel(outs[0], want) <= BF16
+    x = torch.randn(1, c, 64, 64, 64, generator=gen).bfloat16().to(DEV)
+    ys = [hip_ops.depthwise_forward(x, w.to(DEV), b.to(DEV), recipe) for _ in range(3)]
+    assert all(torch.equal(ys[0], y) for y in ys[1:])
+    ref = F.conv3d(x.float(), w.to(DEV).float(), b.to(DEV).float(), padding=1, groups=c)
+    assert max_rel(ys[0], ref) <= BF16
