@@ -176,13 +176,14 @@ int32_t mednext_group_norm_bwd(const void* grad_output, int32_t dy_dtype, const 
  * block's ConvTranspose3d(stride 2), whose output is 2s - 1 per dimension, is
  * scatter (forward), gather (input gradient) and wgrad(big = grad_output,
  * small = x) for the weight (its bias gradient is the sum of grad_output).
- * Kernels: bf16 maps with even big dims, small = big / 2, Wb % 32 == 0,
- * Hb, Wb >= 32 and a small plane above 256 positions (the down blocks at
- * 128^3 / 64^3) run the matrix-core stride-1 kernels (gather: stencil over
- * big, even outputs stored; scatter: flipped-tap stencil over small expanded
- * with zeros; wgrad: weight gradient with dy = small expanded with zeros);
- * small planes of up to 256 positions the band kernels; the rest row-task
- * kernels. The workspace query follows the same choice.
+ * Kernels: bf16 maps with big = 2 small (down block) or 2 small - 1 (up
+ * block) per dimension, Hb, Wb >= 32, an even Wb a multiple of 32 or an odd
+ * Wb with Ws % 8 == 0, and a small plane above 256 positions (128^3 / 64^3
+ * stages) run the matrix-core stride-1 kernels (gather: stencil over big,
+ * even outputs stored; scatter: flipped-tap stencil over small expanded with
+ * zeros; wgrad: weight gradient with dy = small expanded with zeros); small
+ * planes of up to 256 positions the band kernels; the rest row-task kernels.
+ * The workspace query follows the same choice.
  * Replace the reference's F.conv3d / F.conv_transpose3d forwards and their
  * backward kernels (src/mednext_accel/ops/_triton/depthwise.py:206-268,
  * :516-546, :654-719 stride-2; :86-156, :722-850 transposed). */
