@@ -152,6 +152,19 @@ int32_t mednext_group_norm_fwd(const void* x, int32_t x_dtype, const void* gamma
                                int32_t splits, void* workspace, size_t workspace_bytes,
                                void* stream);
 
+/* The forward's statistics without its output: mean / rstd as
+ * mednext_group_norm_fwd writes them (bit-identical), and coef [N*C][4] fp64
+ * (8-byte aligned) = (rstd * gamma, beta, mean, rstd), so GroupNorm(x) =
+ * (x - mean) * (rstd * gamma) + beta per (n, c): the records of the pointwise
+ * NORM prologue, which folds the normalisation into the expand GEMM and
+ * reproduces mednext_group_norm_fwd's bf16 output bit for bit (reference
+ * models/blocks.py:74, :84-86 norm -> conv1). Same workspace as the
+ * forward. */
+int32_t mednext_group_norm_stats(const void* x, int32_t x_dtype, const void* gamma, const void* beta,
+                                 int32_t param_dtype, void* mean, void* rstd, void* coef, int64_t n,
+                                 int64_t c, int64_t spatial, double eps, int32_t splits, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* grad_input (dtype of x, nullable), grad_gamma / grad_beta ([C], param_dtype,
  * nullable) from grad_output (pairs dy/x: f64/f64, f32/f32, f32/bf16, bf16/bf16,
  * f32/f16, f16/f16) and the saved mean/rstd. */
@@ -213,18 +226,20 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
  * partial 8-voxel group uses element accesses), one sample's x and y each
  * < 2 GiB, bf16-aligned tensors and a 16-byte aligned weight. K up to 8192
  * runs the tiled product (see mednext_pw_kernels) and needs what it needs:
- * K % 32 == 0, M % 16 == 0, no GELU or AFFINE prologue, no ROW_REDUCE,
- * blocks_per_sample 0 and the AUTO or TILED choice.
+ * K % 32 == 0, M % 16 == 0, no GELU / AFFINE / NORM prologue, no
+ * ROW_REDUCE, blocks_per_sample 0 and the AUTO or TILED choice.
  * Prologue, applied to every x element as loaded:
  *   MEDNEXT_PW_PROLOGUE_GELU: x -> GELU(x) (exact erf form).
- *   MEDNEXT_PW_PROLOGUE_AFFINE: x -> x * s[n][k] + t[n][k], (s, t) = entries 0
- *     and 1 of the fp64 record prologue_coef[(n * K + k) * 4] (the layout
- *     mednext_grn_stats writes: a GRN folded into the GEMM that consumes it).
- *     The weight gradient and the tiled forward kernel (mednext_pw_kernels)
- *     round x * s + t to bf16 per element; the streaming forward kernels
- *     compute the same W . (x s + t) as (W diag(s)) . x + W . t, with
- *     W diag(s) rounded to bf16 and W . t added to the bias in fp32
- *     (weight_layout 0 only).
+ *   MEDNEXT_PW_PROLOGUE_AFFINE: x -> bf16(fma(x, s, t)), (s, t) = entries 0
+ *     and 1 of the fp64 record prologue_coef[(n * K + k) * 4] taken as
+ *     floats (the records mednext_grn_stats writes: a GRN folded into the
+ *     GEMM that consumes it).
+ *   MEDNEXT_PW_PROLOGUE_NORM: x -> bf16(fma(x - c, s, t)), (s, t, c) =
+ *     entries 0, 1 and 2 as floats (the records mednext_group_norm_stats
+ *     writes: a GroupNorm(C, C) folded into the GEMM that consumes it).
+ *   Both give the value the unfolded normalisation stores, bit for bit.
+ *   Forward epilogues with AFFINE / NORM: BIAS, BIAS_GELU, BIAS_RESIDUAL,
+ *   BIAS_GELU_PAIR, with a [M][K] weight (weight_layout 0) and K <= 2048.
  * Epilogue, applied to each accumulator y[n][m][v] (bias may be NULL):
  *   BIAS:          y = acc + bias[m]
  *   BIAS_GELU:     y = GELU(acc + bias[m])
@@ -244,7 +259,8 @@ int32_t mednext_depthwise3d_s2_wgrad(const void* big, const void* small, void* g
 enum mednext_pw_prologue {
   MEDNEXT_PW_PROLOGUE_NONE = 0,
   MEDNEXT_PW_PROLOGUE_GELU = 1,
-  MEDNEXT_PW_PROLOGUE_AFFINE = 2
+  MEDNEXT_PW_PROLOGUE_AFFINE = 2,
+  MEDNEXT_PW_PROLOGUE_NORM = 3
 };
 enum mednext_pw_epilogue {
   MEDNEXT_PW_EPILOGUE_BIAS = 0,
@@ -313,7 +329,7 @@ size_t mednext_pointwise_fwd_workspace_bytes(int64_t n, int64_t k, int64_t m, in
  * least 256 workgroups, and (given the workspace of mednext_pointwise_fwd_ws)
  * for K >= 256 with a smaller grid, K split over workgroups; TILED takes it
  * wherever it applies; STREAMING never. The tiled
- * kernel applies the AFFINE prologue to X (bf16(x s + t) per element). The
+ * kernel applies the AFFINE / NORM prologue to X as it stages it. The
  * same choice governs the weight gradient's tile: AUTO uses 128 x 128
  * workgroup tiles when M >= 128, K >= 128 and the grid keeps at least 256
  * workgroups, TILED whenever both sides exceed 32,
@@ -352,8 +368,12 @@ int32_t mednext_pointwise_wgrad(const void* grad_output, const void* x, void* gr
                                 int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,
                                 int32_t dtype, int32_t splits, void* stream);
 
-/* mednext_pointwise_wgrad with the prologue's coefficient records (for
- * AFFINE: the GRN output computed from its input as the x operand). */
+/* mednext_pointwise_wgrad with the prologue's coefficient records (AFFINE:
+ * the GRN output computed from its input as the x operand; NORM: the
+ * GroupNorm output). For AFFINE / NORM the product runs on the raw x and the
+ * fixed-order reduction maps each per-sample sum exactly:
+ * sum_v dy x' = s * sum_v dy x + (t - c s) * sum_v dy, in fp64 with the
+ * records' float values (no bf16 rounding of x'). */
 int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const void* x, void* grad_weight,
                                    void* grad_bias, void* workspace, size_t workspace_bytes,
                                    int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue,

@@ -68,6 +68,12 @@ struct AccOf<double> {
   using type = double;
 };
 
+// a * b + c with one rounding in the accumulation type (written out so that
+// kernels that must agree bit for bit do not depend on the compiler's
+// contraction choices).
+__device__ inline float fma_acc(float a, float b, float c) { return fmaf(a, b, c); }
+__device__ inline double fma_acc(double a, double b, double c) { return fma(a, b, c); }
+
 // Four consecutive elements loaded/stored as one vector access. The caller
 // guarantees 4-element alignment.
 template <typename T, typename Acc>

@@ -176,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void gn_apply_kernel(
   const RowSpan rs = row_span(ck.row * v + ck.begin, ck.end - ck.begin, vec_ok);
   for (int64_t i = threadIdx.x; i < rs.scalar_count(); i += blockDim.x) {
     const int64_t k = rs.scalar_index(i);
-    op[k] = Cvt<Ty, Acc>::store((Cvt<Tx, Acc>::load(cp[k]) - m_acc) * scale + offset);
+    op[k] = Cvt<Ty, Acc>::store(fma_acc(Cvt<Tx, Acc>::load(cp[k]) - m_acc, scale, offset));
   }
   for (int64_t j0 = threadIdx.x; j0 < rs.nvec; j0 += kUnroll * blockDim.x) {
     Acc e[kUnroll][8];
@@ -190,11 +190,55 @@ __global__ __launch_bounds__(kThreads) void gn_apply_kernel(
       const int64_t j = j0 + u * static_cast<int64_t>(blockDim.x);
       if (j < rs.nvec) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) e[u][t] = (e[u][t] - m_acc) * scale + offset;
+        for (int t = 0; t < 8; ++t) e[u][t] = fma_acc(e[u][t] - m_acc, scale, offset);
         store8<Ty, Acc>(op + rs.head + 8 * j, e[u]);
       }
     }
   }
+}
+
+// Statistics only (the normalisation folded into the GEMM that consumes it):
+// one thread per (n, c) row combines the row's partials in the fixed order of
+// combine_row, computes mean and rstd exactly as gn_apply_kernel does, and
+// writes them with the row's record coef[row] = (rstd * gamma, beta, mean,
+// rstd) (fp64): taken as floats, fma(x - mean, rstd * gamma, beta) is
+// gn_apply_kernel's fp32 expression, so a consumer reproduces its output.
+template <typename Tx>
+__global__ __launch_bounds__(256) void gn_coef_kernel(const Tx* __restrict__ x, const void* __restrict__ gamma,
+                                                      const void* __restrict__ beta, int pdtype,
+                                                      void* __restrict__ mean_out, void* __restrict__ rstd_out,
+                                                      double* __restrict__ coef, int64_t rows, int64_t c, int64_t v,
+                                                      double eps, int splits, const double* __restrict__ part) {
+  using Acc = typename AccOf<Tx>::type;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  double s1 = 0.0, s2 = 0.0;
+  const double* p = part + row * splits * 2;
+  for (int sp = 0; sp < splits; ++sp) {
+    s1 += p[2 * sp];
+    s2 += p[2 * sp + 1];
+  }
+  const double shift = static_cast<double>(Cvt<Tx, Acc>::load(x[row * v]));
+  const double inv_n = 1.0 / static_cast<double>(v);
+  const double dmean = s1 * inv_n;
+  double var = s2 * inv_n - dmean * dmean;
+  if (var < 0.0) var = 0.0;
+  const double mean = shift + dmean;
+  const double rstd = 1.0 / sqrt(var + eps);
+  const int64_t ch = row % c;
+  const double g = gamma ? load_param(gamma, pdtype, ch) : 1.0;
+  const double bt = beta ? load_param(beta, pdtype, ch) : 0.0;
+  if (sizeof(Acc) == 8) {
+    static_cast<double*>(mean_out)[row] = mean;
+    static_cast<double*>(rstd_out)[row] = rstd;
+  } else {
+    static_cast<float*>(mean_out)[row] = static_cast<float>(mean);
+    static_cast<float*>(rstd_out)[row] = static_cast<float>(rstd);
+  }
+  coef[row * 4] = rstd * g;
+  coef[row * 4 + 1] = bt;
+  coef[row * 4 + 2] = mean;
+  coef[row * 4 + 3] = rstd;
 }
 
 template <typename Ts>
@@ -363,6 +407,22 @@ int gn_fwd_typed(const void* x, const void* gamma, const void* beta, int pdtype,
   return MEDNEXT_STATUS_OK;
 }
 
+template <typename Tx>
+int gn_stats_typed(const void* x, const void* gamma, const void* beta, int pdtype, void* mean, void* rstd,
+                   double* coef, int64_t n, int64_t c, int64_t v, double eps, int splits, double* part,
+                   hipStream_t st) {
+  const int64_t chunk = chunk_len(v, splits);
+  const int64_t blocks = n * c * splits;
+  hipLaunchKernelGGL((gn_stats_kernel<Tx>), dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, st,
+                     static_cast<const Tx*>(x), v, splits, chunk, aligned64(x), part);
+  MEDNEXT_CHECK_LAUNCH();
+  hipLaunchKernelGGL((gn_coef_kernel<Tx>), dim3(static_cast<unsigned>(cdiv(n * c, int64_t(256)))), dim3(256), 0, st,
+                     static_cast<const Tx*>(x), gamma, beta, pdtype, mean, rstd, coef, n * c, c, v, eps, splits,
+                     part);
+  MEDNEXT_CHECK_LAUNCH();
+  return MEDNEXT_STATUS_OK;
+}
+
 template <typename Tdy, typename Tx>
 int gn_bwd_typed(const void* dy, const void* x, const void* mean, const void* rstd,
                  const void* gamma, int pdtype, void* dx, void* dgamma, void* dbeta, int64_t n,
@@ -434,6 +494,34 @@ extern "C" int32_t mednext_group_norm_fwd(const void* x, int32_t x_dtype, const 
 #undef GN_FWD
   set_error("mednext_group_norm_fwd: unsupported (x, y) dtype pair");
   return MEDNEXT_STATUS_UNSUPPORTED;
+}
+
+extern "C" int32_t mednext_group_norm_stats(const void* x, int32_t x_dtype, const void* gamma,
+                                            const void* beta, int32_t param_dtype, void* mean, void* rstd,
+                                            void* coef, int64_t n, int64_t c, int64_t spatial, double eps,
+                                            int32_t splits, void* workspace, size_t workspace_bytes,
+                                            void* stream) {
+  int st = check_common(n, c, spatial, splits);
+  if (st) return st;
+  MEDNEXT_CHECK_ARG(x && mean && rstd && coef, "null tensor pointer");
+  MEDNEXT_CHECK_ARG(dtype_ok(x_dtype) && dtype_ok(param_dtype), "unsupported dtype");
+  MEDNEXT_CHECK_ARG((reinterpret_cast<uintptr_t>(coef) & 7u) == 0, "coef must be 8-byte aligned");
+  MEDNEXT_CHECK_ARG(workspace && workspace_bytes >= workspace_need(n, c, splits), "workspace too small");
+  MEDNEXT_CHECK_ARG(eps >= 0.0, "eps must be non-negative");
+  auto part = static_cast<double*>(workspace);
+  auto s = static_cast<hipStream_t>(stream);
+  auto cf = static_cast<double*>(coef);
+  switch (x_dtype) {
+    case MEDNEXT_DTYPE_F64:
+      return gn_stats_typed<double>(x, gamma, beta, param_dtype, mean, rstd, cf, n, c, spatial, eps, splits, part, s);
+    case MEDNEXT_DTYPE_F32:
+      return gn_stats_typed<float>(x, gamma, beta, param_dtype, mean, rstd, cf, n, c, spatial, eps, splits, part, s);
+    case MEDNEXT_DTYPE_F16:
+      return gn_stats_typed<f16_t>(x, gamma, beta, param_dtype, mean, rstd, cf, n, c, spatial, eps, splits, part, s);
+    default:
+      return gn_stats_typed<bf16_t>(x, gamma, beta, param_dtype, mean, rstd, cf, n, c, spatial, eps, splits, part,
+                                    s);
+  }
 }
 
 extern "C" int32_t mednext_group_norm_bwd(const void* grad_output, int32_t dy_dtype, const void* x,

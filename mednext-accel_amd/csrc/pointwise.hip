@@ -67,18 +67,22 @@ __device__ inline uint4 gelu_vec(uint4 v) {
   return make_uint4(gelu_word(v.x), gelu_word(v.y), gelu_word(v.z), gelu_word(v.w));
 }
 
-// bf16(x * s + t) for the 8 values of one 16-byte group.
-__device__ inline uint32_t affine_word(uint32_t w, float s, float t) {
-  return pack_bf16x2(fmaf(bf16_lo(w), s, t), fmaf(bf16_hi(w), s, t));
+// bf16(fma(x - c, s, t)) for the 8 values of one 16-byte group: c = 0 for an
+// AFFINE record (x - 0 is x), the channel mean for a NORM record (the
+// expression and fp32 operands mednext_group_norm_fwd rounds).
+__device__ inline uint32_t affine_word(uint32_t w, float s, float t, float c) {
+  return pack_bf16x2(fmaf(bf16_lo(w) - c, s, t), fmaf(bf16_hi(w) - c, s, t));
 }
-__device__ inline uint4 affine_vec(uint4 v, float s, float t) {
-  return make_uint4(affine_word(v.x, s, t), affine_word(v.y, s, t), affine_word(v.z, s, t), affine_word(v.w, s, t));
+__device__ inline uint4 affine_vec(uint4 v, float s, float t, float c) {
+  return make_uint4(affine_word(v.x, s, t, c), affine_word(v.y, s, t, c), affine_word(v.z, s, t, c),
+                    affine_word(v.w, s, t, c));
 }
 
 // Extra operands of the AFFINE prologue and the ROW_REDUCE / AFFINE_SCALE /
 // BIAS_GELU_PAIR epilogues (unused members are null).
 struct PwExtra {
-  const double* pcoef;  // [N][K][4]: (s, t, ., .) per (sample, input channel)
+  const double* pcoef;  // [N][K][4]: (s, t, c, .) per (sample, input channel)
+  int centred;          // NORM records: subtract c (entry 2) first; AFFINE: c = 0
   const double* ecoef;  // [N][M][2]: (c0, c1) per (sample, output row)
   double* rpart;        // [N][M][slots][2] row sums
   const bf16_t* aux2;   // AFFINE_SCALE: second per-element operand, shaped like y
@@ -102,31 +106,38 @@ constexpr bool epi_has_aux(int epi) {
 // coefficients c0 and c1 (16 MT floats each).
 constexpr int kRowVecs = 3;
 
-// The forward GEMMs take AFFINE as W . (x s + t) = (W diag(s)) . x + W . t:
-// the column scale goes into the LDS weight block (load_weight_block) and
-// W . t into the row bias, so X is used as loaded.
-// shift[r] = sum_k W[m0 + r][k] t[k] for the workgroup's 16 MT rows (weight
-// stored [M][K]); threads_per_row consecutive lanes share a row and combine
-// their strided partial sums with shuffles (fixed order).
-template <int MT>
-__device__ void affine_row_shift(const bf16_t* __restrict__ w, const double* __restrict__ coef_n, const PwGeom& g,
-                                 int m0, float* shift) {
-  constexpr int ROWS = 16 * MT;
-  constexpr int TPR = kPwThreads / ROWS;
-  const int r = threadIdx.x / TPR, j = threadIdx.x % TPR;
-  const int m = m0 + r;
-  float acc = 0.f;
-  if (m < g.M) {
-    const uint16_t* __restrict__ wr = reinterpret_cast<const uint16_t*>(w) + static_cast<int64_t>(m) * g.K;
-    for (int k = j; k < g.K; k += TPR) acc = fmaf(bf16_to_f32(wr[k]), static_cast<float>(coef_n[k * 4 + 1]), acc);
-  }
+// The AFFINE / NORM prologue (a GRN or GroupNorm folded into the GEMM) is
+// applied to each loaded X row, x -> bf16(fma(x - c[k], s[k], t[k])), with the
+// per-channel (s, t, c) of the sample staged in LDS as floats (zero past K, so
+// padded rows stay zero): bit for bit the value the unfolded normalisation
+// would have stored. Used alike by the streaming, split-K and tiled forward
+// kernels (the weight gradient applies the map to its reduced sums instead).
+template <int PRO>
+__device__ inline void prologue_rows(const uint4 (&r)[8], uint4 (&cur)[8], const float* kcoef, int k0) {
 #pragma unroll
-  for (int off = 1; off < TPR; off <<= 1) acc += __shfl_xor(acc, off);
-  if (j == 0) shift[r] = acc;
+  for (int i = 0; i < 8; ++i) {
+    if constexpr (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
+      const float* kc = kcoef + 3 * (k0 + i);
+      cur[i] = affine_vec(r[i], kc[0], kc[1], kc[2]);
+    } else {
+      cur[i] = PRO == MEDNEXT_PW_PROLOGUE_GELU ? gelu_vec(r[i]) : r[i];
+    }
+  }
 }
 
-// X slice rows through the prologue (the AFFINE prologue is folded into W and
-// the bias, so only GELU touches X).
+// Stages the sample's (s, t, c) of channels [0, kp) as floats (zero past K;
+// c = 0 unless the records are centred).
+__device__ inline void stage_affine(float* kcoef, const double* __restrict__ coef_n, int K, int kp, int centred) {
+  for (int k = threadIdx.x; k < kp; k += kPwThreads) {
+    const bool in = k < K;
+    kcoef[3 * k] = in ? static_cast<float>(coef_n[k * 4]) : 0.f;
+    kcoef[3 * k + 1] = in ? static_cast<float>(coef_n[k * 4 + 1]) : 0.f;
+    kcoef[3 * k + 2] = in && centred ? static_cast<float>(coef_n[k * 4 + 2]) : 0.f;
+  }
+}
+
+// X slice rows through the GELU prologue (the tiled kernel applies AFFINE
+// with its own staged coefficients).
 template <int PRO>
 __device__ inline void apply_prologue(const uint4 (&r)[8], uint4 (&cur)[8]) {
 #pragma unroll
@@ -260,8 +271,7 @@ __device__ inline void store_group(__amdgpu_buffer_rsrc_t r, uint32_t off, uint3
 // 16-byte global reads when whole 8-element groups exist, element reads
 // otherwise (only for small, odd-shaped weights).
 template <int MT>
-__device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, const PwGeom& g, int m0,
-                                  const double* __restrict__ col_scale = nullptr) {
+__device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, const PwGeom& g, int m0) {
   constexpr int ROWS = 16 * MT;
   const int tid = threadIdx.x;
   const int kp = g.ks * 32;
@@ -280,16 +290,6 @@ __device__ void load_weight_block(const bf16_t* __restrict__ w, uint16_t* lds, c
         } else {
           uint32_t wd[4] = {0u, 0u, 0u, 0u};
           for (int e = 0; e < 8 && k8 + e < g.K; ++e) wd[e / 2] |= static_cast<uint32_t>(wr[base + e]) << (16 * (e & 1));
-          v = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-        }
-        if (col_scale != nullptr) {  // W[m][k] * s[k], rounded to bf16
-          uint32_t wd[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-          for (int e = 0; e < 8; e += 2) {
-            const float s0 = k8 + e < g.K ? static_cast<float>(col_scale[(k8 + e) * 4]) : 0.f;
-            const float s1 = k8 + e + 1 < g.K ? static_cast<float>(col_scale[(k8 + e + 1) * 4]) : 0.f;
-            wd[e / 2] = pack_bf16x2(bf16_lo(wd[e / 2]) * s0, bf16_hi(wd[e / 2]) * s1);
-          }
           v = make_uint4(wd[0], wd[1], wd[2], wd[3]);
         }
       }
@@ -341,22 +341,19 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   const int64_t n = rest / g.wgs;
   const int m0 = mg * 16 * MT;
   constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_AFFINE;
-  const double* const coef_n = kAffine ? ex.pcoef + n * g.K * 4 : nullptr;
-  load_weight_block<MT>(w, pw_lds, g, m0, coef_n);
+  load_weight_block<MT>(w, pw_lds, g, m0);
   // Row vectors of this row group as fp32 after the weight block (zero past
-  // M): bias (plus W . t for AFFINE), then the AFFINE_SCALE coefficients c0, c1.
+  // M): bias, then the AFFINE_SCALE coefficients c0, c1; then the AFFINE /
+  // NORM prologue's (s, t, c) per input channel.
   float* const bias_lds = reinterpret_cast<float*>(pw_lds + static_cast<size_t>(16 * MT) * g.ks * 32);
   float* const c0_lds = bias_lds + 16 * MT;
   float* const c1_lds = c0_lds + 16 * MT;
-  if constexpr (kAffine) {
-    affine_row_shift<MT>(w, coef_n, g, m0, c0_lds);
-    __syncthreads();
-  }
+  float* const kcoef = c1_lds + 16 * MT;
+  if constexpr (kAffine) stage_affine(kcoef, ex.pcoef + n * g.K * 4, g.K, g.ks * 32, ex.centred);
   if (threadIdx.x < 16 * MT) {
     const int m = m0 + threadIdx.x;
     const bool in = m < g.M;
-    float b = (epi_has_bias(EPI) && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
-    if constexpr (kAffine) b += c0_lds[threadIdx.x];
+    const float b = (epi_has_bias(EPI) && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
     bias_lds[threadIdx.x] = b;
     if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) {
       c0_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2]) : 0.f;
@@ -403,7 +400,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_kernel(const bf16_t* __r
   };
   auto mma_slice = [&](const uint4 (&r)[8], int ks, f32x4_t (&acc)[MT][8]) {
     uint4 cur[8];
-    apply_prologue<PRO>(r, cur);
+    prologue_rows<PRO>(r, cur, kcoef, 32 * ks + 8 * q);
     uint4 bv[8];
     transpose8x8(cur, bv);
 #pragma unroll
@@ -578,21 +575,17 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
   const int64_t n = rest / g.wgs;
   const int m0 = mg * 16 * MT;
   constexpr bool kAffine = PRO == MEDNEXT_PW_PROLOGUE_AFFINE;
-  const double* const coef_n = kAffine ? ex.pcoef + n * g.K * 4 : nullptr;
-  load_weight_block<MT>(w, pw_lds, g, m0, coef_n);
+  load_weight_block<MT>(w, pw_lds, g, m0);
   float* const bias_lds = reinterpret_cast<float*>(pw_lds + static_cast<size_t>(16 * MT) * g.ks * 32);
   float* const c0_lds = bias_lds + 16 * MT;
   float* const c1_lds = c0_lds + 16 * MT;
   float* const red = bias_lds + kRowVecs * 16 * MT;  // [MT][8][4][64] partial sums
-  if constexpr (kAffine) {
-    affine_row_shift<MT>(w, coef_n, g, m0, c0_lds);
-    __syncthreads();
-  }
+  float* const kcoef = red + MT * 8 * 4 * 64;        // AFFINE / NORM: (s, t, c) per input channel
+  if constexpr (kAffine) stage_affine(kcoef, ex.pcoef + n * g.K * 4, g.K, g.ks * 32, ex.centred);
   if (threadIdx.x < 16 * MT) {
     const int m = m0 + threadIdx.x;
     const bool in = m < g.M;
-    float b = (epi_has_bias(EPI) && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
-    if constexpr (kAffine) b += c0_lds[threadIdx.x];
+    const float b = (epi_has_bias(EPI) && bias != nullptr && in) ? bf16_to_f32(bias[m].bits) : 0.f;
     bias_lds[threadIdx.x] = b;
     if constexpr (EPI == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) {
       c0_lds[threadIdx.x] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2]) : 0.f;
@@ -651,7 +644,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_splitk_kernel(const bf16
       for (int j = 0; j < 8; ++j) acc[mt][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     auto mma_slice = [&](const uint4 (&r)[8], int ks) {
       uint4 cur[8];
-      apply_prologue<PRO>(r, cur);
+      prologue_rows<PRO>(r, cur, kcoef, 32 * ks + 8 * q);
       uint4 bv[8];
       transpose8x8(cur, bv);
 #pragma unroll
@@ -788,7 +781,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
   float* const bias_lds = reinterpret_cast<float*>(stages + nstages * sps * SLICE);
   float* const c0_lds = bias_lds + BM;
   float* const c1_lds = c0_lds + BM;
-  float* const kcoef = c1_lds + BM;  // AFFINE: (s, t) per input channel
+  float* const kcoef = c1_lds + BM;  // AFFINE / NORM: (s, t, c) per input channel
 
   const int mg = static_cast<int>(lin % g.mgroups);
   const int64_t rest = lin / g.mgroups;
@@ -808,13 +801,7 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
       c1_lds[r] = in ? static_cast<float>(ex.ecoef[(n * g.M + m) * 2 + 1]) : 0.f;
     }
   }
-  if constexpr (kAffine) {
-    const double* __restrict__ coef_n = ex.pcoef + n * g.K * 4;
-    for (int k = threadIdx.x; k < g.K; k += kPwThreads) {
-      kcoef[2 * k] = static_cast<float>(coef_n[k * 4]);
-      kcoef[2 * k + 1] = static_cast<float>(coef_n[k * 4 + 1]);
-    }
-  }
+  if constexpr (kAffine) stage_affine(kcoef, ex.pcoef + n * g.K * 4, g.K, g.K, ex.centred);
 
   const uint32_t V = g.V;
   const uint32_t vl = static_cast<uint32_t>(chunk) * kChunk + 8u * n_col;
@@ -863,8 +850,8 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_fwd_tiled_kernel(const bf16_
       if constexpr (kAffine) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const int k = 32 * slice + 8 * q + i;
-          cur[i] = affine_vec(rg[i], kcoef[2 * k], kcoef[2 * k + 1]);
+          const float* kc = kcoef + 3 * (32 * slice + 8 * q + i);
+          cur[i] = affine_vec(rg[i], kc[0], kc[1], kc[2]);
         }
       } else {
         apply_prologue<PRO>(rg, cur);
@@ -1040,7 +1027,6 @@ struct PwWGeom {
   uint32_t span;   // voxels per split (multiple of kWgStage)
   int mblocks, kblocks;
   int64_t stride;  // floats per partial slot: M * K + M
-  const double* pcoef;  // AFFINE prologue records [N][K][4] (else null)
 };
 
 // dW[M][K] = sum_v dY[M][v] X[K][v] over one split's voxel range, for an output
@@ -1080,17 +1066,6 @@ __global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_ke
   const uint32_t vbeg = static_cast<uint32_t>(split) * g.span;
   const uint32_t vend = min(V, vbeg + g.span);
   const bool do_bias = k0 == 0;
-  // AFFINE: (s, t) of the tile's X rows in LDS (zero past K); voxels past
-  // the range load as zero and become t, which meets zero grad_output.
-  __shared__ float aff[PRO == MEDNEXT_PW_PROLOGUE_AFFINE ? 2 * RK : 1];
-  if constexpr (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
-    for (int i = threadIdx.x; i < RK; i += kPwThreads) {
-      const int k = k0 + i;
-      aff[i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4]) : 0.f;
-      aff[RK + i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4 + 1]) : 0.f;
-    }
-    __syncthreads();
-  }
 
   // Load slot u of this thread: tile row r = tid / 16 + 16 u (dY rows first,
   // then X rows), voxels 8 (tid % 16) .. + 7 of the stage.
@@ -1133,8 +1108,6 @@ __global__ __launch_bounds__(kPwThreads, TM * TK >= 16 ? 3 : 4) void pw_wgrad_ke
         }
       } else if (PRO == MEDNEXT_PW_PROLOGUE_GELU) {
         v = gelu_vec(v);  // gelu(0) = 0: missing voxels stay zero
-      } else if (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
-        v = affine_vec(v, aff[r - RM], aff[RK + r - RM]);
       }
       *reinterpret_cast<uint4*>(tile + r * kWgPitch + 8 * grp) = v;
     }
@@ -1228,7 +1201,6 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_wgrad_wide_kernel(const bf16
   static_assert(NLD * kPwThreads == ROWS * (kWgStage / 8), "rows must fill the workgroup");
   extern __shared__ __align__(16) uint16_t wg_lds[];
   uint16_t* const tile = wg_lds;
-  float* const aff = reinterpret_cast<float*>(wg_lds + ROWS * kWgPitch);  // AFFINE (s, t) of the X rows
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = lane & 15, q = lane >> 4;
@@ -1245,14 +1217,6 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_wgrad_wide_kernel(const bf16
   const uint32_t vbeg = static_cast<uint32_t>(split) * g.span;
   const uint32_t vend = min(V, vbeg + g.span);
   const bool do_bias = k0 == 0;
-  if constexpr (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
-    for (int i = threadIdx.x; i < RK; i += kPwThreads) {
-      const int k = k0 + i;
-      aff[i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4]) : 0.f;
-      aff[RK + i] = k < g.K ? static_cast<float>(g.pcoef[(n * g.K + k) * 4 + 1]) : 0.f;
-    }
-    __syncthreads();
-  }
 
   // Load slot u: tile row r = tid / 16 + 16 u (slots 0-7 dY rows, 8-15 X
   // rows), voxels 8 (tid % 16) .. + 7 of the stage.
@@ -1294,8 +1258,6 @@ __global__ __launch_bounds__(kPwThreads, 2) void pw_wgrad_wide_kernel(const bf16
         }
       } else if (PRO == MEDNEXT_PW_PROLOGUE_GELU) {
         v = gelu_vec(v);  // gelu(0) = 0: missing voxels stay zero
-      } else if (PRO == MEDNEXT_PW_PROLOGUE_AFFINE) {
-        v = affine_vec(v, aff[r - RM], aff[RK + r - RM]);
       }
       *reinterpret_cast<uint4*>(tile + r * kWgPitch + 8 * grp) = v;
     }
@@ -1372,12 +1334,25 @@ constexpr int kFinMinBlocks = 512;
 constexpr int kFinSlotsPerLane = 16;
 constexpr int kFinMaxWaves = 16;
 
+// AFFINE / NORM weight gradient. The product kernels run on the raw X; with
+// X' = (x - c) s + t per (sample, channel k), sum_v dY[m][v] X'[k][v] =
+// s P[m][k] + (t - c s) B[m], P = sum_v dY[m][v] x[k][v] and B = sum_v dY[m][v]
+// (the bias column of the same partial slot), so each slot's pair is mapped
+// with its sample's record while it is summed (fp64). Exact where the folded
+// forward rounds X' to bf16.
+struct WgradAffine {
+  const double* coef;  // [N][K][4] records (null: plain product)
+  int64_t k;
+  int64_t splits;  // partial slots per sample
+  int centred;
+};
+
 template <int OUT>
 __global__ __launch_bounds__(64 * kFinMaxWaves) void pw_wgrad_reduce_kernel(const float* __restrict__ partial,
                                                                           bf16_t* __restrict__ dw,
                                                                           bf16_t* __restrict__ db, int64_t mk,
                                                                           int64_t m, int64_t slots,
-                                                                          int64_t stride) {
+                                                                          int64_t stride, WgradAffine af) {
   extern __shared__ double group_sums[];  // [G][OUT]
   constexpr int kSub = 64 / OUT;
   const int lane = threadIdx.x & 63, o = lane % OUT;
@@ -1388,8 +1363,20 @@ __global__ __launch_bounds__(64 * kFinMaxWaves) void pw_wgrad_reduce_kernel(cons
   double s = 0.0;
   if (e < total) {
     const float* p = partial + e;
+    if (af.coef != nullptr && e < mk) {
+      const int64_t row = e / af.k, col = e % af.k;
+      const float* pb = partial + mk + row;
+      for (int64_t t = g; t < slots; t += groups) {
+        const double* r = af.coef + ((t / af.splits) * af.k + col) * 4;
+        const double sc = static_cast<double>(static_cast<float>(r[0]));
+        const double sh = static_cast<double>(static_cast<float>(r[1])) -
+                          (af.centred ? static_cast<double>(static_cast<float>(r[2])) * sc : 0.0);
+        s += sc * static_cast<double>(p[t * stride]) + sh * static_cast<double>(pb[t * stride]);
+      }
+    } else {
 #pragma unroll 8
-    for (int64_t t = g; t < slots; t += groups) s += p[t * stride];
+      for (int64_t t = g; t < slots; t += groups) s += p[t * stride];
+    }
   }
   group_sums[g * OUT + o] = s;
   __syncthreads();
@@ -1421,18 +1408,27 @@ using FwdKernel = void (*)(const bf16_t*, const bf16_t*, const bf16_t*, const bf
 constexpr int kSplitKSlices = 8;  // K >= 256: the four waves of a workgroup split K
 
 // Supported (prologue, epilogue) pairs: NONE with any epilogue, GELU with
-// BIAS .. GELU_GRAD, AFFINE with BIAS or BIAS_RESIDUAL.
+// BIAS .. GELU_GRAD, AFFINE with BIAS, BIAS_GELU, BIAS_RESIDUAL or
+// BIAS_GELU_PAIR (a GroupNorm or GRN folded into the GEMM that consumes it).
 bool pro_epi_supported(int pro, int epi) {
   if (pro == MEDNEXT_PW_PROLOGUE_NONE) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_AUX_SCALE;
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) return epi >= MEDNEXT_PW_EPILOGUE_BIAS && epi <= MEDNEXT_PW_EPILOGUE_GELU_GRAD;
-  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) return epi == MEDNEXT_PW_EPILOGUE_BIAS || epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL;
+  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) {
+    return epi == MEDNEXT_PW_EPILOGUE_BIAS || epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU ||
+           epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL || epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR;
+  }
   return false;
 }
 
 template <int MT>
 FwdKernel splitk_instance(int pro, int epi) {
   if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) {
-    return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL ? pw_fwd_splitk_kernel<MT, 2, 2> : pw_fwd_splitk_kernel<MT, 2, 0>;
+    switch (epi) {
+      case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_splitk_kernel<MT, 2, 1>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_splitk_kernel<MT, 2, 2>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR: return pw_fwd_splitk_kernel<MT, 2, 6>;
+      default: return pw_fwd_splitk_kernel<MT, 2, 0>;
+    }
   }
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
     switch (epi) {
@@ -1457,7 +1453,11 @@ FwdKernel splitk_instance(int pro, int epi) {
 // Four-tile row groups are only used by epilogues without an aux tensor.
 template <int KS, int MT>
 FwdKernel fwd_instance_noaux(int pro, int epi) {
-  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) return pw_fwd_kernel<KS, MT, 2, 0>;
+  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) {
+    return epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR ? pw_fwd_kernel<KS, MT, 2, 6>
+           : epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU    ? pw_fwd_kernel<KS, MT, 2, 1>
+                                                     : pw_fwd_kernel<KS, MT, 2, 0>;
+  }
   if (epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR) return pw_fwd_kernel<KS, MT, 0, 6>;
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
     return epi == MEDNEXT_PW_EPILOGUE_BIAS_GELU ? pw_fwd_kernel<KS, MT, 1, 1> : pw_fwd_kernel<KS, MT, 1, 0>;
@@ -1468,7 +1468,12 @@ FwdKernel fwd_instance_noaux(int pro, int epi) {
 template <int KS, int MT>
 FwdKernel fwd_instance(int pro, int epi) {
   if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) {
-    return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL ? pw_fwd_kernel<KS, MT, 2, 2> : pw_fwd_kernel<KS, MT, 2, 0>;
+    switch (epi) {
+      case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_kernel<KS, MT, 2, 1>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_kernel<KS, MT, 2, 2>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR: return pw_fwd_kernel<KS, MT, 2, 6>;
+      default: return pw_fwd_kernel<KS, MT, 2, 0>;
+    }
   }
   if (pro == MEDNEXT_PW_PROLOGUE_GELU) {
     switch (epi) {
@@ -1510,7 +1515,12 @@ int pick_mt(int64_t k, int64_t m, int epi) {
 template <int MT>
 FwdKernel tiled_instance(int pro, int epi) {
   if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) {
-    return epi == MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL ? pw_fwd_tiled_kernel<MT, 2, 2> : pw_fwd_tiled_kernel<MT, 2, 0>;
+    switch (epi) {
+      case MEDNEXT_PW_EPILOGUE_BIAS_GELU: return pw_fwd_tiled_kernel<MT, 2, 1>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_RESIDUAL: return pw_fwd_tiled_kernel<MT, 2, 2>;
+      case MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR: return pw_fwd_tiled_kernel<MT, 2, 6>;
+      default: return pw_fwd_tiled_kernel<MT, 2, 0>;
+    }
   }
   switch (epi) {
     case MEDNEXT_PW_EPILOGUE_BIAS: return pw_fwd_tiled_kernel<MT, 0, 0>;
@@ -1548,7 +1558,6 @@ using WgradKernel = void (*)(const bf16_t*, const bf16_t*, float*, PwWGeom);
 
 template <int TM, int TK>
 WgradKernel wgrad_instance(int pro) {
-  if (pro == MEDNEXT_PW_PROLOGUE_AFFINE) return pw_wgrad_kernel<TM, TK, 2>;
   return pro == MEDNEXT_PW_PROLOGUE_GELU ? pw_wgrad_kernel<TM, TK, 1> : pw_wgrad_kernel<TM, TK, 0>;
 }
 
@@ -1653,6 +1662,7 @@ bool tiled_only(int64_t k) { return k > kMaxK; }
 
 TiledPlan plan_tiled(int64_t n, int64_t k, int64_t m, int64_t v, int32_t prologue, int32_t epilogue, bool allow_split) {
   TiledPlan t{false, 1, 1, static_cast<int>(k / 32), 0};
+  if (prologue == MEDNEXT_PW_PROLOGUE_NORM) prologue = MEDNEXT_PW_PROLOGUE_AFFINE;  // same kernels
   if (n < 1 || k < 1 || k > kMaxTiledK || m < 1 || v < 1 || !pro_epi_supported(prologue, epilogue)) return t;
   if (tiled_only(k) && prologue == MEDNEXT_PW_PROLOGUE_AFFINE) return t;
   const int choice = g_product_kernels.load(std::memory_order_relaxed);
@@ -1717,7 +1727,7 @@ int32_t launch_tiled(const void* x, const void* weight, const void* bias, const 
   const int64_t nstages = g.kslices > kTileSlices ? 2 : 1;
   const size_t slice = static_cast<size_t>(8 * 64 + 4 * mt * 64) * 16;
   const size_t lds = static_cast<size_t>(nstages * sps) * slice + 3 * 64 * mt * sizeof(float) +
-                     (prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? 2 * static_cast<size_t>(k) * sizeof(float) : 0);
+                     (prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? 3 * static_cast<size_t>(k) * sizeof(float) : 0);
   FwdKernel fn = mt == 1 ? tiled_instance<1>(prologue, epilogue) : tiled_instance<2>(prologue, epilogue);
   const auto st = static_cast<hipStream_t>(stream);
   hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds, st,
@@ -1766,6 +1776,9 @@ extern "C" int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, c
                                             void* row_partial, int32_t dtype, int32_t blocks_per_sample,
                                             void* workspace, size_t workspace_bytes, void* stream) {
   if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
+  // NORM runs the AFFINE kernels with the records' centre subtracted first.
+  const int centred = prologue == MEDNEXT_PW_PROLOGUE_NORM ? 1 : 0;
+  if (centred) prologue = MEDNEXT_PW_PROLOGUE_AFFINE;
   const bool reduce = epilogue == MEDNEXT_PW_EPILOGUE_ROW_REDUCE;
   MEDNEXT_CHECK_ARG(x != nullptr && weight != nullptr && (y != nullptr || reduce), "null tensor pointer");
   MEDNEXT_CHECK_ARG(weight_layout == 0 || weight_layout == 1, "weight_layout must be 0 ([M][K]) or 1 ([K][M])");
@@ -1774,9 +1787,9 @@ extern "C" int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, c
   MEDNEXT_CHECK_ARG(epilogue != MEDNEXT_PW_EPILOGUE_AFFINE_SCALE || aux2 != nullptr, "AFFINE_SCALE needs aux2");
   MEDNEXT_CHECK_ARG(epilogue != MEDNEXT_PW_EPILOGUE_BIAS_GELU_PAIR || y2 != nullptr, "BIAS_GELU_PAIR needs y2");
   MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_AFFINE || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
-                    "the AFFINE prologue needs 8-byte aligned coefficient records");
+                    "the AFFINE / NORM prologue needs 8-byte aligned coefficient records");
   MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_AFFINE || weight_layout == 0,
-                    "the AFFINE prologue takes a [M][K] weight");
+                    "the AFFINE / NORM prologue takes a [M][K] weight");
   MEDNEXT_CHECK_ARG(epilogue != MEDNEXT_PW_EPILOGUE_AFFINE_SCALE ||
                         (epilogue_coef != nullptr && aligned(epilogue_coef, 8)),
                     "the AFFINE_SCALE epilogue needs 8-byte aligned coefficients");
@@ -1787,7 +1800,7 @@ extern "C" int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, c
                         aligned(weight, 16) && (bias == nullptr || aligned(bias, 2)),
                     "pointwise tensors must be bf16-aligned and the weight 16-byte aligned");
   MEDNEXT_CHECK_ARG(blocks_per_sample >= 0, "blocks_per_sample must be >= 0 (0 = automatic)");
-  PwExtra ex{static_cast<const double*>(prologue_coef), static_cast<const double*>(epilogue_coef),
+  PwExtra ex{static_cast<const double*>(prologue_coef), centred, static_cast<const double*>(epilogue_coef),
              static_cast<double*>(row_partial), static_cast<const bf16_t*>(aux2), static_cast<bf16_t*>(y2), 0,
              nullptr};
   if (blocks_per_sample == 0) {
@@ -1801,15 +1814,16 @@ extern "C" int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, c
   }
   MEDNEXT_CHECK_ARG(k <= kMaxK,
                     "input channels above 2048 take the tiled product only (K <= 8192 and a multiple of 32, M a "
-                    "multiple of 16, no GELU / AFFINE prologue or ROW_REDUCE epilogue, AUTO or TILED kernels, "
-                    "blocks_per_sample 0)");
+                    "multiple of 16, no GELU / AFFINE / NORM prologue or ROW_REDUCE epilogue, AUTO or TILED "
+                    "kernels, blocks_per_sample 0)");
   FwdPlan p = plan_fwd(n, k, m, v, epilogue, blocks_per_sample);
   p.g.wt = weight_layout;
   ex.slots = p.slots;
   MEDNEXT_CHECK_ARG(p.blocks < (int64_t{1} << 31), "grid too large");
   const int mt = p.mt;
   const size_t lds = static_cast<size_t>(16 * mt) * p.g.ks * 32 * 2 + kRowVecs * 16 * mt * sizeof(float) +
-                     (p.splitk ? static_cast<size_t>(mt) * 8 * 4 * 64 * sizeof(float) : 0);
+                     (p.splitk ? static_cast<size_t>(mt) * 8 * 4 * 64 * sizeof(float) : 0) +
+                     (prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? static_cast<size_t>(p.g.ks) * 32 * 3 * sizeof(float) : 0);
   hipLaunchKernelGGL(pick_fwd(k, mt, prologue, epilogue), dim3(static_cast<unsigned>(p.blocks)), dim3(kPwThreads),
                      lds, static_cast<hipStream_t>(stream), static_cast<const bf16_t*>(x),
                      static_cast<const bf16_t*>(weight), static_cast<const bf16_t*>(bias),
@@ -1870,10 +1884,15 @@ extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const voi
   if (int st = check_pw_shape(n, k, m, v, dtype)) return st;
   MEDNEXT_CHECK_ARG(grad_output != nullptr && x != nullptr && grad_weight != nullptr, "null tensor pointer");
   MEDNEXT_CHECK_ARG(prologue == MEDNEXT_PW_PROLOGUE_NONE || prologue == MEDNEXT_PW_PROLOGUE_GELU ||
-                        prologue == MEDNEXT_PW_PROLOGUE_AFFINE,
+                        prologue == MEDNEXT_PW_PROLOGUE_AFFINE || prologue == MEDNEXT_PW_PROLOGUE_NORM,
                     "bad prologue");
-  MEDNEXT_CHECK_ARG(prologue != MEDNEXT_PW_PROLOGUE_AFFINE || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
-                    "the AFFINE prologue needs 8-byte aligned coefficient records");
+  const bool affine = prologue == MEDNEXT_PW_PROLOGUE_AFFINE || prologue == MEDNEXT_PW_PROLOGUE_NORM;
+  MEDNEXT_CHECK_ARG(!affine || (prologue_coef != nullptr && aligned(prologue_coef, 8)),
+                    "the AFFINE / NORM prologue needs 8-byte aligned coefficient records");
+  // AFFINE / NORM: the product runs on the raw X and the reduction maps it.
+  const WgradAffine af{affine ? static_cast<const double*>(prologue_coef) : nullptr, k, 0,
+                       prologue == MEDNEXT_PW_PROLOGUE_NORM ? 1 : 0};
+  if (affine) prologue = MEDNEXT_PW_PROLOGUE_NONE;
   MEDNEXT_CHECK_ARG(splits >= 1 && splits <= 65535, "splits must be in [1, 65535]");
   MEDNEXT_CHECK_ARG(aligned(grad_output, 2) && aligned(x, 2) && aligned(grad_weight, 2) &&
                         (grad_bias == nullptr || aligned(grad_bias, 2)),
@@ -1900,17 +1919,13 @@ extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const voi
   g.mblocks = static_cast<int>(cdiv(m, side_m));
   g.kblocks = static_cast<int>(cdiv(k, side_k));
   g.stride = m * k + m;
-  g.pcoef = static_cast<const double*>(prologue_coef);
   const int64_t blocks = n * g.splits * g.mblocks * static_cast<int64_t>(g.kblocks);
   MEDNEXT_CHECK_ARG(blocks < (int64_t{1} << 31), "grid too large");
   const auto s = static_cast<hipStream_t>(stream);
   auto* part = static_cast<float*>(workspace);
   if (wide) {
-    const size_t lds = static_cast<size_t>(2 * kWgWideRows) * kWgPitch * 2 +
-                       (prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? 2 * kWgWideRows * sizeof(float) : 0);
-    WgradKernel fn = prologue == MEDNEXT_PW_PROLOGUE_AFFINE ? pw_wgrad_wide_kernel<2>
-                     : prologue == MEDNEXT_PW_PROLOGUE_GELU ? pw_wgrad_wide_kernel<1>
-                                                            : pw_wgrad_wide_kernel<0>;
+    const size_t lds = static_cast<size_t>(2 * kWgWideRows) * kWgPitch * 2;
+    WgradKernel fn = prologue == MEDNEXT_PW_PROLOGUE_GELU ? pw_wgrad_wide_kernel<1> : pw_wgrad_wide_kernel<0>;
     hipLaunchKernelGGL(fn, dim3(static_cast<unsigned>(blocks)), dim3(kPwThreads), lds, s,
                        static_cast<const bf16_t*>(grad_output), static_cast<const bf16_t*>(x), part, g);
   } else {
@@ -1929,8 +1944,10 @@ extern "C" int32_t mednext_pointwise_wgrad_ex(const void* grad_output, const voi
   const size_t fin_lds = static_cast<size_t>(waves) * 64 * sizeof(double);
   auto reduce = out == 64 ? pw_wgrad_reduce_kernel<64> : out == 32 ? pw_wgrad_reduce_kernel<32>
                                                                    : pw_wgrad_reduce_kernel<16>;
+  WgradAffine fin_af = af;
+  fin_af.splits = g.splits;
   hipLaunchKernelGGL(reduce, fin_grid, dim3(64 * waves), fin_lds, s, part, static_cast<bf16_t*>(grad_weight),
-                     static_cast<bf16_t*>(grad_bias), m * k, m, slots, g.stride);
+                     static_cast<bf16_t*>(grad_bias), m * k, m, slots, g.stride, fin_af);
   MEDNEXT_CHECK_LAUNCH();
   return MEDNEXT_STATUS_OK;
 }

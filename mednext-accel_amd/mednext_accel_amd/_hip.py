@@ -60,6 +60,10 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
         _i32,
         (_p, _i32, _p, _p, _i32, _p, _i32, _p, _p, _i64, _i64, _i64, c_double, _i32, _p, c_size_t, _p),
     ),
+    "mednext_group_norm_stats": (
+        _i32,
+        (_p, _i32, _p, _p, _i32, _p, _p, _p, _i64, _i64, _i64, c_double, _i32, _p, c_size_t, _p),
+    ),
     "mednext_group_norm_bwd": (
         _i32,
         (_p, _i32, _p, _i32, _p, _p, _p, _i32, _p, _p, _p, _i64, _i64, _i64, _i32, _p, c_size_t, _p),
@@ -122,7 +126,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -570,6 +570,15 @@ class AdaptiveGroupNorm3d(_AdaptiveModule):
         y, _mean, _rstd = hip_ops.group_norm_channels(x, weight, bias, self.eps, out_dtype)
         return y
 
+    def hip_selected(self, x: Tensor) -> bool:
+        """Whether ``forward`` would run the HIP kernels on ``x`` (policy and
+        execution guards), for a consumer that folds the normalisation."""
+        if x.ndim != 5 or not x.is_contiguous() or not torch.is_grad_enabled():
+            return False
+        context = _context_from_tensor(x, self.model_context, training=self.training)
+        decision = self.resolver.resolve(self.descriptor, context, context.phase)
+        return decision.implementation == "hip_group_norm" and _hip_ops() is not None
+
     def extra_repr(self) -> str:
         return f"{self.num_groups}, {self.num_channels}, eps={self.eps}, affine={self.affine}"
 
@@ -627,6 +636,11 @@ class AdaptiveExpansion:
             and pointwise_supported(b.expand.out_channels, b.project.out_channels, v)
         )
 
+    #: Fold the block's GroupNorm into the expand GEMM (``folds_norm`` /
+    #: ``folded``) when its HIP kernels are selected: one statistics pass, and
+    #: the expand GEMM normalises as it loads (no normalised tensor).
+    fold_norm = True
+
     def __call__(self, h: Tensor, residual: Tensor | None) -> Tensor:
         b = self.block
         dt = torch.bfloat16
@@ -639,6 +653,43 @@ class AdaptiveExpansion:
             out = _hip_ops().mlp_expansion_stored(h.to(dt), w1, b1, w2, b2, res)[0]
         else:
             out = _hip_ops().mlp_expansion(h.to(dt), w1, b1, w2, b2, res)[0]
+        if residual is not None and not fuse_residual:
+            out = out + residual
+        return out
+
+    def folds_norm(self, d: Tensor) -> bool:
+        """Whether ``folded`` applies to the depthwise output ``d``: an affine
+        GroupNorm(C, C) wrapped for HIP whose kernels are selected for d, and
+        an expand width the AFFINE prologue takes (its coefficients sit in
+        LDS: at most 2048 input channels)."""
+        norm = self.block.norm
+        return (
+            self.fold_norm
+            and isinstance(norm, AdaptiveGroupNorm3d)
+            and norm.affine
+            and norm.num_groups == norm.num_channels
+            and norm.weight is not None
+            and norm.bias is not None
+            and self.block.expand.in_channels <= 2048
+            and norm.hip_selected(d)
+        )
+
+    def folded(self, d: Tensor, residual: Tensor | None) -> Tensor:
+        """``project(GELU(expand(GroupNorm(d)))) [+ residual]`` with the
+        normalisation inside the expand GEMM (``hip_ops.gn_mlp_expansion``)."""
+        b = self.block
+        norm = b.norm
+        dt = torch.bfloat16
+        w1, w2 = cast_param(b.expand.weight, dt), cast_param(b.project.weight, dt)
+        b1 = cast_param(b.expand.bias, dt) if b.expand.bias is not None else None
+        b2 = cast_param(b.project.bias, dt) if b.project.bias is not None else None
+        # Autocast runs group_norm in float32: float32 affine parameters.
+        gamma, beta = norm.weight.float(), norm.bias.float()
+        fuse_residual = residual is not None and residual.dtype == dt and residual.is_contiguous()
+        stored = b.expand.out_channels >= self.stored_gelu_from
+        out = _hip_ops().gn_mlp_expansion(
+            d.to(dt), gamma, beta, w1, b1, w2, b2, residual if fuse_residual else None, float(norm.eps), stored
+        )[0]
         if residual is not None and not fuse_residual:
             out = out + residual
         return out

@@ -81,9 +81,16 @@ class MedNeXtBlock(nn.Module):
         if fused is not None and fused.applies(x):
             d, res = self._depthwise_and_residual(x)
             if fused.supports(d):
-                h = self.norm(d, out_dtype=torch.bfloat16)
                 residual = res if self.use_residual else None
-                if self.checkpoint_expansion and self.training and torch.is_grad_enabled():
+                recompute = self.checkpoint_expansion and self.training and torch.is_grad_enabled()
+                # The GroupNorm folds into the expand GEMM when its HIP kernels
+                # are selected and the branch is not recomputed (a recompute
+                # would repeat the statistics pass); otherwise it runs here and
+                # the expansion takes its bf16 output.
+                if not recompute and fused.folds_norm(d):
+                    return fused.folded(d, residual)
+                h = self.norm(d, out_dtype=torch.bfloat16)
+                if recompute:
                     return checkpoint(fused, h, residual, use_reentrant=False, preserve_rng_state=False)
                 return fused(h, residual)
             return self._finish(self.norm(d), res)

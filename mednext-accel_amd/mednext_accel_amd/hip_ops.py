@@ -296,6 +296,46 @@ def group_norm_forward(
     return y, mean, rstd
 
 
+def group_norm_stats(
+    x: Tensor,
+    weight: Tensor | None,
+    bias: Tensor | None,
+    eps: float = 1e-5,
+    splits: int | None = None,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """GroupNorm(C, C) statistics without the normalised tensor: (coef [N, C, 4]
+    float64 = (rstd * gamma, beta, mean, rstd), the NORM prologue's records,
+    with which the pointwise kernels reproduce ``group_norm_forward``'s bf16
+    output bit for bit; mean [N*C]; rstd [N*C]), mean / rstd bit-identical to
+    ``group_norm_forward``'s."""
+    _check_device(x)
+    if x.ndim < 2 or not x.is_contiguous() or x.numel() == 0:
+        raise ValueError("a nonempty contiguous [N, C, ...] input is required")
+    n, c = int(x.shape[0]), int(x.shape[1])
+    v = x.numel() // (n * c)
+    params = [p for p in (weight, bias) if p is not None]
+    pdtype = params[0].dtype if params else torch.float32
+    for p in params:
+        if p.shape != (c,) or p.dtype != pdtype or not p.is_cuda:
+            raise ValueError("affine parameters must be [C] CUDA tensors of one dtype")
+    coef = torch.empty((n, c, 4), device=x.device, dtype=torch.float64)
+    mean = torch.empty((n * c,), device=x.device, dtype=_stats_dtype(x))
+    rstd = torch.empty_like(mean)
+    splits = group_norm_splits(n, c, v) if splits is None else int(splits)
+    lib = _hip.load()
+    nbytes = lib.mednext_group_norm_workspace_bytes(n, c, v, splits)
+    workspace = torch.empty((max(1, nbytes),), device=x.device, dtype=torch.uint8)
+    _hip.check(
+        lib.mednext_group_norm_stats(
+            x.data_ptr(), _hip.dtype_code(x.dtype), _hip.ptr(weight), _hip.ptr(bias), _hip.dtype_code(pdtype),
+            mean.data_ptr(), rstd.data_ptr(), coef.data_ptr(), n, c, v, float(eps), splits, workspace.data_ptr(),
+            nbytes, _hip.stream_of(x),
+        ),
+        "mednext_group_norm_stats",
+    )
+    return coef, mean, rstd
+
+
 def group_norm_backward(
     grad_output: Tensor,
     x: Tensor,
@@ -339,7 +379,7 @@ def group_norm_backward(
 
 # --------------------------------------------------------------------- pointwise
 
-PW_PROLOGUE_NONE, PW_PROLOGUE_GELU, PW_PROLOGUE_AFFINE = 0, 1, 2
+PW_PROLOGUE_NONE, PW_PROLOGUE_GELU, PW_PROLOGUE_AFFINE, PW_PROLOGUE_NORM = 0, 1, 2, 3
 PW_EPILOGUE_BIAS, PW_EPILOGUE_BIAS_GELU, PW_EPILOGUE_BIAS_RESIDUAL, PW_EPILOGUE_GELU_GRAD = 0, 1, 2, 3
 PW_EPILOGUE_ROW_REDUCE, PW_EPILOGUE_AFFINE_SCALE, PW_EPILOGUE_BIAS_GELU_PAIR, PW_EPILOGUE_AUX_SCALE = 4, 5, 6, 7
 #: Forward kernel family (include/mednext_hip.h ``mednext_pw_kernels``): the
@@ -396,7 +436,7 @@ def pointwise_conv(
     product is ``W^T . x`` (the conv's input gradient). ``aux`` (and ``aux2``
     for AFFINE_SCALE) are per-element operands shaped like ``y``: the residual
     (BIAS_RESIDUAL), the GELU pre-activation (GELU_GRAD), the row-sum weights
-    (ROW_REDUCE). ``prologue_coef`` ([N, K, 4] float64) feeds AFFINE,
+    (ROW_REDUCE). ``prologue_coef`` ([N, K, 4] float64) feeds AFFINE / NORM,
     ``epilogue_coef`` ([N, M, 2] float64) AFFINE_SCALE. ROW_REDUCE writes
     ``row_partial`` ([N, M, slots, 2] float64, slots from
     ``pointwise_row_slots``) and returns None; BIAS_GELU_PAIR returns
@@ -475,7 +515,9 @@ def pointwise_weight_grad(
     prologue_coef: Tensor | None = None,
 ) -> tuple[Tensor, Tensor | None]:
     """(dW [Cout, Cin, 1, 1, 1], dB [Cout] or None) of ``y = W . prologue(x) + b``
-    (``prologue_coef`` as for ``pointwise_conv``'s AFFINE)."""
+    (``prologue_coef`` as for ``pointwise_conv``'s AFFINE / NORM; the library
+    maps the raw product's per-sample sums exactly instead of rounding
+    prologue(x) to bf16)."""
     _check_device(grad_output, x)
     _check_pointwise_tensor(grad_output, "grad_output")
     _check_pointwise_tensor(x, "x")
@@ -934,6 +976,140 @@ def _mlp_stored_backward(ctx, grad_out, _grad_a, _grad_dgelu):
 
 
 mlp_expansion_stored.register_autograd(_mlp_stored_backward, setup_context=_setup_mlp_stored)
+
+
+@torch.library.custom_op("mednext_accel_amd::gn_mlp_expansion", mutates_args=())
+def gn_mlp_expansion(
+    d: Tensor,
+    gamma: Tensor,
+    beta: Tensor,
+    w1: Tensor,
+    b1: Tensor | None,
+    w2: Tensor,
+    b2: Tensor | None,
+    residual: Tensor | None,
+    eps: float,
+    stored: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """MedNeXt block ``norm -> expand -> GELU -> project (+ residual)`` with
+    the GroupNorm folded into the expand GEMM (reference models/blocks.py:74,
+    :84-91): one statistics pass over the depthwise output d gives the
+    per-(n, c) records, and the expand GEMM applies GroupNorm through its NORM
+    prologue as it loads d (bit for bit the bf16 values ``group_norm_forward``
+    writes), so the normalised tensor is never written or read.
+    ``stored`` selects the GELU handling of ``mlp_expansion_stored`` (the
+    expand GEMM writes GELU(h) and GELU'(h)) or of ``mlp_expansion`` (it
+    writes h; the project GEMM and the backward recompute GELU).
+
+    Returns ``(out, act, dgelu, coef, mean, rstd)``: act = GELU(h) (stored)
+    or h; dgelu = GELU'(h) (stored) or an empty tensor; coef [N, C, 4] fp64
+    (``group_norm_stats``); mean / rstd [N*C] as ``group_norm_forward`` writes
+    them."""
+    d = d.contiguous()
+    coef, mean, rstd = group_norm_stats(d, gamma, beta, eps)
+    res = residual.contiguous() if residual is not None else None
+    epi_out = PW_EPILOGUE_BIAS if res is None else PW_EPILOGUE_BIAS_RESIDUAL
+    if stored:
+        act, dgelu = pointwise_conv(d, w1, b1, prologue=PW_PROLOGUE_NORM, epilogue=PW_EPILOGUE_BIAS_GELU_PAIR,
+                                    prologue_coef=coef)
+        out = pointwise_conv(act, w2, b2, aux=res, epilogue=epi_out)
+    else:
+        act = pointwise_conv(d, w1, b1, prologue=PW_PROLOGUE_NORM, epilogue=PW_EPILOGUE_BIAS, prologue_coef=coef)
+        dgelu = act.new_empty((0,))
+        out = pointwise_conv(act, w2, b2, aux=res, prologue=PW_PROLOGUE_GELU, epilogue=epi_out)
+    return out, act, dgelu, coef, mean, rstd
+
+
+@gn_mlp_expansion.register_fake
+def _(d, gamma, beta, w1, b1, w2, b2, residual, eps, stored):
+    n, c = d.shape[0], d.shape[1]
+    h = d.new_empty((n, w1.shape[0], *d.shape[2:]))
+    return (
+        d.new_empty((n, w2.shape[0], *d.shape[2:])),
+        h,
+        torch.empty_like(h) if stored else d.new_empty((0,)),
+        d.new_empty((n, c, 4), dtype=torch.float64),
+        d.new_empty((n * c,), dtype=torch.float32),
+        d.new_empty((n * c,), dtype=torch.float32),
+    )
+
+
+@torch.library.custom_op("mednext_accel_amd::gn_mlp_expansion_backward", mutates_args=())
+def gn_mlp_expansion_backward(
+    grad_out: Tensor,
+    d: Tensor,
+    act: Tensor,
+    dgelu: Tensor,
+    coef: Tensor,
+    mean: Tensor,
+    rstd: Tensor,
+    gamma: Tensor,
+    w1: Tensor,
+    w2: Tensor,
+    stored: bool,
+) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(dd, dgamma, dbeta, dW1, db1, dW2, db2) of ``gn_mlp_expansion``:
+    dh = (W2^T . dout) * GELU'(h); dW2 = dout . GELU(h)^T; dW1 = dh . GN(d)^T
+    from the raw product dh . d^T mapped through the NORM records; dz = W1^T . dh; and the
+    GroupNorm backward of dz at d."""
+    grad_out = grad_out.contiguous()
+    if stored:
+        dh = pointwise_conv(grad_out, w2, aux=dgelu, epilogue=PW_EPILOGUE_AUX_SCALE, transpose=True)
+        dw2, db2 = pointwise_weight_grad(grad_out, act)
+    else:
+        dh = pointwise_conv(grad_out, w2, aux=act, epilogue=PW_EPILOGUE_GELU_GRAD, transpose=True)
+        dw2, db2 = pointwise_weight_grad(grad_out, act, prologue=PW_PROLOGUE_GELU)
+    dw1, db1 = pointwise_weight_grad(dh, d, prologue=PW_PROLOGUE_NORM, prologue_coef=coef)
+    dz = pointwise_conv(dh, w1, transpose=True)
+    dd, dgamma, dbeta = group_norm_backward(dz, d, mean, rstd, gamma)
+    return dd, dgamma, dbeta, dw1, db1, dw2, db2
+
+
+@gn_mlp_expansion_backward.register_fake
+def _(grad_out, d, act, dgelu, coef, mean, rstd, gamma, w1, w2, stored):
+    return (
+        torch.empty_like(d),
+        torch.empty_like(gamma),
+        torch.empty_like(gamma),
+        w1.new_empty(w1.shape),
+        w1.new_empty((w1.shape[0],)),
+        w2.new_empty(w2.shape),
+        w2.new_empty((w2.shape[0],)),
+    )
+
+
+def _setup_gn_mlp(ctx, inputs, output):
+    d, gamma, beta, w1, b1, w2, b2, residual, eps, stored = inputs
+    _out, act, dgelu, coef, mean, rstd = output
+    ctx.mark_non_differentiable(act, dgelu, coef, mean, rstd)
+    ctx.set_materialize_grads(False)
+    ctx.save_for_backward(d, act, dgelu, coef, mean, rstd, gamma, w1, w2)
+    ctx.stored = stored
+    ctx.has_b1, ctx.has_b2, ctx.has_residual = b1 is not None, b2 is not None, residual is not None
+
+
+def _gn_mlp_backward(ctx, grad_out, *_unused):
+    if grad_out is None:
+        return (None,) * 10
+    d, act, dgelu, coef, mean, rstd, gamma, w1, w2 = ctx.saved_tensors
+    dd, dgamma, dbeta, dw1, db1, dw2, db2 = gn_mlp_expansion_backward(
+        grad_out, d, act, dgelu, coef, mean, rstd, gamma, w1, w2, ctx.stored
+    )
+    return (
+        dd,
+        dgamma,
+        dbeta,
+        dw1,
+        db1 if ctx.has_b1 else None,
+        dw2,
+        db2 if ctx.has_b2 else None,
+        grad_out if ctx.has_residual else None,
+        None,
+        None,
+    )
+
+
+gn_mlp_expansion.register_autograd(_gn_mlp_backward, setup_context=_setup_gn_mlp)
 
 
 # ------------------------------------------------------------ stride-2 depthwise

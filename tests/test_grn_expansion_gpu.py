@@ -156,8 +156,9 @@ def test_affine_prologue_forward_and_weight_grad():
     assert rel_l2(y.view(n, m, v), want) <= 8e-3
     dy = torch.randn(n, m, s, s, s, device=DEV).bfloat16()
     dw, db = P.pointwise_weight_grad(dy, a, prologue=P.PW_PROLOGUE_AFFINE, prologue_coef=coef)
-    zb = z.bfloat16().double()  # the weight gradient rounds x * s + t per element
-    want_dw = torch.einsum("nmv,nkv->mk", dy.double().view(n, m, v), zb)
+    cf = coef.float().double()  # the records as the kernels take them
+    zx = a.double().view(n, k, v) * cf[..., :1] + cf[..., 1:2]  # exact: the library maps the raw product's sums
+    want_dw = torch.einsum("nmv,nkv->mk", dy.double().view(n, m, v), zx)
     assert rel_l2(dw.view(m, k), want_dw) <= 8e-3
     assert rel_l2(db, dy.double().sum(dim=(0, 2, 3, 4))) <= 8e-3
 

@@ -22,6 +22,7 @@ from helpers import BF16, FP32_OUT, FP32_WGRAD, check_against_truth, max_rel, re
 from mednext_accel_amd import CheckpointConfig, MedNeXtBlock, mednext_base, mednext_small
 from mednext_accel_amd.adaptive import (
     AdaptiveDepthwise3d,
+    AdaptiveExpansion,
     AdaptiveGroupNorm3d,
     ModelOptimizationContext,
     install_adaptive_operators,
@@ -36,6 +37,7 @@ DW_OP = "mednext_accel_amd::depthwise_conv3d_odd_regular"
 DX_OP = "mednext_accel_amd::depthwise_input_grad_odd_regular"
 DWG_OP = "mednext_accel_amd::depthwise_weight_grad_odd_regular"
 GN_OP = "mednext_accel_amd::group_norm_channels"
+GN_MLP_OP = "mednext_accel_amd::gn_mlp_expansion"  # GroupNorm folded into the expand GEMM
 MLP_OP = "mednext_accel_amd::mlp_expansion"
 MLP_STORED_OP = "mednext_accel_amd::mlp_expansion_stored"
 
@@ -173,7 +175,8 @@ def test_block_cfg2_bf16_autocast_matches_reference_block(channels, size, ratio)
         want = ref(x)
         with Observe() as seen:
             got = cand(y)
-    assert DW_OP in seen.ops and GN_OP in seen.ops and (MLP_OP in seen.ops or MLP_STORED_OP in seen.ops)
+    # The block's GroupNorm folds into the expand GEMM (gn_mlp_expansion).
+    assert DW_OP in seen.ops and GN_MLP_OP in seen.ops and GN_OP not in seen.ops
     exact = truth(z)
     g = torch.randn_like(want)
     wants = torch.autograd.grad(want, (x, *ref.parameters()), g)
@@ -222,8 +225,7 @@ def test_base_training_step_128_bf16_matches_reference():
             loss = step()
         losses.append(float(loss))
         if model is cand:
-            assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops and GN_OP in seen.ops
-            assert MLP_OP in seen.ops and MLP_STORED_OP in seen.ops
+            assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops and GN_MLP_OP in seen.ops
         del step
     assert abs(losses[0] - losses[1]) / abs(losses[1]) < BF16
     for (name, p), q in zip(cand.named_parameters(), ref.parameters(), strict=True):
@@ -254,13 +256,45 @@ def test_large_k5_checkpointed_step_matches_reference():
         losses.append(float(loss.detach()))
         norms.append(torch.stack([p.grad.float().norm() for p in model.parameters()]))
         if model is cand:
-            assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops
-            assert MLP_OP in seen.ops and MLP_STORED_OP in seen.ops
+            assert DW_OP in seen.ops and DX_OP in seen.ops and DWG_OP in seen.ops and GN_OP in seen.ops
+            # Checkpointed expansions keep GroupNorm unfolded (no second statistics pass).
+            assert MLP_OP in seen.ops and MLP_STORED_OP in seen.ops and GN_MLP_OP not in seen.ops
         del step
     assert abs(losses[0] - losses[1]) / abs(losses[1]) < BF16
     assert torch.isfinite(norms[0]).all()
     assert float(((norms[0] - norms[1]).norm() / norms[1].norm())) < 5e-2
     torch.cuda.empty_cache()
+
+
+def test_groupnorm_fold_is_bit_identical_to_the_unfolded_path():
+    """MedNeXt-S (C=8, 32^3, bf16 autocast, no checkpointing) with every
+    block's GroupNorm folded into its expand GEMM or run as its own kernels:
+    the NORM prologue hands the GEMM the bf16 values the GroupNorm kernel
+    writes, so the output and every gradient are bit-identical, except the
+    expand weight's, which the folded path takes from the exact map of the raw
+    product (no per-element rounding of the normalised operand)."""
+    torch.manual_seed(11)
+    model = mednext_small(in_channels=1, out_channels=2, base_channels=8).to(DEV).train()
+    x = torch.randn(1, 1, 32, 32, 32, device=DEV)
+    runs = {}
+    try:
+        for fold in (True, False):
+            AdaptiveExpansion.fold_norm = fold
+            model.zero_grad(set_to_none=True)
+            with torch.autocast(DEV, dtype=torch.bfloat16), Observe() as seen:
+                out = model(x)
+            assert (GN_MLP_OP in seen.ops) == fold and (GN_OP in seen.ops) != fold
+            out.float().square().mean().backward()
+            runs[fold] = (out.detach(), {n: p.grad.detach().clone() for n, p in model.named_parameters()})
+    finally:
+        AdaptiveExpansion.fold_norm = True
+    assert torch.equal(runs[True][0], runs[False][0])
+    for name, g in runs[True][1].items():
+        other = runs[False][1][name]
+        if name.endswith("expand.weight"):
+            assert rel_l2(g, other) <= 1e-2, name
+        else:
+            assert torch.equal(g, other), name
 
 
 @pytest.mark.parametrize("style", ["expansion", "block"])

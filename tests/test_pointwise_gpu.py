@@ -206,6 +206,126 @@ def test_fused_mlp_expansion_matches_unfused_fp32(residual, c, r, s, stored):
         assert max_rel(a, b) <= BF16, name
 
 
+@pytest.mark.parametrize("stored", [False, True])
+@pytest.mark.parametrize("n,c,r,s,residual", [(1, 32, 2, 32, True), (2, 64, 3, 12, True), (1, 96, 4, 9, False)])
+def test_groupnorm_folded_expansion_matches_fp32(n, c, r, s, residual, stored):
+    """gn_mlp_expansion = project(GELU(expand(GroupNorm(d)))) + residual with the
+    GroupNorm folded into the expand GEMM's NORM prologue, fwd + bwd (d, gamma,
+    beta, both weights and biases, residual) vs the same composition in fp32
+    PyTorch on the bf16 operands."""
+    print(f"[gn folded expansion] n={n} c={c} r={r} s={s} residual={residual} stored={stored}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(3 + c)
+    d = (torch.randn(n, c, s, s, s, generator=gen, device=DEV) * 2 + 0.5).bfloat16()
+    res = torch.randn(n, c, s, s, s, generator=gen, device=DEV).bfloat16()
+    gamma = 1 + 0.2 * torch.randn(c, generator=gen, device=DEV)
+    beta = 0.1 * torch.randn(c, generator=gen, device=DEV)
+    w1 = (torch.randn(r * c, c, 1, 1, 1, generator=gen, device=DEV) * c**-0.5).bfloat16()
+    b1 = (torch.randn(r * c, generator=gen, device=DEV) * 0.1).bfloat16()
+    w2 = (torch.randn(c, r * c, 1, 1, 1, generator=gen, device=DEV) * (r * c) ** -0.5).bfloat16()
+    b2 = (torch.randn(c, generator=gen, device=DEV) * 0.1).bfloat16()
+    leaves = [t.clone().requires_grad_() for t in (d, gamma, beta, w1, b1, w2, b2, res)]
+    out = hip_ops.gn_mlp_expansion(*leaves[:7], leaves[7] if residual else None, 1e-5, stored)[0]
+    ref_leaves = [t.float().requires_grad_() for t in (d, gamma, beta, w1, b1, w2, b2, res)]
+    df, gf, bf_, w1f, b1f, w2f, b2f, rf = ref_leaves
+    ref = F.conv3d(F.gelu(F.conv3d(F.group_norm(df, c, gf, bf_, 1e-5), w1f, b1f)), w2f, b2f) + (rf if residual else 0)
+    assert max_rel(out, ref) <= BF16
+    g = torch.randn_like(ref).bfloat16()
+    inputs = leaves if residual else leaves[:7]
+    got = torch.autograd.grad(out, inputs, g)
+    want = torch.autograd.grad(ref, ref_leaves if residual else ref_leaves[:7], g.float())
+    for name, a, b in zip(["d", "gamma", "beta", "w1", "b1", "w2", "b2", "res"], got, want):
+        assert max_rel(a, b) <= BF16, name
+
+
+def test_groupnorm_stats_match_the_forward():
+    """group_norm_stats: mean / rstd bit-identical to group_norm_forward's, and
+    the NORM records (rstd * gamma, beta, mean, rstd) reproduce its output."""
+    gen = torch.Generator(device=DEV).manual_seed(9)
+    x = (torch.randn(2, 24, 9, 10, 11, generator=gen, device=DEV) * 3 + 1).bfloat16()
+    w = torch.randn(24, generator=gen, device=DEV)
+    b = torch.randn(24, generator=gen, device=DEV)
+    y, mean, rstd = hip_ops.group_norm_forward(x, w, b, 1e-5, torch.float32)
+    coef, m2, r2 = hip_ops.group_norm_stats(x, w, b, 1e-5)
+    assert torch.equal(mean, m2) and torch.equal(rstd, r2)
+    assert torch.equal(coef[..., 2].flatten().float(), mean) and torch.equal(coef[..., 3].flatten().float(), rstd)
+    assert torch.equal(coef[..., 0], coef[..., 3] * w.double())  # rstd * gamma in fp64
+    assert torch.equal(coef[..., 1], b.double().expand(2, 24))
+    s_, t_, c_ = (coef[..., i].float().view(2, 24, 1, 1, 1) for i in range(3))
+    assert torch.allclose((x.float() - c_) * s_ + t_, y, rtol=1e-5, atol=1e-5)
+
+
+# (n, k, m, s): streaming kernels (K 32 / 96), split-K (K 256), and shapes the
+# tiled product takes under AUTO (K 256 with a wide M).
+NORM_SHAPES = [(1, 32, 64, 16), (2, 96, 192, 9), (1, 256, 64, 8), (1, 256, 1024, 16)]
+
+
+@pytest.mark.parametrize("n,k,m,s", NORM_SHAPES)
+def test_norm_prologue_reproduces_the_group_norm_output_bitwise(n, k, m, s):
+    """The NORM prologue hands the MFMAs exactly the bf16 values
+    group_norm_forward writes: every kernel family (streaming / split-K,
+    tiled at 128 and 64 rows) and epilogue gives bit-identical outputs with
+    the normalisation folded or run first."""
+    print(f"[norm prologue bitwise] n={n} k={k} m={m} s={s}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(k + m)
+    d = (torch.randn(n, k, s, s, s, generator=gen, device=DEV) * 2 - 0.7).bfloat16()
+    gamma = 1 + 0.3 * torch.randn(k, generator=gen, device=DEV)
+    beta = 0.2 * torch.randn(k, generator=gen, device=DEV)
+    w = (torch.randn(m, k, 1, 1, 1, generator=gen, device=DEV) * k**-0.5).bfloat16()
+    b = (torch.randn(m, generator=gen, device=DEV) * 0.1).bfloat16()
+    res = torch.randn(n, m, s, s, s, generator=gen, device=DEV).bfloat16()
+    h, _, _ = hip_ops.group_norm_forward(d, gamma, beta, 1e-5, torch.bfloat16)
+    coef, _, _ = hip_ops.group_norm_stats(d, gamma, beta, 1e-5)
+    cases = [
+        (hip_ops.PW_EPILOGUE_BIAS, None),
+        (hip_ops.PW_EPILOGUE_BIAS_RESIDUAL, res),
+        (hip_ops.PW_EPILOGUE_BIAS_GELU_PAIR, None),
+    ]
+    try:
+        for choice in (hip_ops.PW_KERNELS_AUTO, hip_ops.PW_KERNELS_STREAMING, hip_ops.PW_KERNELS_TILED,
+                       hip_ops.PW_KERNELS_TILED_64):
+            hip_ops.set_pointwise_kernels(choice)
+            for epi, aux in cases:
+                folded = hip_ops.pointwise_conv(d, w, b, aux=aux, epilogue=epi, prologue=hip_ops.PW_PROLOGUE_NORM,
+                                                prologue_coef=coef)
+                plain = hip_ops.pointwise_conv(h, w, b, aux=aux, epilogue=epi)
+                for a, c in zip(folded if isinstance(folded, tuple) else (folded,),
+                                plain if isinstance(plain, tuple) else (plain,)):
+                    assert torch.equal(a, c), (choice, epi)
+    finally:
+        hip_ops.set_pointwise_kernels(hip_ops.PW_KERNELS_AUTO)
+
+
+@pytest.mark.parametrize("n,k,m,s", [(2, 32, 64, 12), (1, 128, 256, 16), (2, 96, 160, 10)])
+def test_norm_weight_grad_is_the_exact_map_of_the_raw_product(n, k, m, s):
+    """NORM / AFFINE weight gradients: the library sums dy x over voxels and
+    maps each sample's sums with its records, so dW matches
+    sum dy ((x - c) s + t) in float64 (records taken as floats) to the bf16
+    rounding of the output, on every weight-gradient tile (64 x 64 and
+    128 x 128)."""
+    print(f"[norm wgrad] n={n} k={k} m={m} s={s}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(7 * k + m)
+    x = (torch.randn(n, k, s, s, s, generator=gen, device=DEV) * 1.5 + 2.0).bfloat16()
+    dy = torch.randn(n, m, s, s, s, generator=gen, device=DEV).bfloat16()
+    gamma = 1 + 0.3 * torch.randn(k, generator=gen, device=DEV)
+    beta = 0.2 * torch.randn(k, generator=gen, device=DEV)
+    coef, _, _ = hip_ops.group_norm_stats(x, gamma, beta, 1e-5)
+    cf = coef.float().double()
+    v = s**3
+    xs = (x.double().view(n, k, v) - cf[..., 2:3]) * cf[..., :1] + cf[..., 1:2]
+    dyd = dy.double().view(n, m, v)
+    want_dw = torch.einsum("nmv,nkv->mk", dyd, xs)
+    want_db = dyd.sum(dim=(0, 2))
+    try:
+        for choice in (hip_ops.PW_KERNELS_STREAMING, hip_ops.PW_KERNELS_TILED):
+            hip_ops.set_pointwise_kernels(choice)
+            dw, db = hip_ops.pointwise_weight_grad(dy, x, prologue=hip_ops.PW_PROLOGUE_NORM, prologue_coef=coef)
+            err = (dw.view(m, k).double() - want_dw).abs() / want_dw.abs().clamp_min(1e-3 * want_dw.abs().max())
+            assert float(err.max()) <= 2**-8, choice  # one bf16 rounding of the output
+            assert max_rel(db, want_db) <= 2**-8
+    finally:
+        hip_ops.set_pointwise_kernels(hip_ops.PW_KERNELS_AUTO)
+
+
 def test_opcheck_pointwise_ops():
     gen = torch.Generator(device=DEV).manual_seed(4)
     x = torch.randn(1, 32, 2, 4, 8, generator=gen, device=DEV).bfloat16().requires_grad_()
@@ -216,6 +336,10 @@ def test_opcheck_pointwise_ops():
     res = torch.randn(1, 32, 2, 4, 8, generator=gen, device=DEV).bfloat16().requires_grad_()
     torch.library.opcheck(hip_ops.mlp_expansion, (x, w, b, w2, None, res))
     torch.library.opcheck(hip_ops.mlp_expansion_stored, (x, w, b, w2, None, res))
+    gamma = torch.randn(x.shape[1], device=DEV).requires_grad_()
+    beta = torch.randn(x.shape[1], device=DEV).requires_grad_()
+    for stored in (False, True):
+        torch.library.opcheck(hip_ops.gn_mlp_expansion, (x, gamma, beta, w, b, w2, None, res, 1e-5, stored))
 
 
 def test_channels_above_2048_take_the_tiled_product():

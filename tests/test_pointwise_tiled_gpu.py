@@ -197,7 +197,8 @@ def test_weight_grad_tiles(n, k, m, spatial, prologue):
     if prologue == "gelu":
         xf = F.gelu(xf)
     elif prologue == "affine":
-        xf = (xf * coef[..., :1] + coef[..., 1:2]).bfloat16().double()  # rounded per element, as the kernels do
+        cf = coef.float().double()  # records as floats; the map of the raw product's sums is exact
+        xf = xf * cf[..., :1] + cf[..., 1:2]
     dyf = dy.double().flatten(2)
     want_dw = torch.einsum("nmv,nkv->mk", dyf, xf)
     want_db = dyf.sum(dim=(0, 2))
