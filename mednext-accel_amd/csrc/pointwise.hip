@@ -1364,14 +1364,23 @@ __global__ __launch_bounds__(64 * kFinMaxWaves) void pw_wgrad_reduce_kernel(cons
   if (e < total) {
     const float* p = partial + e;
     if (af.coef != nullptr && e < mk) {
-      const int64_t row = e / af.k, col = e % af.k;
+      // Slots are sample-major (splits per sample): this thread's slots of
+      // one sample are summed first, then mapped with that sample's record.
+      const int64_t row = e / af.k, col = e - row * af.k;
       const float* pb = partial + mk + row;
-      for (int64_t t = g; t < slots; t += groups) {
-        const double* r = af.coef + ((t / af.splits) * af.k + col) * 4;
+      int64_t t = g;
+      for (int64_t smp = 0; t < slots; ++smp) {
+        const int64_t end = min(slots, (smp + 1) * af.splits);
+        double sp = 0.0, sb = 0.0;
+        for (; t < end; t += groups) {
+          sp += p[t * stride];
+          sb += pb[t * stride];
+        }
+        const double* r = af.coef + (smp * af.k + col) * 4;
         const double sc = static_cast<double>(static_cast<float>(r[0]));
         const double sh = static_cast<double>(static_cast<float>(r[1])) -
                           (af.centred ? static_cast<double>(static_cast<float>(r[2])) * sc : 0.0);
-        s += sc * static_cast<double>(p[t * stride]) + sh * static_cast<double>(pb[t * stride]);
+        s += sc * sp + sh * sb;
       }
     } else {
 #pragma unroll 8
