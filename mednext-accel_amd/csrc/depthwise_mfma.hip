@@ -190,10 +190,9 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
   const f32x4_t acc_init = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   // Per-thread chunk coordinates of the fill (the same for every plane).
-  // Threads without a chunk (ch_lds -1) write the 16-byte sink that follows
-  // the two plane buffers, at a fixed address: an offset from the buffer being
-  // filled would land 2 * LR * LC elements past the second one, inside the
-  // output staging tile (or past the allocation without one).
+  // Threads without a chunk (ch_lds -1) store nothing: their stores are
+  // masked off (a shared sink address would serialise every such lane of an
+  // instruction on one LDS bank).
   const __amdgpu_buffer_rsrc_t xr = slab_rsrc(xnc, static_cast<uint32_t>(in_slab * 2));
   const __amdgpu_buffer_rsrc_t yr = slab_rsrc(ync, static_cast<uint32_t>(out_slab * 2));
   const __amdgpu_buffer_rsrc_t ar =
@@ -271,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_stencil_kernel(const bf16_t*
       } else {
         v = pre[u];
       }
-      *reinterpret_cast<uint4*>(ch_lds[u] >= 0 ? buf + ch_lds[u] : lds + 2 * LR * LC) = v;
+      if (ch_lds[u] >= 0) *reinterpret_cast<uint4*>(buf + ch_lds[u]) = v;
     }
   };
 
@@ -537,7 +536,6 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
   extern __shared__ __align__(16) unsigned char smem_raw[];
   uint16_t* const lds = reinterpret_cast<uint16_t*>(smem_raw);
   uint16_t* const dlds = lds + 2 * T::XBUF;
-  uint16_t* const dummy = dlds + 2 * T::DBUF;  // 16-byte sink for threads without a chunk
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int n16 = lane & 15, q = lane >> 4;
@@ -652,14 +650,14 @@ __global__ __launch_bounds__(kThreads) void dw_mfma_wgrad_kernel(const bf16_t* _
       } else {
         v = p.xv[u];
       }
-      *reinterpret_cast<uint4*>(xl[u] >= 0 ? xb + xl[u] : dummy) = v;
+      if (xl[u] >= 0) *reinterpret_cast<uint4*>(xb + xl[u]) = v;  // masked off without a chunk
     }
 #pragma unroll
     for (int u = 0; u < T::NDC; ++u) {
       uint4 v = p.dv[u];
       // UPDY: 4 small values -> 8 big columns, zeros at the odd ones.
       if constexpr (UPDY) v = make_uint4(v.x & 0xffffu, v.x >> 16, v.y & 0xffffu, v.y >> 16);
-      *reinterpret_cast<uint4*>(dl[u] >= 0 ? db + dl[u] : dummy) = v;
+      if (dl[u] >= 0) *reinterpret_cast<uint4*>(db + dl[u]) = v;
     }
   };
 
@@ -795,7 +793,7 @@ template <int K, bool FLIP, int CT, int PD>
 int launch_stencil(const void* x, const void* wt, const void* bias, void* y, const MGeom& g,
                    int64_t blocks, hipStream_t st, const void* acc = nullptr) {
   constexpr int P = K / 2;
-  // two plane buffers + one dummy 16-byte slot for threads without a fill chunk
+  // two plane buffers, 8 spare elements, then (k = 3) the output staging tile
   constexpr size_t stage = stencil_stages_output(K) ? static_cast<size_t>(2) * (16 * kRT) * (16 * CT + 8) : 0;
   constexpr size_t lds = (static_cast<size_t>(2) * (16 * kRT + 2 * P) * stencil_pitch(K, CT) + 8 + stage) * 2;
   auto px = static_cast<const bf16_t*>(x);
