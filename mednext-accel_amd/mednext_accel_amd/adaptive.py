@@ -599,6 +599,17 @@ class AdaptiveExpansion:
     #: MI355X, fwd + bwd per block: 64 hidden @128^3 686 vs 721 us (recompute
     #: wins), 192 @64^3 385 vs 351, 512 @32^3 229 vs 190, 2048 @8^3 219 vs 178.
     stored_gelu_from = 128
+    #: Project widths up to which GELU is recomputed whatever the hidden width:
+    #: a project GEMM this narrow is one row group, so it (and its weight
+    #: gradient) evaluates GELU once per element, while storing GELU' writes
+    #: another hidden-sized tensor (the up block into stage 0: 128 hidden,
+    #: 32 outputs, at 128^3).
+    recompute_gelu_up_to = 32
+
+    def stores_gelu(self) -> bool:
+        """Whether the expansion stores GELU and GELU' of the expand output."""
+        b = self.block
+        return b.expand.out_channels >= self.stored_gelu_from and b.project.out_channels > self.recompute_gelu_up_to
 
     def __init__(self, block: nn.Module, resolver: PolicyResolver, model_context: ModelOptimizationContext,
                  *, role: str | None = None) -> None:
@@ -649,7 +660,7 @@ class AdaptiveExpansion:
         b2 = cast_param(b.project.bias, dt) if b.project.bias is not None else None
         fuse_residual = residual is not None and residual.dtype == dt and residual.is_contiguous()
         res = residual if fuse_residual else None
-        if b.expand.out_channels >= self.stored_gelu_from:
+        if self.stores_gelu():
             out = _hip_ops().mlp_expansion_stored(h.to(dt), w1, b1, w2, b2, res)[0]
         else:
             out = _hip_ops().mlp_expansion(h.to(dt), w1, b1, w2, b2, res)[0]
@@ -686,7 +697,7 @@ class AdaptiveExpansion:
         # Autocast runs group_norm in float32: float32 affine parameters.
         gamma, beta = norm.weight.float(), norm.bias.float()
         fuse_residual = residual is not None and residual.dtype == dt and residual.is_contiguous()
-        stored = b.expand.out_channels >= self.stored_gelu_from
+        stored = self.stores_gelu()
         out = _hip_ops().gn_mlp_expansion(
             d.to(dt), gamma, beta, w1, b1, w2, b2, residual if fuse_residual else None, float(norm.eps), stored
         )[0]
