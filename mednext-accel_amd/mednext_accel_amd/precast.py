@@ -11,9 +11,11 @@ bf16 rounding of the same fp32 weights, the same fp32 widening of the same
 bf16 gradients.
 
 The adaptive operators fetch their bf16 weights through ``cast_param``, which
-returns the pre-cast copy while the model's forward runs and falls back to
-``tensor.to(dtype)`` otherwise (evaluation, no autocast, checkpoint
-recomputation during the backward).
+returns the pre-cast copy from the forward until that forward's backward has
+gone through the copies (so checkpointed branches recomputed during the
+backward reuse them instead of casting every weight again), and falls back to
+``tensor.to(dtype)`` otherwise (evaluation, no autocast, a parameter changed in
+place since the cast).
 """
 
 from __future__ import annotations
@@ -21,15 +23,34 @@ from __future__ import annotations
 import torch
 from torch import Tensor, nn
 
-_ACTIVE: dict[int, Tensor] | None = None
+# id(parameter) -> (bf16 copy, the parameter's version counter when cast), and
+# the forward that made them (its _CastMany backward drops them).
+_ACTIVE: dict[int, tuple[Tensor, int]] | None = None
+_OWNER: object | None = None
+
+
+def _copy_of(p: Tensor, dtype: torch.dtype) -> Tensor | None:
+    if _ACTIVE is None:
+        return None
+    entry = _ACTIVE.get(id(p))
+    if entry is None or entry[0].dtype != dtype or entry[1] != p._version:
+        return None
+    return entry[0]
+
+
+def _drop(owner: object | None = None) -> None:
+    """Forget the copies (only those of ``owner``'s forward, when given)."""
+    global _ACTIVE, _OWNER
+    if owner is None or owner is _OWNER:
+        _ACTIVE, _OWNER = None, None
 
 
 def cast_param(p: Tensor, dtype: torch.dtype) -> Tensor:
-    """``p.to(dtype)``, served from the current forward's pre-cast copies when
-    ``p`` is one of them."""
-    if _ACTIVE is not None and p.dtype != dtype:
-        t = _ACTIVE.get(id(p))
-        if t is not None and t.dtype == dtype:
+    """``p.to(dtype)``, served from the pre-cast copies when ``p`` is one of
+    them and has not changed in place since."""
+    if p.dtype != dtype:
+        t = _copy_of(p, dtype)
+        if t is not None:
             return t
     return p.to(dtype)
 
@@ -71,7 +92,8 @@ def precast_or_param(p: Tensor | None) -> Tensor | None:
     nothing)."""
     if p is None or _ACTIVE is None:
         return p
-    return _ACTIVE.get(id(p), p)
+    entry = _ACTIVE.get(id(p))
+    return entry[0] if entry is not None and entry[1] == p._version else p
 
 
 class _CastMany(torch.autograd.Function):
@@ -80,7 +102,8 @@ class _CastMany(torch.autograd.Function):
     a 16-byte boundary."""
 
     @staticmethod
-    def forward(ctx, dtype: torch.dtype, *params: Tensor):
+    def forward(ctx, dtype: torch.dtype, owner: object, *params: Tensor):
+        ctx.owner = owner
         ctx.meta = [(p.shape, p.numel()) for p in params]
         ctx.src_dtype = params[0].dtype
         ctx.set_materialize_grads(False)
@@ -89,14 +112,17 @@ class _CastMany(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, *grads: Tensor | None):
+        # Every use of the copies, checkpoint recomputation included, has now
+        # produced its gradient: the optimizer step may follow.
+        _drop(ctx.owner)
         live = [g is not None for g in grads]
         if not any(live):
-            return (None,) * (len(grads) + 1)
+            return (None,) * (len(grads) + 2)
         ref = next(g for g in grads if g is not None)
         parts = [g if g is not None else ref.new_zeros(n) for g, (_, n) in zip(grads, ctx.meta)]
         flat = torch.cat(_packed(parts, [n for _, n in ctx.meta])).to(ctx.src_dtype)
         views = _unpacked(flat, ctx.meta)
-        return (None, *(v if ok else None for v, ok in zip(views, live)))
+        return (None, None, *(v if ok else None for v, ok in zip(views, live)))
 
 
 def precast_parameters(model: nn.Module) -> list[nn.Parameter]:
@@ -117,10 +143,9 @@ def precast_parameters(model: nn.Module) -> list[nn.Parameter]:
 
 
 def _precast_before(module: nn.Module, args) -> None:
-    global _ACTIVE
-    # Copies of an earlier forward that did not return (an exception skips the
-    # post hook's normal path) must never serve this one.
-    _ACTIVE = None
+    global _ACTIVE, _OWNER
+    # Copies of an earlier forward never serve this one.
+    _drop()
     params = module.__dict__.get("_mednext_precast_params")
     dtype = module.__dict__.get("_mednext_precast_dtype")
     if not params:
@@ -133,19 +158,24 @@ def _precast_before(module: nn.Module, args) -> None:
         and torch.get_autocast_dtype(device) == dtype
         and all(p.dtype != dtype for p in params)
     ):
-        copies = _CastMany.apply(dtype, *params)
-        _ACTIVE = {id(p): c for p, c in zip(params, copies)}
+        owner = object()
+        copies = _CastMany.apply(dtype, owner, *params)
+        _ACTIVE = {id(p): (c, p._version) for p, c in zip(params, copies)}
+        _OWNER = owner
 
 
 def _precast_after(module: nn.Module, args, output) -> None:
-    global _ACTIVE
-    _ACTIVE = None
+    # The copies stay for the backward's checkpoint recomputation; a forward
+    # that raised (the hook then sees no output) leaves none behind.
+    if output is None:
+        _drop()
 
 
 def install_weight_precast(model: nn.Module, dtype: torch.dtype = torch.bfloat16) -> int:
     """Pre-cast ``precast_parameters(model)`` to ``dtype`` at the start of every
     training forward run under autocast with that dtype (grad enabled), and
-    drop the copies when the forward returns. The parameter list lives in the
+    drop the copies when the backward has gone through them (or at the next
+    forward, or when the forward raises). The parameter list lives in the
     model's ``__dict__`` (a deep copy of the model gets its own) and the hooks
     are module-level functions. Returns how many parameters are covered."""
     params = precast_parameters(model)

@@ -8,6 +8,8 @@ import copy
 from dataclasses import replace
 
 import torch
+from torch import nn
+from torch.utils.checkpoint import checkpoint
 
 from mednext_accel_amd import MedNeXtV1
 from mednext_accel_amd.config import get_mednext_v1_config
@@ -18,7 +20,7 @@ from mednext_accel_amd.precast import _CastMany, cast_param, precast_parameters
 def test_cast_many_is_the_per_tensor_casts():
     gen = torch.Generator().manual_seed(3)
     params = [torch.randn(shape, generator=gen, requires_grad=True) for shape in ((3, 4), (5,), (2, 1, 3, 3, 3))]
-    outs = _CastMany.apply(torch.bfloat16, *params)
+    outs = _CastMany.apply(torch.bfloat16, object(), *params)
     for o, p in zip(outs, params, strict=True):
         assert o.dtype == torch.bfloat16 and o.shape == p.shape
         assert torch.equal(o, p.detach().to(torch.bfloat16))
@@ -55,7 +57,7 @@ def test_model_with_precast_trains_like_one_without():
 
 def test_copies_start_on_16_byte_boundaries():
     params = [torch.randn(n, requires_grad=True) for n in (3, 8, 13, 1, 27)]
-    outs = _CastMany.apply(torch.bfloat16, *params)
+    outs = _CastMany.apply(torch.bfloat16, object(), *params)
     base = outs[0].data_ptr()
     for o, p in zip(outs, params, strict=True):
         assert (o.data_ptr() - base) % 16 == 0
@@ -89,3 +91,63 @@ def test_failed_forward_leaves_no_stale_copies():
     x = torch.randn(1, 1, 32, 32, 32)
     with torch.no_grad():
         assert torch.equal(model(x), reference(x))
+
+
+class _Checkpointed(nn.Module):
+    """A checkpointed branch that fetches its weight through cast_param, as the
+    fused expansions do."""
+
+    def __init__(self) -> None:
+        super().__init__()
+        self.w = nn.Parameter(torch.randn(16, 16))
+
+    def forward(self, x):
+        return checkpoint(lambda t: torch.tanh(t @ cast_param(self.w, torch.bfloat16)), x, use_reentrant=False)
+
+
+def test_copies_serve_the_backward_recompute_then_drop():
+    """The pre-cast copies outlive the forward so that a checkpointed branch
+    recomputed in the backward reuses them (no second cast of its weights);
+    the backward through the copies drops them before any optimizer step, and
+    a copy whose parameter changed in place is never served. Gradients match a
+    plain per-use cast."""
+    from mednext_accel_amd import precast
+
+    torch.manual_seed(1)
+    model, plain = _Checkpointed(), _Checkpointed()
+    plain.load_state_dict(model.state_dict())
+    model.__dict__["_mednext_precast_params"] = [model.w]
+    model.__dict__["_mednext_precast_dtype"] = torch.bfloat16
+    model.register_forward_pre_hook(precast._precast_before)
+    model.register_forward_hook(precast._precast_after, always_call=True)
+    x = torch.randn(4, 16)
+    served = []
+    real = precast._copy_of
+
+    def spy(p, dtype):
+        t = real(p, dtype)
+        served.append(t is not None)
+        return t
+
+    precast._copy_of = spy
+    try:
+        with torch.autocast("cpu", dtype=torch.bfloat16):
+            out = model(x)
+        assert precast._ACTIVE is not None  # kept for the backward
+        out.float().sum().backward()
+    finally:
+        precast._copy_of = real
+    assert served == [True, True]  # the forward and the recompute both got the copy
+    assert precast._ACTIVE is None  # dropped by the backward through the copies
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        plain(x).float().sum().backward()
+    assert torch.equal(model.w.grad, plain.w.grad)
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        model(x)
+    copy_now = cast_param(model.w, torch.bfloat16)
+    assert copy_now is precast._ACTIVE[id(model.w)][0]
+    with torch.no_grad():
+        model.w.add_(1.0)
+    fresh = cast_param(model.w, torch.bfloat16)
+    assert fresh is not copy_now and torch.equal(fresh, model.w.detach().bfloat16())
+    precast._drop()
