@@ -304,7 +304,8 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_apply_kernel(
     const Tdy* __restrict__ dy, const Tx* __restrict__ x, const void* __restrict__ mean,
     const void* __restrict__ rstd, const void* __restrict__ gamma, int pdtype,
     Tx* __restrict__ dx, int64_t c, int64_t v, int splits, int64_t chunk, bool vec_ok,
-    const double* __restrict__ part, double* __restrict__ rows_out) {
+    const double* __restrict__ part, double* __restrict__ rows_out, void* __restrict__ dgamma,
+    void* __restrict__ dbeta) {
   using Acc = typename AccOf<Tx>::type;
   const Chunk ck = chunk_of_block(v, splits, chunk);
   double sa, sb;
@@ -312,6 +313,10 @@ __global__ __launch_bounds__(kThreads) void gn_bwd_apply_kernel(
   if (ck.split == 0 && threadIdx.x == 0) {
     rows_out[ck.row * 2] = sa;
     rows_out[ck.row * 2 + 1] = sb;
+    // One sample (dgamma / dbeta passed): the row sums are the parameter
+    // gradients, stored as gn_param_grad_kernel would store them (0 + sum).
+    if (dgamma) store_param(dgamma, pdtype, ck.row, 0.0 + sb);
+    if (dbeta) store_param(dbeta, pdtype, ck.row, 0.0 + sa);
   }
   if (dx == nullptr) return;
   const Tx* __restrict__ xr = x + ck.row * v;
@@ -435,12 +440,14 @@ int gn_bwd_typed(const void* dy, const void* x, const void* mean, const void* rs
                      dim3(kThreads), 0, st, static_cast<const Tdy*>(dy),
                      static_cast<const Tx*>(x), mean, rstd, v, splits, chunk, vec_ok, part);
   MEDNEXT_CHECK_LAUNCH();
+  // One sample: the apply kernel stores the parameter gradients itself.
+  const bool one = n == 1;
   hipLaunchKernelGGL((gn_bwd_apply_kernel<Tdy, Tx>), dim3(static_cast<unsigned>(blocks)),
                      dim3(kThreads), 0, st, static_cast<const Tdy*>(dy),
                      static_cast<const Tx*>(x), mean, rstd, gamma, pdtype, static_cast<Tx*>(dx),
-                     c, v, splits, chunk, vec_ok, part, rows);
+                     c, v, splits, chunk, vec_ok, part, rows, one ? dgamma : nullptr, one ? dbeta : nullptr);
   MEDNEXT_CHECK_LAUNCH();
-  if (dgamma || dbeta) {
+  if (!one && (dgamma || dbeta)) {
     hipLaunchKernelGGL(gn_param_grad_kernel, dim3(static_cast<unsigned>(cdiv(c, 256))),
                        dim3(256), 0, st, rows, n, c, dgamma, dbeta, pdtype);
     MEDNEXT_CHECK_LAUNCH();

@@ -125,3 +125,24 @@ def test_deterministic():
     ga = hip_ops.group_norm_backward(dy, x, a[1], a[2], None)
     gb = hip_ops.group_norm_backward(dy, x, a[1], a[2], None)
     assert all(torch.equal(p, q) for p, q in zip(ga, gb))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_one_sample_parameter_gradients_match_the_batched_sum(dtype):
+    """With one sample the apply kernel stores dgamma / dbeta itself (no
+    parameter-gradient launch); they are the bits the batched path gives when
+    a second sample contributes a zero gradient."""
+    print(f"[gn one-sample param grads] dtype={dtype}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(21)
+    x = torch.randn(2, 24, 9, 10, 11, generator=gen, device=DEV).to(dtype)
+    dy = torch.randn(2, 24, 9, 10, 11, generator=gen, device=DEV).to(dtype)
+    dy[1] = 0
+    gam = torch.randn(24, generator=gen, device=DEV)
+    bet = torch.randn(24, generator=gen, device=DEV)
+    for splits in (1, 3):
+        _, mean1, rstd1 = hip_ops.group_norm_forward(x[:1].contiguous(), gam, bet, 1e-5, None, splits=splits)
+        _, dg1, db1 = hip_ops.group_norm_backward(dy[:1].contiguous(), x[:1].contiguous(), mean1, rstd1, gam,
+                                                  splits=splits)
+        _, mean2, rstd2 = hip_ops.group_norm_forward(x, gam, bet, 1e-5, None, splits=splits)
+        _, dg2, db2 = hip_ops.group_norm_backward(dy, x, mean2, rstd2, gam, splits=splits)
+        assert torch.equal(dg1, dg2) and torch.equal(db1, db2), splits
