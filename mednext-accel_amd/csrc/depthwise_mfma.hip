@@ -508,7 +508,7 @@ struct WgradTile {
   static constexpr int NXC = (XROWS * XCPR + kThreads - 1) / kThreads;
   static constexpr int NDC = (DROWS * DCPR + kThreads - 1) / kThreads;
   static constexpr int TILES_PER_ROUND = 3;        // accumulator tiles reduced per LDS round
-  static constexpr size_t LOOP_BYTES = (2 * static_cast<size_t>(XBUF) + 2 * DBUF + 16) * 2;
+  static constexpr size_t LOOP_BYTES = (2 * static_cast<size_t>(XBUF) + 2 * DBUF) * 2;  // double-buffered x and dy planes
   static constexpr size_t RED_BYTES = static_cast<size_t>(4) * TILES_PER_ROUND * 256 * 4;
   static constexpr size_t BYTES = LOOP_BYTES > RED_BYTES ? LOOP_BYTES : RED_BYTES;
 };
