@@ -130,6 +130,12 @@ MFMA_TARGET_WORKGROUPS = {
     ("weight_grad", 3): 5 * CU_COUNT // 2,
     ("weight_grad", 5): 2 * CU_COUNT,
 }
+# Kinds whose grid is kept within one round of the target instead of reaching
+# it. The k5 weight-grad kernel holds two workgroups per CU (210 registers),
+# and a second, partial round costs about as much as a full one: C64 64^3
+# D-run 22 (576 workgroups) 49.6 us against D-run 32 (384) 37.7 us; at C32
+# 128^3, 352 to 1536 workgroups all run 108-118 us.
+MFMA_ONE_ROUND = {("weight_grad", 5)}
 
 
 def mfma_wgrad_rows(kernel_size: int, tile_w: int) -> int:
@@ -238,7 +244,8 @@ def depthwise_recipe(
     bf16 shapes the matrix-core kernels take use them, with ``tile_w = min(128,
     W)`` columns per workgroup: forward / input-grad tiles are 32 rows high,
     weight-grad tiles ``mfma_wgrad_rows(k, tile_w)``. The D-run per workgroup is
-    the longest that still yields ``MFMA_TARGET_WORKGROUPS``.
+    the longest that still yields ``MFMA_TARGET_WORKGROUPS`` (for the kinds of
+    ``MFMA_ONE_ROUND``, the shortest that stays within it).
     Small planes (H * W <= 256: the 16^3 and 8^3 stages) run the volume
     kernels (one workgroup per 64-position band of a plane and D-run) with
     ``tile_w = VOLUME_BAND`` and the D-run of ``volume_depth_chunk``, in the
@@ -260,6 +267,9 @@ def depthwise_recipe(
             rows, kind = MFMA_TILE_ROWS, "stencil"
         slabs = batch * channels * _cdiv(h, rows) * _cdiv(w, tile_w)
         target = MFMA_TARGET_WORKGROUPS[(kind, kernel_size)]
+        if (kind, kernel_size) in MFMA_ONE_ROUND:
+            chunks = max(1, target // slabs)
+            return [ENGINE_MFMA, tile_w, max(_cdiv(d, chunks), depth_chunk_floor(d, kernel_size))]
         return [ENGINE_MFMA, tile_w, _depth_chunk(d, slabs, kernel_size, target)]
     if volume_supported(spatial) and phase in VOLUME_PHASES:
         acc_bytes = 8 if dtype == "float64" else 4
