@@ -991,13 +991,17 @@ namespace {
 // keep the reference's signature). Stencil: the widest tile the row allows and
 // D-runs for ~2 workgroups per CU, as for the stride-1 stencil. Weight
 // gradient: the stride-1 weight gradient's targets (2.5 workgroups per CU for
-// k = 3, 2 for k = 5).
+// k = 3; for k = 5 at most 2).
 constexpr int64_t kS2StencilTarget = 2 * 256;
 
 int s2_tile_cols(int64_t wb) { return wb >= 128 ? 128 : wb >= 64 ? 64 : 32; }
 
-int s2_depth_chunk(int64_t db, int64_t slabs, int64_t target) {
-  const int64_t chunks = std::max<int64_t>(1, cdiv(target, std::max<int64_t>(1, slabs)));
+// within: at most `target` workgroups (the k = 5 weight gradient, two resident
+// per CU, whose partial second round costs about as much as a full one)
+// instead of at least.
+int s2_depth_chunk(int64_t db, int64_t slabs, int64_t target, bool within = false) {
+  const int64_t sl = std::max<int64_t>(1, slabs);
+  const int64_t chunks = std::max<int64_t>(1, within ? target / sl : cdiv(target, sl));
   return static_cast<int>(std::max<int64_t>(2, cdiv(db, chunks)));
 }
 
@@ -1020,7 +1024,7 @@ int s2_wgrad_geom(int64_t n, int64_t c, int64_t db, int64_t hb, int64_t wb, int6
   const int64_t rows = int64_t(16 - (k - 1)) * (4 / (*tile_cols / 32));
   const int64_t slabs = n * c * cdiv(hb, rows) * cdiv(wb, int64_t(*tile_cols));
   const int64_t target = k == 3 ? 5 * 256 / 2 : 2 * 256;
-  const int dc = s2_depth_chunk(db, slabs, target);
+  const int dc = s2_depth_chunk(db, slabs, target, k == 5);
   if (int st = plan_wgrad(n, c, db, hb, wb, k, *tile_cols, dc, g, blocks, splits, true)) return st;
   g->Ds = static_cast<int>(ds);
   g->Hs = static_cast<int>(hs);
