@@ -438,15 +438,20 @@ int32_t mednext_grn_bwd(const void* grad_output, int32_t dy_dtype, const void* x
  * reference's up blocks (models/blocks.py:176-181, models/blocks_v2.py:128-133).
  * The backward writes grad_main (on the grid), grad_small (the even grid
  * points) and, when grad_bias != NULL, grad_bias = the sum of grad_out over
- * the other grid points (fixed-order fp64 reduction of per-plane fp32
- * partials in the caller's workspace). */
+ * the other grid points, or with bias_over_grid = 1 over the whole
+ * (D-1)(H-1)(W-1) grid (fixed-order fp64 reduction of per-plane fp32
+ * partials in the caller's workspace, rounded once). bias_over_grid is for a
+ * caller that computed small with the bias's value but routes the bias's
+ * gradient here: the sum is then its whole gradient, one rounding, as the
+ * reference's conv_transpose3d bias reduction. */
 int32_t mednext_up_join_fwd(const void* main_in, const void* small, const void* bias, void* out, int64_t n,
                             int64_t c, int64_t d, int64_t h, int64_t w, int32_t lead, int32_t dtype,
                             void* stream);
 size_t mednext_up_join_bwd_workspace_bytes(int64_t n, int64_t c, int64_t d);
 int32_t mednext_up_join_bwd(const void* grad_out, void* grad_main, void* grad_small, void* grad_bias,
                             void* workspace, size_t workspace_bytes, int64_t n, int64_t c, int64_t d,
-                            int64_t h, int64_t w, int32_t lead, int32_t dtype, void* stream);
+                            int64_t h, int64_t w, int32_t lead, int32_t bias_over_grid, int32_t dtype,
+                            void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,4 +13,4 @@ void set_error(const std::string& msg) { g_last_error = msg; }
 
 extern "C" const char* mednext_hip_last_error(void) { return mednext::g_last_error.c_str(); }
 
-extern "C" int32_t mednext_hip_abi_version(void) { return 13; }
+extern "C" int32_t mednext_hip_abi_version(void) { return 14; }

@@ -16,9 +16,12 @@
 // bf16 operands. The backward reads grad_out once and writes
 //   grad_main = grad_out on the grid, grad_y = grad_out at all-even grid
 //   points, grad_b = sum of grad_out over the other grid points
-// (the bias at all-even points reaches y through the GEMM's own bias). The
-// bias sums are per-(n, c, plane) fp32 partials reduced in a fixed order in
-// fp64 by a second kernel.
+// (the bias at all-even points reaches y through the GEMM's own bias), or,
+// with bias_over_grid, over the whole (2s - 1)^3 grid: the caller then gave
+// the GEMM the bias's value only, and this sum, rounded once, is the bias's
+// whole gradient, as the transposed conv's own bias reduction is. The bias
+// sums are per-(n, c, plane) fp32 partials reduced in a fixed order in fp64
+// by a second kernel.
 //
 // One workgroup per output plane (n, c, Z); each thread produces 8
 // consecutive X of one row (a 16-byte store), reading main and y with element
@@ -34,6 +37,7 @@ constexpr int kThreads = 256;
 struct JoinGeom {
   int C, D, H, W;  // output extents (even)
   int lead;        // 1: pad at the start (v1), 0: at the end (v2)
+  int bias_over_grid;  // backward: bias sum over every grid point
 };
 
 __device__ inline float ld(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
@@ -109,6 +113,7 @@ __global__ __launch_bounds__(kThreads) void up_join_bwd_kernel(const uint16_t* _
         mplane[static_cast<int64_t>(y) * Wm + x] = bits;
         if (even_row && x % 2 == 0) {
           splane[static_cast<int64_t>(y / 2) * Ws + x / 2] = bits;
+          if (g.bias_over_grid) bsum += bf16_to_f32(bits);
         } else {
           bsum += bf16_to_f32(bits);
         }
@@ -147,8 +152,9 @@ int check_join(int64_t n, int64_t c, int64_t d, int64_t h, int64_t w, int32_t le
   return MEDNEXT_STATUS_OK;
 }
 
-JoinGeom make_join(int64_t c, int64_t d, int64_t h, int64_t w, int32_t lead) {
-  return JoinGeom{static_cast<int>(c), static_cast<int>(d), static_cast<int>(h), static_cast<int>(w), lead};
+JoinGeom make_join(int64_t c, int64_t d, int64_t h, int64_t w, int32_t lead, int32_t bias_over_grid = 0) {
+  return JoinGeom{static_cast<int>(c), static_cast<int>(d), static_cast<int>(h), static_cast<int>(w), lead,
+                  bias_over_grid != 0 ? 1 : 0};
 }
 
 }  // namespace
@@ -177,13 +183,15 @@ extern "C" size_t mednext_up_join_bwd_workspace_bytes(int64_t n, int64_t c, int6
 
 extern "C" int32_t mednext_up_join_bwd(const void* grad_out, void* grad_main, void* grad_small, void* grad_bias,
                                        void* workspace, size_t workspace_bytes, int64_t n, int64_t c, int64_t d,
-                                       int64_t h, int64_t w, int32_t lead, int32_t dtype, void* stream) {
+                                       int64_t h, int64_t w, int32_t lead, int32_t bias_over_grid, int32_t dtype,
+                                       void* stream) {
   if (int st = check_join(n, c, d, h, w, lead, dtype)) return st;
+  MEDNEXT_CHECK_ARG(bias_over_grid == 0 || bias_over_grid == 1, "bias_over_grid must be 0 or 1");
   MEDNEXT_CHECK_ARG(grad_out != nullptr && grad_main != nullptr && grad_small != nullptr, "null tensor pointer");
   MEDNEXT_CHECK_ARG((reinterpret_cast<uintptr_t>(grad_out) & 15u) == 0, "grad_out must be 16-byte aligned");
   MEDNEXT_CHECK_ARG(workspace != nullptr && workspace_bytes >= mednext_up_join_bwd_workspace_bytes(n, c, d),
                     "workspace too small");
-  const JoinGeom g = make_join(c, d, h, w, lead);
+  const JoinGeom g = make_join(c, d, h, w, lead, bias_over_grid);
   const auto s = static_cast<hipStream_t>(stream);
   float* part = static_cast<float*>(workspace);
   hipLaunchKernelGGL(up_join_bwd_kernel, dim3(static_cast<unsigned>(n * c * d)), dim3(kThreads), 0, s,

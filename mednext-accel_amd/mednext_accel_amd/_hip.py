@@ -115,7 +115,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     "mednext_up_join_bwd_workspace_bytes": (c_size_t, (_i64, _i64, _i64)),
     "mednext_up_join_bwd": (
         _i32,
-        (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _p),
+        (_p, _p, _p, _p, _p, c_size_t, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i32, _p),
     ),
     "mednext_depthwise3d_s2_gather": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
     "mednext_depthwise3d_s2_scatter": (_i32, (_p, _p, _p, _p, *(_i64,) * 8, _i32, _i32, _p)),
@@ -126,7 +126,7 @@ SIGNATURES: dict[str, tuple[object, tuple[object, ...]]] = {
     ),
 }
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -329,10 +329,11 @@ class AdaptivePointwise3d(_AdaptiveModule):
 
     def join_parts(self, x: Tensor) -> tuple[Tensor, Tensor | None] | None:
         """For a stride-2 transposed 1x1x1 conv on the matrix-core route: the
-        GEMM output at the input's voxels (bias included) and the bf16 bias,
-        which an up block turns into its padded residual sum in one pass
-        (``hip_ops.up_block_join``); None when this module would not take the
-        HIP route for ``x``."""
+        GEMM output at the input's voxels (bias value included, not tracked)
+        and the bf16 bias, which an up block turns into its padded residual sum
+        in one pass (``hip_ops.up_block_join`` with ``bias_in_small``: the
+        bias's whole gradient comes from the join's one reduction); None when
+        this module would not take the HIP route for ``x``."""
         if not (self.transposed and self.stride == (2, 2, 2)):
             return None
         context = _context_from_tensor(x, self.model_context, training=self.training)
@@ -344,7 +345,8 @@ class AdaptivePointwise3d(_AdaptiveModule):
             return None
         dt = torch.bfloat16
         bias = cast_param(self.bias, dt) if self.bias is not None else None
-        return ops.pointwise_conv_transpose3d(x.to(dt), cast_param(self.weight, dt), bias), bias
+        value = bias.detach() if bias is not None else None
+        return ops.pointwise_conv_transpose3d(x.to(dt), cast_param(self.weight, dt), value), bias
 
     def forward(self, x: Tensor) -> Tensor:
         context = _context_from_tensor(x, self.model_context, training=self.training)

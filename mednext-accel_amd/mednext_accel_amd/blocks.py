@@ -211,7 +211,7 @@ def join_up_residual(residual: nn.Module, x: Tensor, main: Tensor, *, lead: int)
     from . import hip_ops
 
     small, bias = parts
-    return hip_ops.up_block_join(main, small, bias, lead)
+    return hip_ops.up_block_join(main, small, bias, lead, True)
 
 
 class OutputHead(nn.Module):

@@ -1333,8 +1333,13 @@ def up_join(main: Tensor, small: Tensor, bias: Tensor | None, lead: int) -> Tens
     return out
 
 
-def up_join_backward(grad_out: Tensor, lead: int, with_bias: bool) -> tuple[Tensor, Tensor, Tensor | None]:
-    """(grad_main, grad_small, grad_bias or None) of ``up_join``."""
+def up_join_backward(
+    grad_out: Tensor, lead: int, with_bias: bool, bias_over_grid: bool = False
+) -> tuple[Tensor, Tensor, Tensor | None]:
+    """(grad_main, grad_small, grad_bias or None) of ``up_join``; with
+    ``bias_over_grid`` grad_bias sums grad_out over the whole (2s - 1)^3 grid,
+    all-even points included (the bias's whole gradient when ``small`` was
+    computed with an untracked copy of it)."""
     _check_device(grad_out)
     if grad_out.dtype != torch.bfloat16 or not grad_out.is_contiguous() or grad_out.ndim != 5:
         raise ValueError("grad_out must be a contiguous bfloat16 NCDHW tensor")
@@ -1348,7 +1353,8 @@ def up_join_backward(grad_out: Tensor, lead: int, with_bias: bool) -> tuple[Tens
     _hip.check(
         lib.mednext_up_join_bwd(
             grad_out.data_ptr(), gmain.data_ptr(), gsmall.data_ptr(), _hip.ptr(gbias), ws.data_ptr(), nbytes,
-            n, c, d, h, w, int(lead), _hip.DTYPE_CODES[torch.bfloat16], _hip.stream_of(grad_out),
+            n, c, d, h, w, int(lead), int(bool(bias_over_grid)), _hip.DTYPE_CODES[torch.bfloat16],
+            _hip.stream_of(grad_out),
         ),
         "mednext_up_join_bwd",
     )
@@ -1356,41 +1362,47 @@ def up_join_backward(grad_out: Tensor, lead: int, with_bias: bool) -> tuple[Tens
 
 
 @torch.library.custom_op("mednext_accel_amd::up_block_join", mutates_args=())
-def up_block_join(main: Tensor, small: Tensor, bias: Tensor | None, lead: int) -> Tensor:
+def up_block_join(main: Tensor, small: Tensor, bias: Tensor | None, lead: int, bias_in_small: bool = False) -> Tensor:
     """Custom-op form of ``up_join`` (reference models/blocks.py:179-181,
-    models/blocks_v2.py:131-133)."""
+    models/blocks_v2.py:131-133). ``bias_in_small``: the caller computed
+    ``small`` with the bias's value but without tracking it, so the bias's
+    gradient is the sum over the whole grid (one rounding, as the reference's
+    conv_transpose3d bias reduction) instead of over the non-even points."""
     return up_join(main, small, bias, lead)
 
 
 @up_block_join.register_fake
-def _(main, small, bias, lead):
+def _(main, small, bias, lead, bias_in_small=False):
     return main.new_empty((main.shape[0], main.shape[1], *(s + 1 for s in main.shape[2:])))
 
 
 @torch.library.custom_op("mednext_accel_amd::up_block_join_backward", mutates_args=())
-def up_block_join_backward_op(grad_out: Tensor, lead: int, with_bias: bool) -> tuple[Tensor, Tensor, Tensor]:
-    gmain, gsmall, gbias = up_join_backward(grad_out.contiguous(), lead, with_bias)
+def up_block_join_backward_op(
+    grad_out: Tensor, lead: int, with_bias: bool, bias_over_grid: bool
+) -> tuple[Tensor, Tensor, Tensor]:
+    gmain, gsmall, gbias = up_join_backward(grad_out.contiguous(), lead, with_bias, bias_over_grid)
     return gmain, gsmall, gbias if gbias is not None else grad_out.new_empty((0,))
 
 
 @up_block_join_backward_op.register_fake
-def _(grad_out, lead, with_bias):
+def _(grad_out, lead, with_bias, bias_over_grid):
     n, c, d, h, w = grad_out.shape
     return (grad_out.new_empty((n, c, d - 1, h - 1, w - 1)), grad_out.new_empty((n, c, d // 2, h // 2, w // 2)),
             grad_out.new_empty((c,) if with_bias else (0,)))
 
 
 def _setup_join(ctx, inputs, output):
-    _main, _small, bias, lead = inputs
+    _main, _small, bias, lead, bias_in_small = inputs
     ctx.lead = lead
     ctx.has_bias = bias is not None
+    ctx.bias_in_small = bias_in_small
 
 
 def _join_backward(ctx, grad_out):
     need_main, need_small, need_bias = ctx.needs_input_grad[:3]
     with_bias = ctx.has_bias and need_bias
-    gmain, gsmall, gbias = up_block_join_backward_op(grad_out.contiguous(), ctx.lead, with_bias)
-    return (gmain if need_main else None, gsmall if need_small else None, gbias if with_bias else None, None)
+    gmain, gsmall, gbias = up_block_join_backward_op(grad_out.contiguous(), ctx.lead, with_bias, ctx.bias_in_small)
+    return (gmain if need_main else None, gsmall if need_small else None, gbias if with_bias else None, None, None)
 
 
 up_block_join.register_autograd(_join_backward, setup_context=_setup_join)

@@ -31,14 +31,17 @@ def residual_grid(small, bias, full):
 @pytest.mark.parametrize("lead", [0, 1])
 @pytest.mark.parametrize("n,c,s,with_bias", [(1, 32, (8, 8, 8), True), (2, 3, (4, 6, 8), False),
                                              (1, 5, (3, 2, 4), True)])
-def test_join_is_pad_and_add(lead, n, c, s, with_bias):
-    print(f"[up join] lead={lead} n={n} c={c} s={s} bias={with_bias}", flush=True)
+@pytest.mark.parametrize("bias_in_small", [False, True])
+def test_join_is_pad_and_add(lead, n, c, s, with_bias, bias_in_small):
+    if bias_in_small and not with_bias:
+        pytest.skip("the flag only changes the bias gradient")
+    print(f"[up join] lead={lead} n={n} c={c} s={s} bias={with_bias} bias_in_small={bias_in_small}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(sum(s) + c + lead)
     full = tuple(2 * v - 1 for v in s)
     main = torch.randn(n, c, *full, generator=g, device=DEV).bfloat16().requires_grad_()
     small = torch.randn(n, c, *s, generator=g, device=DEV).bfloat16().requires_grad_()
     bias = torch.randn(c, generator=g, device=DEV).bfloat16().requires_grad_() if with_bias else None
-    out = P.up_block_join(main, small, bias, lead)
+    out = P.up_block_join(main, small, bias, lead, bias_in_small)
     pad = (1, 0) * 3 if lead else (0, 1) * 3
     ref = F.pad(main, pad) + F.pad(residual_grid(small, bias, full), pad)
     assert out.shape == ref.shape and torch.equal(out, ref)
@@ -49,8 +52,47 @@ def test_join_is_pad_and_add(lead, n, c, s, with_bias):
     assert torch.equal(got[0], want[0]) and torch.equal(got[1], want[1])
     if with_bias:
         grid = dout[:, :, lead:lead + full[0], lead:lead + full[1], lead:lead + full[2]].double()
-        odd = grid.sum(dim=(0, 2, 3, 4)) - grid[:, :, ::2, ::2, ::2].sum(dim=(0, 2, 3, 4))
-        assert rel_l2(got[2].double(), odd) <= 1e-2
+        whole = grid.sum(dim=(0, 2, 3, 4))
+        odd = whole - grid[:, :, ::2, ::2, ::2].sum(dim=(0, 2, 3, 4))
+        assert rel_l2(got[2].double(), whole if bias_in_small else odd) <= 1e-2
+
+
+def bf16_ulps(a, b):
+    """Distance in bf16 steps between two bf16 tensors of the same sign pattern."""
+    ia = a.view(torch.int16).to(torch.int32)
+    ib = b.view(torch.int16).to(torch.int32)
+    return (ia - ib).abs()
+
+
+@pytest.mark.parametrize("lead", [0, 1])
+def test_residual_bias_gradient_is_one_rounding(lead):
+    """The up block's residual bias through the join (GEMM with the bias's
+    value, join with bias_in_small): its gradient is the whole-grid sum of
+    grad_out rounded once to bf16, within one bf16 step of the fp64 sum and
+    within bf16 tolerance of the fp32 conv_transpose3d + pad + add reference
+    (reference models/blocks.py:176-181)."""
+    print(f"[up join bias] lead={lead}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(7 + lead)
+    n, cin, cout, s = 1, 16, 8, (8, 8, 8)
+    full = tuple(2 * v - 1 for v in s)
+    x = torch.randn(n, cin, *s, generator=g, device=DEV)
+    w = torch.randn(cin, cout, 1, 1, 1, generator=g, device=DEV) * cin**-0.5
+    b = torch.randn(cout, generator=g, device=DEV).requires_grad_()
+    main = torch.randn(n, cout, *full, generator=g, device=DEV)
+    bb = b.bfloat16()
+    small = P.pointwise_conv_transpose3d(x.bfloat16(), w.bfloat16(), bb.detach())
+    out = P.up_block_join(main.bfloat16(), small, bb, lead, True)
+    dout = torch.randn(out.shape, generator=g, device=DEV).bfloat16()
+    (gb,) = torch.autograd.grad(out, (b,), dout)
+    grid = dout[:, :, lead:lead + full[0], lead:lead + full[1], lead:lead + full[2]].double()
+    exact = grid.sum(dim=(0, 2, 3, 4))
+    assert int(bf16_ulps(gb.bfloat16(), exact.float().bfloat16()).max()) <= 1
+    b32 = b.detach().clone().requires_grad_()
+    pad = (1, 0) * 3 if lead else (0, 1) * 3
+    res = F.conv_transpose3d(x, w, b32, stride=2)
+    ref = F.pad(main, pad) + F.pad(res, pad)
+    (gb32,) = torch.autograd.grad(ref, (b32,), dout.float())
+    assert rel_l2(gb.double(), gb32.double()) <= 8e-3
 
 
 class Observe(TorchDispatchMode):
