@@ -330,7 +330,7 @@ def pointwise_supported(in_channels: int, out_channels: int, voxels: int) -> boo
 @functools.lru_cache(maxsize=4096)
 def pointwise_blocks(batch: int, k: int, m: int, voxels: int) -> int:
     """Workgroups per (sample, row group) for pw_fwd_kernel; 0 lets the library
-    pick: two resident 4-wave workgroups per CU over the whole grid (the
+    pick: at most two resident 4-wave workgroups per CU over the whole grid (the
     kernel is register-bound to two waves per SIMD), at least one 128-voxel
     chunk per wave."""
     del batch, k, m, voxels
