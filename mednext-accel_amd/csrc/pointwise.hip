@@ -1516,6 +1516,7 @@ int pick_mt(int64_t k, int64_t m, int epi) {
   // Two aux rows per output row: two m-tiles fit the register budget only with
   // the single-slice loop unrolled (K <= 32).
   if (epi == MEDNEXT_PW_EPILOGUE_AFFINE_SCALE) return ks == 1 && m > 16 && fits(2) ? 2 : 1;
+  // MT = 4 is instantiated for a single K slice only (pick_fwd).
   if (!aux && ks == 1 && m > 32 && fits(4)) return 4;
   if (m > 16 && fits(2)) return 2;
   return 1;
@@ -1832,6 +1833,7 @@ extern "C" int32_t mednext_pointwise_fwd_ws(const void* x, const void* weight, c
   p.g.wt = weight_layout;
   ex.slots = p.slots;
   MEDNEXT_CHECK_ARG(p.blocks < (int64_t{1} << 31), "grid too large");
+  MEDNEXT_CHECK_ARG(p.mt != 4 || p.g.ks == 1, "internal: 64-row groups take one 32-channel K slice");
   const int mt = p.mt;
   const size_t lds = static_cast<size_t>(16 * mt) * p.g.ks * 32 * 2 + kRowVecs * 16 * mt * sizeof(float) +
                      (p.splitk ? static_cast<size_t>(mt) * 8 * 4 * 64 * sizeof(float) : 0) +
